@@ -1,0 +1,136 @@
+/* nsfps -- MI355X-native farthest point sampling (NS-FPS semantics).
+ *
+ * C ABI of the drop-in boundary.  Plain pointers and sizes only; every entry
+ * point returns an nsfps_status and, on failure, leaves a message readable with
+ * nsfps_last_error() (thread-local).  The library never falls back to a CPU
+ * path: without a usable HIP device, compute entry points fail with
+ * NSFPS_EDEVICE.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   nsfps_range_derive   SpaceRange derived fields + make_range()
+ *                        (src/yuezu_fps.h:56-83, src/yuezu_fps.cpp:7-161)
+ *   nsfps_bbox           compute_bbox()          (src/yuezu_fps.cpp:643-670)
+ *   nsfps_fps            yuezu_fps() behind fps_numpy()
+ *                        (src/yuezu_fps.h:211-212, src/yuezu_fps.cpp:676-730,
+ *                         yuezu_fps/yuezu_fps_pybind.cpp:67-86)
+ *   nsfps_fps_bbox       fps_with_bbox()  (yuezu_fps/yuezu_fps_pybind.cpp:88-101)
+ *   nsfps_fps_batched    no single counterpart: B independent yuezu_fps() calls
+ *                        (the batched set-abstraction use of fps_numpy)
+ *   nsfps_fps_device     yuezu_fps() on device-resident input (cf. the
+ *                        reference GPU driver's FpsGPU::sample,
+ *                        eval/src_gpu/yuezu_fps_gpu.h:90-126)
+ */
+#ifndef NSFPS_H
+#define NSFPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  NSFPS_OK = 0,
+  NSFPS_EINVAL = 1,      /* invalid argument (shape, range, non-finite input) */
+  NSFPS_EDEVICE = 2,     /* HIP runtime / device failure, or no device */
+  NSFPS_ENOMEM = 3,      /* device allocation failed */
+  NSFPS_EUNSUPPORTED = 4 /* valid input outside what this build handles */
+} nsfps_status;
+
+/* The nine primary SpaceRange fields (src/yuezu_fps.h:56-60).  Derived fields
+ * are always recomputed from these, so a range edited field by field can never
+ * carry stale derived values. */
+typedef struct {
+  float min_x, max_x;
+  float min_y, max_y;
+  float min_z, max_z;
+  uint32_t x_blocks, y_blocks, z_blocks;
+} nsfps_range;
+
+/* Derived SpaceRange values (src/yuezu_fps.cpp:7-40, 136-161). */
+typedef struct {
+  float inv_bs[3];     /* 1.0f / ((max - min) / (float)blocks) */
+  float block_size[3]; /* (max - min) / blocks */
+  uint32_t bits[3];    /* ceil(log2(blocks)), at least 1 */
+  uint32_t total_bits;
+  uint64_t total_blocks;
+} nsfps_range_info;
+
+/* Per-call measurements of the last compute call on this thread. */
+typedef struct {
+  double build_ms;   /* device time: cell keys, sorts, leaves (hipEvents) */
+  double sample_ms;  /* device time: the sampling loop (hipEvents) */
+  double device_ms;  /* build_ms + sample_ms */
+  double e2e_ms;     /* host wall time of the whole call incl. copies */
+  uint64_t n_points;
+  uint64_t n_clouds;
+  uint64_t n_leaves;
+  uint64_t wide_iters;  /* iterations run by the grid-wide kernel */
+  uint64_t samples;     /* samples produced (sum over clouds) */
+} nsfps_stats;
+
+/* Library constants mirrored from src/yuezu_fps.h:19-50. */
+#define NSFPS_DEFAULT_X_BLOCKS 16
+#define NSFPS_DEFAULT_Y_BLOCKS 16
+#define NSFPS_DEFAULT_Z_BLOCKS 16
+#define NSFPS_MORTON_BLOCK_SIZE 16
+#define NSFPS_CACHE_BLOCK_SIZE 16
+
+const char *nsfps_last_error(void);
+const char *nsfps_version(void);
+
+/* Number of visible HIP devices (0 when none); never fails. */
+int nsfps_device_count(void);
+
+/* Derived fields and Morton LUTs of a range.  luts receives the x, y and z
+ * LUTs back to back (2^bits[0] + 2^bits[1] + 2^bits[2] entries) when non-NULL
+ * and lut_cap is large enough.  Replaces make_range()/make_uniform_range()'s
+ * derivation (src/yuezu_fps.cpp:98-161). */
+nsfps_status nsfps_range_derive(const nsfps_range *range, nsfps_range_info *info,
+                                uint32_t *luts, uint64_t lut_cap);
+
+/* compute_bbox(): exact fp32 bounds -/+ 1e-6 and the given block counts
+ * (src/yuezu_fps.cpp:648-670).  n == 0 gives [0,1]^3 with 1x1x1 blocks. */
+nsfps_status nsfps_bbox(const float *xyz, uint64_t n, uint32_t x_blocks,
+                        uint32_t y_blocks, uint32_t z_blocks, nsfps_range *out);
+
+/* FPS of one cloud.  xyz: host pointer, n x 3 float32, C order.  range == NULL
+ * selects compute_bbox with the default 16^3 blocks.  out: host buffer of at
+ * least n_samples int32 entries; *out_len receives the sample count (smaller
+ * than n_samples when the maximum min-distance reaches 0).  Start index 0,
+ * n_samples >= n returns 0..n-1, n == 0 or n_samples == 0 returns nothing. */
+nsfps_status nsfps_fps(const float *xyz, uint64_t n, uint64_t n_samples,
+                       const nsfps_range *range, int32_t *out, uint64_t *out_len);
+
+/* fps_with_bbox(): compute_bbox with the given block counts, then FPS. */
+nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples,
+                            uint32_t x_blocks, uint32_t y_blocks,
+                            uint32_t z_blocks, int32_t *out, uint64_t *out_len);
+
+/* B independent clouds of n points each (xyz: B x n x 3, host).  ranges: B
+ * ranges, or NULL for a per-cloud compute_bbox with blocks3 (NULL -> 16^3).
+ * out: B x n_samples int32 (row b holds cloud b's samples); out_lens: B. */
+nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
+                               uint64_t n_samples, const nsfps_range *ranges,
+                               const uint32_t *blocks3, int32_t *out,
+                               uint64_t *out_lens);
+
+/* FPS of one cloud whose points already live in device memory (d_xyz, n x 3
+ * float32) writing device memory (d_out, n_samples int32).  stream is a
+ * hipStream_t (NULL = default stream); the call returns after the stream work
+ * completes.  range must be non-NULL. */
+nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples,
+                              const nsfps_range *range, int32_t *d_out,
+                              uint64_t *out_len, void *stream);
+
+/* Measurements of the last compute call made on this thread. */
+nsfps_status nsfps_get_stats(nsfps_stats *stats);
+
+/* Releases the cached device workspace of the calling process. */
+void nsfps_release_workspace(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

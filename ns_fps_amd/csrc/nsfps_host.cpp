@@ -1,0 +1,667 @@
+// Host library behind the C ABI (include/nsfps.h): range derivation,
+// validation, device workspace, build orchestration and the sampling launch.
+//
+// Reference interfaces mirrored (paths relative to the reference tree):
+//   range derivation   src/yuezu_fps.cpp:7-161
+//   compute_bbox       src/yuezu_fps.cpp:643-670
+//   yuezu_fps guards   src/yuezu_fps.cpp:676-688 (empty, n_samples >= N)
+#include "nsfps.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "nsfps_internal.h"
+#include "nsfps_launch.h"
+
+namespace nsfps {
+namespace {
+
+constexpr float kBoundaryEps = 1e-6f;  // BOUNDARY_EPS, src/yuezu_fps.h:43-45
+
+thread_local std::string g_err;
+thread_local nsfps_stats g_stats;
+
+nsfps_status fail(nsfps_status s, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return s;
+}
+
+#define HIP_TRY(expr)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail(e_ == hipErrorOutOfMemory ? NSFPS_ENOMEM : NSFPS_EDEVICE, "%s: %s (%s:%d)", \
+                  #expr, hipGetErrorString(e_), __FILE__, __LINE__);                     \
+  } while (0)
+
+// ---------------------------------------------------------------- range ----
+
+uint32_t calc_bits(uint32_t blocks) {  // _calc_bits, src/yuezu_fps.cpp:45-50
+  uint32_t bits = 0;
+  while (bits < 32 && (1u << bits) < blocks) ++bits;
+  return bits ? bits : 1;
+}
+
+struct HostRange {
+  nsfps_range prim;
+  nsfps_range_info info;
+  std::vector<uint32_t> lut[3];
+  RangeDev dev;
+};
+
+nsfps_status check_range(const nsfps_range &r) {
+  const float b[6] = {r.min_x, r.max_x, r.min_y, r.max_y, r.min_z, r.max_z};
+  for (float v : b)
+    if (!std::isfinite(v)) return fail(NSFPS_EINVAL, "range bounds must be finite");
+  if (!(r.max_x > r.min_x) || !(r.max_y > r.min_y) || !(r.max_z > r.min_z))
+    return fail(NSFPS_EINVAL, "range must satisfy max > min on every axis");
+  const uint32_t bl[3] = {r.x_blocks, r.y_blocks, r.z_blocks};
+  for (uint32_t v : bl) {
+    if (v == 0) return fail(NSFPS_EINVAL, "block counts must be >= 1");
+    if (v > 1024) return fail(NSFPS_EUNSUPPORTED, "block counts above 1024 per axis are not supported");
+  }
+  return NSFPS_OK;
+}
+
+// make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
+// _compute_bit_positions/_generate_morton_lut (:52-97).
+void derive(const nsfps_range &r, HostRange &h) {
+  h.prim = r;
+  const float mn[3] = {r.min_x, r.min_y, r.min_z};
+  const float mx[3] = {r.max_x, r.max_y, r.max_z};
+  const uint32_t bl[3] = {r.x_blocks, r.y_blocks, r.z_blocks};
+  uint32_t tb = 0;
+  for (int a = 0; a < 3; ++a) {
+    h.info.inv_bs[a] = 1.0f / ((mx[a] - mn[a]) / (float)bl[a]);
+    h.info.block_size[a] = (mx[a] - mn[a]) / (float)bl[a];
+    h.info.bits[a] = calc_bits(bl[a]);
+    tb += h.info.bits[a];
+  }
+  h.info.total_bits = tb;
+  h.info.total_blocks = (uint64_t)bl[0] * bl[1] * bl[2];
+  // bit positions: min(bits) rounds of x,y,z, then x,y,z where present
+  uint32_t common = std::min({h.info.bits[0], h.info.bits[1], h.info.bits[2]});
+  uint32_t maxb = std::max({h.info.bits[0], h.info.bits[1], h.info.bits[2]});
+  std::vector<uint32_t> pos[3];
+  uint32_t bit = 0;
+  for (uint32_t i = 0; i < common; ++i)
+    for (int a = 0; a < 3; ++a) pos[a].push_back(bit++);
+  for (uint32_t i = common; i < maxb; ++i)
+    for (int a = 0; a < 3; ++a)
+      if (i < h.info.bits[a]) pos[a].push_back(bit++);
+  for (int a = 0; a < 3; ++a) {
+    uint32_t count = 1u << h.info.bits[a];
+    h.lut[a].assign(count, 0);
+    for (uint32_t v = 0; v < count; ++v) {
+      uint32_t code = 0;
+      for (uint32_t k = 0; k < h.info.bits[a]; ++k)
+        if (v & (1u << k)) code |= 1u << pos[a][k];
+      h.lut[a][v] = code;
+    }
+  }
+  RangeDev &d = h.dev;
+  bool bij = true;
+  uint32_t off = 0;
+  for (int a = 0; a < 3; ++a) {
+    d.mn[a] = mn[a];
+    d.hiclamp[a] = mx[a] - kBoundaryEps;
+    d.inv_bs[a] = h.info.inv_bs[a];
+    d.bsize[a] = h.info.block_size[a];
+    d.blocks[a] = bl[a];
+    d.lut_off[a] = off;
+    off += 1u << h.info.bits[a];
+    if (bl[a] != (1u << h.info.bits[a])) bij = false;  // not a power of two, or 1
+  }
+  d.T = (uint32_t)h.info.total_blocks;
+  d.bijective = bij ? 1u : 0u;
+}
+
+void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) {
+  // compute_bbox, src/yuezu_fps.cpp:648-670 (std::min/std::max comparisons)
+  if (n == 0) {
+    r.min_x = 0; r.max_x = 1; r.min_y = 0; r.max_y = 1; r.min_z = 0; r.max_z = 1;
+    r.x_blocks = r.y_blocks = r.z_blocks = 1;
+    return;
+  }
+  float mn[3] = {xyz[0], xyz[1], xyz[2]}, mx[3] = {xyz[0], xyz[1], xyz[2]};
+  for (uint64_t i = 0; i < n; ++i)
+    for (int a = 0; a < 3; ++a) {
+      float v = xyz[3 * i + a];
+      mn[a] = (v < mn[a]) ? v : mn[a];
+      mx[a] = (mx[a] < v) ? v : mx[a];
+    }
+  r.min_x = mn[0] - kBoundaryEps; r.max_x = mx[0] + kBoundaryEps;
+  r.min_y = mn[1] - kBoundaryEps; r.max_y = mx[1] + kBoundaryEps;
+  r.min_z = mn[2] - kBoundaryEps; r.max_z = mx[2] + kBoundaryEps;
+}
+
+// ------------------------------------------------------------ workspace ----
+
+struct Arena {
+  char *base = nullptr;
+  size_t cap = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  int device = -1;
+};
+
+std::mutex g_mu;
+Arena g_arena[16];
+
+// Bump layout over an arena; a null base measures the size.
+struct Bump {
+  char *base;
+  size_t off = 0;
+  explicit Bump(char *b) : base(b) {}
+  template <class T>
+  T *take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    T *p = base ? reinterpret_cast<T *>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+nsfps_status arena_for_device(Arena **out) {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return fail(NSFPS_EDEVICE, "no HIP device available (nsfps has no CPU path)");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 16) return fail(NSFPS_EDEVICE, "device ordinal %d out of range", dev);
+  Arena &a = g_arena[dev];
+  if (!a.stream) {
+    HIP_TRY(hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking));
+    for (auto &e : a.ev) HIP_TRY(hipEventCreate(&e));
+    a.device = dev;
+  }
+  *out = &a;
+  return NSFPS_OK;
+}
+
+nsfps_status arena_reserve(Arena &a, size_t bytes) {
+  if (bytes <= a.cap) return NSFPS_OK;
+  if (a.base) {
+    HIP_TRY(hipStreamSynchronize(a.stream));
+    HIP_TRY(hipFree(a.base));
+    a.base = nullptr;
+    a.cap = 0;
+  }
+  size_t want = bytes + bytes / 8 + (1u << 20);
+  hipError_t e = hipMalloc(&a.base, want);
+  if (e != hipSuccess) {
+    a.base = nullptr;
+    return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", want, hipGetErrorString(e));
+  }
+  a.cap = want;
+  return NSFPS_OK;
+}
+
+// ------------------------------------------------------------ one cloud ----
+
+struct CloudPlan {
+  uint32_t n = 0, m = 0;
+  HostRange rng;
+  const float *d_xyz_in = nullptr;  // device input (external) or staged copy
+  const float *h_xyz = nullptr;     // host input to stage, or null
+  CloudDev dev{};
+  uint32_t *d_lut = nullptr;
+  uint32_t *d_bad = nullptr;
+  uint32_t *d_nleaves = nullptr;    // cell_leaf[T]
+  uint32_t *d_counts = nullptr, *d_lc = nullptr;
+  uint32_t *d_phys0 = nullptr;
+  float *d_xyz_stage = nullptr;
+  uint32_t leaf_ub = 0;
+};
+
+struct Scratch {
+  uint32_t *bucket, *fine, *kA, *kB, *vA, *vB, *vC, *hist;
+};
+
+int key_bits_for(uint32_t T) {
+  int b = 0;
+  while (b < 32 && (1ull << b) < (uint64_t)T) ++b;
+  return b;
+}
+
+// Lays out the persistent buffers of one cloud.
+void layout_cloud(Bump &bp, CloudPlan &p) {
+  const uint32_t n = p.n, T = p.rng.dev.T;
+  p.leaf_ub = n / kLeaf + 1 + std::min<uint32_t>(T, n);
+  uint32_t l1_ub = (p.leaf_ub + kFan - 1) / kFan;
+  CloudDev &c = p.dev;
+  if (p.h_xyz) p.d_xyz_stage = bp.take<float>((size_t)n * 3);
+  p.d_lut = bp.take<uint32_t>(3 * 1024 + 16);
+  c.X = bp.take<float>(n);
+  c.Y = bp.take<float>(n);
+  c.Z = bp.take<float>(n);
+  c.C = bp.take<float>(n);
+  c.RANK = bp.take<uint32_t>(n);
+  c.ORIG = bp.take<uint32_t>(n);
+  p.d_counts = bp.take<uint32_t>((size_t)T + 1);
+  p.d_lc = bp.take<uint32_t>((size_t)T + 1);
+  c.cell_leaf = p.d_lc;
+  c.leaf_lo = bp.take<float4>(p.leaf_ub);
+  c.leaf_hi = bp.take<float4>(p.leaf_ub);
+  c.leaf_cell = bp.take<uint32_t>(p.leaf_ub);
+  c.leaf_key = bp.take<uint64_t>(p.leaf_ub);
+  c.leaf_win = bp.take<uint32_t>(p.leaf_ub);
+  c.l1_key = bp.take<uint64_t>(l1_ub);
+  c.l1_win = bp.take<uint32_t>(l1_ub);
+  c.root_key = bp.take<uint64_t>(1);
+  c.root_win = bp.take<uint32_t>(1);
+  c.iter = bp.take<uint32_t>(1);
+  c.done = bp.take<uint32_t>(1);
+  c.counter = bp.take<uint32_t>(1);
+  p.d_bad = bp.take<uint32_t>(1);
+  p.d_phys0 = bp.take<uint32_t>(1);
+  c.out = bp.take<int32_t>(p.m);
+  c.lut = p.d_lut;
+  c.n = n;
+  c.m = p.m;
+  c.r = p.rng.dev;
+}
+
+void layout_scratch(Bump &bp, uint32_t n, Scratch &s) {
+  s.bucket = bp.take<uint32_t>(n);
+  s.fine = bp.take<uint32_t>(n);
+  s.kA = bp.take<uint32_t>(n);
+  s.kB = bp.take<uint32_t>(n);
+  s.vA = bp.take<uint32_t>(n);
+  s.vB = bp.take<uint32_t>(n);
+  s.vC = bp.take<uint32_t>(n);
+  s.hist = bp.take<uint32_t>(radix_hist_len(n) + 16);
+}
+
+// Device build of one cloud up to (and including) the initial tree.  Leaves
+// the leaf count in p.dev.nleaves (one synchronising read-back).
+nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
+  CloudDev &c = p.dev;
+  const uint32_t n = p.n, T = p.rng.dev.T;
+  // LUTs
+  std::vector<uint32_t> lut;
+  for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
+  HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
+  const float *xyz = p.d_xyz_in;
+  if (p.h_xyz) {
+    HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)n * 12, hipMemcpyHostToDevice, st));
+    xyz = p.d_xyz_stage;
+  }
+  HIP_TRY(hipMemsetAsync(p.d_counts, 0, ((size_t)T + 1) * 4, st));
+  HIP_TRY(hipMemsetAsync(p.d_bad, 0, 4, st));
+  HIP_TRY(launch_cell_keys(xyz, n, p.rng.dev, p.d_lut, s.bucket, s.fine, p.d_counts, p.d_bad, st));
+  // sort 1: bucket order (stable) -> logical order
+  int bt = key_bits_for(T);
+  uint32_t *lorig = nullptr, *ko = nullptr;
+  if (bt == 0) {
+    // single bucket: logical order is the input order; sort by nothing
+    HIP_TRY(hipMemsetAsync(s.kA, 0, (size_t)n * 4, st));
+    // identity values via a one-pass sort on a zero key
+    HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, 8, s.hist, true, &ko, &lorig, st));
+  } else {
+    HIP_TRY(hipMemcpyAsync(s.kA, s.bucket, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, true, &ko, &lorig, st));
+  }
+  // sort 2: (bucket, sub-cell) inside the logical order; values = logical rank
+  int fb = std::min<int>((int)kFineBits, 32 - bt);
+  int fshift = (int)kFineBits - fb;
+  uint32_t *k2 = (ko == s.kA) ? s.kB : s.kA;
+  uint32_t *k2tmp = (k2 == s.kA) ? s.kB : s.kA;
+  uint32_t *v2 = (lorig == s.vA) ? s.vB : s.vA;
+  HIP_TRY(launch_key2(lorig, s.bucket, s.fine, n, fshift, fb, k2, st));
+  uint32_t *prank = nullptr, *kdummy = nullptr;
+  int k2bits = bt + fb;
+  if (k2bits == 0) k2bits = 8;
+  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, k2bits, s.hist, true, &kdummy, &prank, st));
+  uint32_t *RANK = const_cast<uint32_t *>(c.RANK), *ORIG = const_cast<uint32_t *>(c.ORIG);
+  HIP_TRY(launch_gather(prank, lorig, xyz, n, const_cast<float *>(c.X), const_cast<float *>(c.Y),
+                        const_cast<float *>(c.Z), c.C, RANK, ORIG, p.d_phys0, st));
+  // cell table and leaves
+  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, st));
+  HIP_TRY(launch_scan(p.d_counts, T, st));  // -> cell_start (T + 1)
+  HIP_TRY(launch_scan(p.d_lc, T, st));      // -> cell_leaf (T + 1)
+  uint32_t host_small[2] = {0, 0};
+  HIP_TRY(hipMemcpyAsync(&host_small[0], p.d_lc + T, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&host_small[1], p.d_bad, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (host_small[1]) return fail(NSFPS_EINVAL, "points must be finite");
+  c.nleaves = host_small[0];
+  if (c.nleaves > p.leaf_ub)
+    return fail(NSFPS_EDEVICE, "internal: leaf count %u exceeds bound %u", c.nleaves, p.leaf_ub);
+  c.nl1 = (c.nleaves + kFan - 1) / kFan;
+  if (c.nl1 > kMaxL1)
+    return fail(NSFPS_EUNSUPPORTED, "cloud needs %u level-1 nodes (max %u)", c.nl1, kMaxL1);
+  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.nleaves, p.rng.dev, c.X, c.Y, c.Z, c.RANK,
+                            const_cast<float4 *>(c.leaf_lo), const_cast<float4 *>(c.leaf_hi),
+                            const_cast<uint32_t *>(c.leaf_cell), c.leaf_key, c.leaf_win, st));
+  // phys0 -> CloudDev (read back; the kernels take it by value)
+  HIP_TRY(hipMemcpyAsync(&c.phys0, p.d_phys0, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  HIP_TRY(launch_init_state(c, st));
+  return NSFPS_OK;
+}
+
+uint32_t wide_iters_for(const CloudPlan &p) {
+  if (!p.rng.dev.bijective) return 0;
+  const char *env = getenv("NSFPS_WIDE_ITERS");
+  uint64_t e;
+  if (env) {
+    e = strtoull(env, nullptr, 10);
+  } else {
+    e = p.n / 1024;
+    e = std::max<uint64_t>(e, 16);
+    e = std::min<uint64_t>(e, 2048);
+  }
+  return (uint32_t)std::min<uint64_t>(e, p.m);
+}
+
+double ms_between(hipEvent_t a, hipEvent_t b) {
+  float ms = 0;
+  if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return -1.0;
+  return ms;
+}
+
+// Runs a list of clouds: builds each, then one sampling launch for all.
+nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, bool out_on_host,
+                        int32_t *h_out, uint64_t out_stride, uint64_t *out_lens) {
+  auto t0 = std::chrono::steady_clock::now();
+  Arena *ap = nullptr;
+  nsfps_status rc = arena_for_device(&ap);
+  if (rc) return rc;
+  Arena &a = *ap;
+  hipStream_t st = user_stream ? user_stream : a.stream;
+  // measure
+  uint32_t nmax = 0;
+  for (auto &p : plans) nmax = std::max(nmax, p.n);
+  Bump meas(nullptr);
+  for (auto &p : plans) layout_cloud(meas, p);
+  Scratch sc{};
+  layout_scratch(meas, nmax, sc);
+  CloudDev *d_clouds = meas.take<CloudDev>(plans.size());
+  (void)d_clouds;
+  rc = arena_reserve(a, meas.off + 4096);
+  if (rc) return rc;
+  Bump bp(a.base);
+  for (auto &p : plans) layout_cloud(bp, p);
+  layout_scratch(bp, nmax, sc);
+  d_clouds = bp.take<CloudDev>(plans.size());
+
+  HIP_TRY(hipEventRecord(a.ev[0], st));
+  uint64_t leaves = 0, points = 0, wide_total = 0;
+  uint32_t max_nl1 = 1;
+  for (auto &p : plans) {
+    rc = build_cloud(p, sc, st);
+    if (rc) return rc;
+    leaves += p.dev.nleaves;
+    points += p.n;
+    max_nl1 = std::max(max_nl1, p.dev.nl1);
+  }
+  HIP_TRY(hipEventRecord(a.ev[1], st));
+  // sampling
+  std::vector<CloudDev> devs;
+  for (auto &p : plans) devs.push_back(p.dev);
+  if (plans.size() == 1) {
+    uint32_t e = wide_iters_for(plans[0]);
+    wide_total = e;
+    if (e) {
+      uint32_t grid = std::max<uint32_t>(1, plans[0].dev.nl1);
+      HIP_TRY(launch_wide_steps(plans[0].dev, e, grid, st));
+    }
+  }
+  HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
+                         hipMemcpyHostToDevice, st));
+  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), max_nl1, st));
+  HIP_TRY(hipEventRecord(a.ev[2], st));
+  // results
+  std::vector<uint32_t> lens(plans.size());
+  for (size_t i = 0; i < plans.size(); ++i)
+    HIP_TRY(hipMemcpyAsync(&lens[i], plans[i].dev.iter, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  uint64_t samples = 0;
+  for (size_t i = 0; i < plans.size(); ++i) {
+    out_lens[i] = lens[i];
+    samples += lens[i];
+    if (out_on_host) {
+      HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
+                             hipMemcpyDeviceToHost, st));
+    }
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  auto t1 = std::chrono::steady_clock::now();
+  nsfps_stats &S = g_stats;
+  S.build_ms = ms_between(a.ev[0], a.ev[1]);
+  S.sample_ms = ms_between(a.ev[1], a.ev[2]);
+  S.device_ms = S.build_ms + S.sample_ms;
+  S.e2e_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  S.n_points = points;
+  S.n_clouds = plans.size();
+  S.n_leaves = leaves;
+  S.wide_iters = wide_total;
+  S.samples = samples;
+  return NSFPS_OK;
+}
+
+// Guards of yuezu_fps (src/yuezu_fps.cpp:678-688) that need no device.
+bool trivial(uint64_t n, uint64_t m, int32_t *out, uint64_t *len) {
+  if (n == 0 || m == 0) {
+    *len = 0;
+    return true;
+  }
+  if (m >= n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = (int32_t)i;
+    *len = n;
+    return true;
+  }
+  if (m == 1) {
+    out[0] = 0;
+    *len = 1;
+    return true;
+  }
+  return false;
+}
+
+void reset_stats() { memset(&g_stats, 0, sizeof(g_stats)); }
+
+}  // namespace
+}  // namespace nsfps
+
+using namespace nsfps;
+
+extern "C" {
+
+const char *nsfps_last_error(void) { return g_err.c_str(); }
+
+const char *nsfps_version(void) { return "nsfps 0.1.0 (gfx950)"; }
+
+int nsfps_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+nsfps_status nsfps_range_derive(const nsfps_range *range, nsfps_range_info *info, uint32_t *luts,
+                                uint64_t lut_cap) {
+  if (!range || !info) return fail(NSFPS_EINVAL, "range and info must be non-NULL");
+  const uint32_t bl[3] = {range->x_blocks, range->y_blocks, range->z_blocks};
+  for (uint32_t v : bl)
+    if (v == 0 || v > (1u << 20)) return fail(NSFPS_EINVAL, "block counts must be in [1, 2^20]");
+  HostRange h;
+  derive(*range, h);
+  *info = h.info;
+  if (luts) {
+    uint64_t need = h.lut[0].size() + h.lut[1].size() + h.lut[2].size();
+    if (need > lut_cap) return fail(NSFPS_EINVAL, "lut buffer too small (%llu needed)",
+                                    (unsigned long long)need);
+    uint64_t o = 0;
+    for (int a = 0; a < 3; ++a)
+      for (uint32_t v : h.lut[a]) luts[o++] = v;
+  }
+  return NSFPS_OK;
+}
+
+nsfps_status nsfps_bbox(const float *xyz, uint64_t n, uint32_t xb, uint32_t yb, uint32_t zb,
+                        nsfps_range *out) {
+  if (!out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  bbox_of(xyz, n, *out);
+  if (n) {
+    out->x_blocks = xb;
+    out->y_blocks = yb;
+    out->z_blocks = zb;
+  }
+  return NSFPS_OK;
+}
+
+static nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m,
+                                    const nsfps_range *range, int32_t *out, uint64_t *out_len) {
+  reset_stats();
+  if (!out_len || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+  nsfps_range r = *range;
+  nsfps_status rc = check_range(r);
+  if (rc) return rc;
+  if (trivial(n, m, out, out_len)) return NSFPS_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  std::vector<CloudPlan> plans(1);
+  CloudPlan &p = plans[0];
+  p.n = (uint32_t)n;
+  p.m = (uint32_t)m;
+  derive(r, p.rng);
+  p.h_xyz = xyz;
+  return run_clouds(plans, nullptr, true, out, 0, out_len);
+}
+
+nsfps_status nsfps_fps(const float *xyz, uint64_t n, uint64_t n_samples, const nsfps_range *range,
+                       int32_t *out, uint64_t *out_len) {
+  nsfps_range r;
+  if (range) {
+    r = *range;
+  } else {
+    if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
+    bbox_of(xyz, n, r);
+    if (n) r.x_blocks = r.y_blocks = r.z_blocks = NSFPS_DEFAULT_X_BLOCKS;
+  }
+  return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+}
+
+nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples, uint32_t xb,
+                            uint32_t yb, uint32_t zb, int32_t *out, uint64_t *out_len) {
+  if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
+  nsfps_range r;
+  bbox_of(xyz, n, r);
+  if (n) {
+    r.x_blocks = xb;
+    r.y_blocks = yb;
+    r.z_blocks = zb;
+  }
+  return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+}
+
+nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n, uint64_t m,
+                               const nsfps_range *ranges, const uint32_t *blocks3, int32_t *out,
+                               uint64_t *out_lens) {
+  reset_stats();
+  if (batch == 0) return NSFPS_OK;
+  if (!out_lens || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+  if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
+  std::vector<nsfps_range> rs(batch);
+  for (uint64_t b = 0; b < batch; ++b) {
+    if (ranges) {
+      rs[b] = ranges[b];
+    } else {
+      bbox_of(xyz + b * n * 3, n, rs[b]);
+      if (n) {
+        rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
+        rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
+        rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
+      }
+    }
+    nsfps_status rc = check_range(rs[b]);
+    if (rc) return rc;
+  }
+  bool all_trivial = true;
+  for (uint64_t b = 0; b < batch; ++b) {
+    uint64_t len = 0;
+    if (!trivial(n, m, out + b * m, &len)) {
+      all_trivial = false;
+      break;
+    }
+    out_lens[b] = len;
+  }
+  if (all_trivial) return NSFPS_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  std::vector<CloudPlan> plans(batch);
+  for (uint64_t b = 0; b < batch; ++b) {
+    plans[b].n = (uint32_t)n;
+    plans[b].m = (uint32_t)m;
+    derive(rs[b], plans[b].rng);
+    plans[b].h_xyz = xyz + b * n * 3;
+  }
+  return run_clouds(plans, nullptr, true, out, m, out_lens);
+}
+
+nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const nsfps_range *range,
+                              int32_t *d_out, uint64_t *out_len, void *stream) {
+  reset_stats();
+  if (!range || !out_len || (m && !d_out) || (n && !d_xyz))
+    return fail(NSFPS_EINVAL, "null pointer");
+  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+  nsfps_status rc = check_range(*range);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  hipStream_t st = (hipStream_t)stream;
+  if (n == 0 || m == 0 || m >= n || m == 1) {
+    std::vector<int32_t> tmp((size_t)std::min<uint64_t>(std::max<uint64_t>(n, 1), m ? m : 1));
+    trivial(n, m, tmp.data(), out_len);
+    if (*out_len) {
+      HIP_TRY(hipMemcpyAsync(d_out, tmp.data(), *out_len * 4, hipMemcpyHostToDevice, st));
+      HIP_TRY(hipStreamSynchronize(st));
+    }
+    return NSFPS_OK;
+  }
+  std::vector<CloudPlan> plans(1);
+  CloudPlan &p = plans[0];
+  p.n = (uint32_t)n;
+  p.m = (uint32_t)m;
+  derive(*range, p.rng);
+  p.d_xyz_in = d_xyz;
+  rc = run_clouds(plans, st, false, nullptr, 0, out_len);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
+nsfps_status nsfps_get_stats(nsfps_stats *stats) {
+  if (!stats) return fail(NSFPS_EINVAL, "null pointer");
+  *stats = g_stats;
+  return NSFPS_OK;
+}
+
+void nsfps_release_workspace(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (auto &a : g_arena) {
+    if (a.base) {
+      (void)hipFree(a.base);
+      a.base = nullptr;
+      a.cap = 0;
+    }
+  }
+}
+
+}  // extern "C"
