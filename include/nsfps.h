@@ -60,6 +60,8 @@ typedef struct {
 typedef struct {
   double build_ms;   /* device time: cell keys, sorts, leaves (hipEvents) */
   double sample_ms;  /* device time: the sampling loop (hipEvents) */
+  double wide_ms;    /* part of sample_ms spent in grid-wide iterations */
+  double late_ms;    /* the single-workgroup loop kernel alone */
   double device_ms;  /* build_ms + sample_ms */
   double e2e_ms;     /* host wall time of the whole call incl. copies */
   uint64_t n_points;
@@ -67,6 +69,8 @@ typedef struct {
   uint64_t n_leaves;
   uint64_t wide_iters;  /* iterations run by the grid-wide kernel */
   uint64_t samples;     /* samples produced (sum over clouds) */
+  uint32_t padded;      /* 1 when the single cloud used the padded cell layout */
+  uint32_t lds_bytes;   /* dynamic LDS of the single-workgroup loop */
 } nsfps_stats;
 
 /* Library constants mirrored from src/yuezu_fps.h:19-50. */
@@ -125,6 +129,17 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples
 
 /* Measurements of the last compute call made on this thread. */
 nsfps_status nsfps_get_stats(nsfps_stats *stats);
+
+/* Phase clocks and work counters of the single-workgroup sampling loop of the
+ * last call on this thread (cloud 0), recorded only when the environment
+ * variable NSFPS_PROFILE is set (all zero otherwise).  Words 0-8: s_memtime
+ * cycles spent between the loop's barriers (0 cube, 1 cell enumeration + scan,
+ * 2 flatten, 3 fast phase A: candidate + sibling loads, 4 fast phase B,
+ * 5 fast phase C / slow rounds, 6 slow level-1 rebuild, 7 level 2, 8 root);
+ * 16 iterations, 17 fast iterations, 18 cube cells, 19 candidate leaves,
+ * 20 dirty level-1 nodes on fast iterations, 21 elapsed s_memrealtime ticks
+ * (100 MHz).  No counterpart in the reference (it has no instrumentation). */
+nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords);
 
 /* Releases the cached device workspace of the calling process. */
 void nsfps_release_workspace(void);

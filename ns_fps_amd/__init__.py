@@ -1,0 +1,13 @@
+"""MI355X-native farthest point sampling with the NS-FPS (yuezu_fps) semantics.
+
+* ``ns_fps_amd.yuezu_fps_module`` -- drop-in Python module (SpaceRange,
+  make_range, make_uniform_range, fps, fps_with_bbox, constants, plus
+  fps_batched), built from csrc/ by ``python -m ns_fps_amd.build``.
+* ``ns_fps_amd.capi`` -- ctypes binding of the C ABI (include/nsfps.h).
+* ``ns_fps_amd.workloads`` -- seeded synthetic clouds of the benchmark.
+
+There is no CPU implementation: without the built HIP library and a device,
+compute calls raise.
+"""
+
+__version__ = "0.1.0"

@@ -1,0 +1,157 @@
+"""ctypes binding of the C ABI in include/nsfps.h (libnsfps.so).
+
+Mirrors the header one to one; the pybind11 module yuezu_fps_module is the
+drop-in Python surface, this binding exists for callers that need the raw
+entry points (device-resident input, statistics, loop profile).  A minimal
+HIP helper (hipMalloc / hipMemcpy / hipFree from libamdhip64) provides device
+buffers for nsfps_fps_device without any other framework.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnsfps.so")
+
+NSFPS_OK, NSFPS_EINVAL, NSFPS_EDEVICE, NSFPS_ENOMEM, NSFPS_EUNSUPPORTED = range(5)
+
+
+class Range(ctypes.Structure):
+    _fields_ = [("min_x", ctypes.c_float), ("max_x", ctypes.c_float),
+                ("min_y", ctypes.c_float), ("max_y", ctypes.c_float),
+                ("min_z", ctypes.c_float), ("max_z", ctypes.c_float),
+                ("x_blocks", ctypes.c_uint32), ("y_blocks", ctypes.c_uint32),
+                ("z_blocks", ctypes.c_uint32)]
+
+    @classmethod
+    def of(cls, rng):
+        return cls(*[float(v) for v in rng[:6]], *[int(v) for v in rng[6:9]])
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [("build_ms", ctypes.c_double), ("sample_ms", ctypes.c_double),
+                ("wide_ms", ctypes.c_double), ("late_ms", ctypes.c_double),
+                ("device_ms", ctypes.c_double),
+                ("e2e_ms", ctypes.c_double), ("n_points", ctypes.c_uint64),
+                ("n_clouds", ctypes.c_uint64), ("n_leaves", ctypes.c_uint64),
+                ("wide_iters", ctypes.c_uint64), ("samples", ctypes.c_uint64),
+                ("padded", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class NsfpsError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"nsfps status {status}: {msg}")
+        self.status = status
+
+
+_vp = ctypes.c_void_p
+_u64 = ctypes.c_uint64
+
+
+class Lib:
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (python -m ns_fps_amd.build)")
+        self.lib = ctypes.CDLL(path)
+        self.lib.nsfps_last_error.restype = ctypes.c_char_p
+        self.lib.nsfps_version.restype = ctypes.c_char_p
+
+    def _check(self, rc):
+        if rc != NSFPS_OK:
+            raise NsfpsError(rc, self.lib.nsfps_last_error().decode())
+
+    def device_count(self):
+        return self.lib.nsfps_device_count()
+
+    def fps(self, points, n_samples, rng=None):
+        p = np.ascontiguousarray(points, dtype=np.float32)
+        out = np.zeros(max(int(n_samples), 1), np.int32)
+        n = _u64()
+        r = ctypes.byref(Range.of(rng)) if rng is not None else None
+        self._check(self.lib.nsfps_fps(p.ctypes.data_as(_vp), _u64(len(p)), _u64(int(n_samples)),
+                                       r, out.ctypes.data_as(_vp), ctypes.byref(n)))
+        return out[:n.value].copy()
+
+    def fps_bbox(self, points, n_samples, blocks=(16, 16, 16)):
+        p = np.ascontiguousarray(points, dtype=np.float32)
+        out = np.zeros(max(int(n_samples), 1), np.int32)
+        n = _u64()
+        self._check(self.lib.nsfps_fps_bbox(p.ctypes.data_as(_vp), _u64(len(p)),
+                                            _u64(int(n_samples)), *[ctypes.c_uint32(b) for b in blocks],
+                                            out.ctypes.data_as(_vp), ctypes.byref(n)))
+        return out[:n.value].copy()
+
+    def fps_batched(self, clouds, n_samples, ranges=None, blocks=(16, 16, 16)):
+        P = np.ascontiguousarray(clouds, dtype=np.float32)
+        B, n = P.shape[0], P.shape[1]
+        out = np.zeros((B, max(int(n_samples), 1)), np.int32)
+        lens = np.zeros(B, np.uint64)
+        rs = None
+        if ranges is not None:
+            arr = (Range * B)(*[Range.of(r) for r in ranges])
+            rs = arr
+        b3 = (ctypes.c_uint32 * 3)(*blocks)
+        self._check(self.lib.nsfps_fps_batched(P.ctypes.data_as(_vp), _u64(B), _u64(n),
+                                               _u64(int(n_samples)), rs, b3,
+                                               out.ctypes.data_as(_vp), lens.ctypes.data_as(_vp)))
+        return [out[b, :int(lens[b])].copy() for b in range(B)]
+
+    def fps_device(self, d_xyz, n, n_samples, rng, d_out, stream=None):
+        n_out = _u64()
+        self._check(self.lib.nsfps_fps_device(_vp(d_xyz), _u64(n), _u64(int(n_samples)),
+                                              ctypes.byref(Range.of(rng)), _vp(d_out),
+                                              ctypes.byref(n_out), _vp(stream)))
+        return n_out.value
+
+    def stats(self):
+        s = Stats()
+        self._check(self.lib.nsfps_get_stats(ctypes.byref(s)))
+        return s.as_dict()
+
+    def loop_profile(self):
+        w = (ctypes.c_uint64 * 24)()
+        self._check(self.lib.nsfps_get_loop_profile(w, ctypes.c_uint32(24)))
+        return list(w)
+
+
+class Hip:
+    """Just enough of the HIP runtime for device buffers."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        self.rt = ctypes.CDLL("libamdhip64.so")
+
+    def _ck(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
+
+    def malloc(self, nbytes):
+        p = _vp()
+        self._ck(self.rt.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nbytes)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        self._ck(self.rt.hipFree(_vp(p)), "hipFree")
+
+    def upload(self, arr):
+        a = np.ascontiguousarray(arr)
+        d = self.malloc(a.nbytes)
+        self._ck(self.rt.hipMemcpy(_vp(d), a.ctypes.data_as(_vp), ctypes.c_size_t(a.nbytes), self.H2D),
+                 "hipMemcpy")
+        return d
+
+    def download(self, d, count, dtype):
+        out = np.zeros(count, dtype)
+        if count:
+            self._ck(self.rt.hipMemcpy(out.ctypes.data_as(_vp), _vp(d), ctypes.c_size_t(out.nbytes),
+                                       self.D2H), "hipMemcpy")
+        return out
+
+    def synchronize(self):
+        self._ck(self.rt.hipDeviceSynchronize(), "hipDeviceSynchronize")

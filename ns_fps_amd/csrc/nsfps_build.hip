@@ -1,0 +1,436 @@
+// Structure build on the device (gfx950): per-point bucket key with the
+// reference's cell rule, two stable LSD radix sorts, SoA gather into physical
+// slots, cell table, leaves with bounding boxes, level-1 tree nodes.
+//
+// Logical order (the reference's layout, src/yuezu_fps.cpp:277-283, 411-416,
+// 431-438) = stable sort of the input rows by bucket; the logical rank of a
+// point is its position in that order and breaks ties in the argmax.  The
+// physical order additionally sorts each bucket by a sub-cell Morton code so
+// that 64-point leaves are spatially tight; it never changes the result.
+#include <hip/hip_runtime.h>
+
+#include "nsfps_device.h"
+#include "nsfps_launch.h"
+
+namespace nsfps {
+
+// Bucket and sub-cell code per input row; bucket populations; non-finite flag.
+__global__ void k_cell_keys(const float *__restrict__ xyz, uint32_t n, RangeDev r,
+                            const uint32_t *__restrict__ lut, uint32_t *__restrict__ bucket,
+                            uint32_t *__restrict__ fine, uint32_t *__restrict__ counts,
+                            uint32_t *__restrict__ bad) {
+  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v[3] = {xyz[3 * (size_t)i], xyz[3 * (size_t)i + 1], xyz[3 * (size_t)i + 2]};
+  uint32_t c[3], f = 0;
+  bool finite = true;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    finite = finite && isfinite(v[a]);
+    c[a] = cell_axis(r, a, v[a]);
+    float cl = std_max(r.mn[a], std_min(v[a], r.hiclamp[a]));
+    float t = (cl - r.mn[a]) * r.inv_bs[a] - (float)c[a];
+    int s = (int)(t * 8.0f);
+    s = s < 0 ? 0 : (s > 7 ? 7 : s);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) f |= (uint32_t)((s >> k) & 1) << (3 * k + a);
+  }
+  if (!finite) atomicOr(bad, 1u);
+  uint32_t b = bucket_of(r, lut, c[0], c[1], c[2]);
+  bucket[i] = b;
+  fine[i] = f;
+  atomicAdd(&counts[b], 1u);
+}
+
+// --- stable LSD radix sort (8-bit digits), u32 keys and values -------------
+constexpr int kSortThreads = 256;
+constexpr int kSortRounds = 16;                        // per wave: 16 x 64 keys
+constexpr int kSortTile = kSortThreads * kSortRounds;  // 4096 keys per block
+
+__global__ __launch_bounds__(kSortThreads) void k_radix_hist(const uint32_t *__restrict__ keys,
+                                                            uint32_t n, int shift,
+                                                            uint32_t *__restrict__ hist,
+                                                            uint32_t nblocks) {
+  __shared__ uint32_t cnt[256];
+  cnt[threadIdx.x] = 0;
+  __syncthreads();
+  size_t base = (size_t)blockIdx.x * kSortTile;
+  for (int i = threadIdx.x; i < kSortTile; i += kSortThreads) {
+    size_t e = base + i;
+    if (e < n) atomicAdd(&cnt[(keys[e] >> shift) & 255u], 1u);
+  }
+  __syncthreads();
+  hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = cnt[threadIdx.x];
+}
+
+// Exclusive scan of len u32 in place by one 1024-thread workgroup; data[len]
+// receives the total.
+__global__ __launch_bounds__(1024) void k_scan_excl(uint32_t *__restrict__ data, uint32_t len) {
+  __shared__ uint32_t wsum[16];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t per = (len + 1023) / 1024;
+  uint32_t b = tid * per, e = b + per < len ? b + per : len;
+  uint32_t s = 0;
+  for (uint32_t i = b; i < e; ++i) s += data[i];
+  uint32_t v = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    uint32_t o = __shfl_up(v, off, 64);
+    if (lane >= (uint32_t)off) v += o;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t w = lane < 16 ? wsum[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      uint32_t o = __shfl_up(w, off, 64);
+      if (lane >= (uint32_t)off) w += o;
+    }
+    if (lane < 16) wsum[lane] = w;
+  }
+  __syncthreads();
+  uint32_t run = v - s + (wave ? wsum[wave - 1] : 0);
+  for (uint32_t i = b; i < e; ++i) {
+    uint32_t t = data[i];
+    data[i] = run;
+    run += t;
+  }
+  if (tid == 1023) data[len] = wsum[15];
+}
+
+// Stable scatter of one digit pass.  Each wave ranks its 1024 keys in order
+// (16 rounds of 64): lanes with the same digit are found with 8 ballots, the
+// running per-digit count of the wave lives in LDS; waves are then offset by
+// an exclusive prefix over waves.
+__global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
+    const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, uint32_t *__restrict__ kout,
+    uint32_t *__restrict__ vout, uint32_t n, int shift, const uint32_t *__restrict__ hist,
+    uint32_t nblocks) {
+  __shared__ uint32_t wcnt[kSortThreads / 64][256];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < (kSortThreads / 64) * 256; i += kSortThreads) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  const size_t base = (size_t)blockIdx.x * kSortTile + (size_t)wave * (64 * kSortRounds);
+  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+  uint32_t key[kSortRounds], val[kSortRounds], rnk[kSortRounds];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    size_t e = base + (size_t)r * 64 + lane;
+    bool valid = e < n;
+    key[r] = valid ? kin[e] : 0u;
+    val[r] = valid ? (vin ? vin[e] : (uint32_t)e) : 0u;
+  }
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    size_t e = base + (size_t)r * 64 + lane;
+    bool valid = e < n;
+    uint32_t d = (key[r] >> shift) & 255u;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      uint64_t m = __ballot((d >> b) & 1u);
+      peers &= ((d >> b) & 1u) ? m : ~m;
+    }
+    uint32_t before = (uint32_t)__popcll(peers & lt);
+    uint32_t baseq = valid ? wcnt[wave][d] : 0u;
+    rnk[r] = baseq + before;
+    // all lanes read their base before a leader writes (in-order LDS, one wave)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    if (valid && before == 0) wcnt[wave][d] = baseq + (uint32_t)__popcll(peers);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+  }
+  __syncthreads();
+  {
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / 64; ++w) {
+      uint32_t c = wcnt[w][tid];
+      wcnt[w][tid] = s;
+      s += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    size_t e = base + (size_t)r * 64 + lane;
+    if (e < n) {
+      uint32_t d = (key[r] >> shift) & 255u;
+      uint32_t pos = hist[(size_t)d * nblocks + blockIdx.x] + wcnt[wave][d] + rnk[r];
+      kout[pos] = key[r];
+      vout[pos] = val[r];
+    }
+  }
+}
+
+// Secondary key per logical position: bucket, then the sub-cell code.
+__global__ void k_key2(const uint32_t *__restrict__ lorig, const uint32_t *__restrict__ bucket,
+                       const uint32_t *__restrict__ fine, uint32_t n, int fine_shift,
+                       int fine_bits, uint32_t *__restrict__ key2) {
+  uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  uint32_t o = lorig[p];
+  uint32_t f = fine_bits > 0 ? (fine[o] >> fine_shift) : 0u;
+  key2[p] = (bucket[o] << fine_bits) | f;
+}
+
+// Leaves per bucket, and the largest bucket population.
+__global__ void k_leaf_counts(const uint32_t *__restrict__ counts, uint32_t T,
+                              uint32_t *__restrict__ lc, uint32_t *__restrict__ maxocc) {
+  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= T) return;
+  uint32_t c = counts[b];
+  lc[b] = (c + kLeaf - 1) / kLeaf;
+  if (c) atomicMax(maxocc, c);
+}
+
+__global__ void k_cell_info(const uint32_t *__restrict__ cell_start,
+                            const uint32_t *__restrict__ cell_leaf, uint32_t T,
+                            uint2 *__restrict__ info) {
+  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b > T) return;
+  info[b] = make_uint2(cell_start[b], cell_leaf[b]);
+}
+
+// Gather into physical slots; min-distance starts at FLT_MAX
+// (src/yuezu_fps.cpp:215-223).  Dense: slot = physical position p.  Padded:
+// slot = bucket * cap + (p - first position of the bucket).
+__global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__restrict__ lorig,
+                         const uint32_t *__restrict__ bucket, const uint32_t *__restrict__ cell_start,
+                         const float *__restrict__ xyz, uint32_t n, uint32_t padded, uint32_t cap,
+                         float4 *__restrict__ P4, uint2 *__restrict__ RO,
+                         uint32_t *__restrict__ phys0) {
+  uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  uint32_t rk = prank[p];
+  uint32_t o = lorig[rk];
+  uint32_t slot = p;
+  if (padded) {
+    uint32_t b = bucket[o];
+    slot = b * cap + (p - cell_start[b]);
+  }
+  P4[slot] = make_float4(xyz[3 * (size_t)o], xyz[3 * (size_t)o + 1], xyz[3 * (size_t)o + 2],
+                         FLT_MAX);
+  RO[slot] = make_uint2(rk, o);
+  if (o == 0) *phys0 = slot;
+}
+
+// Leaf descriptors (first slot, point count, cell) of every leaf of bucket b.
+__global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
+                            const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
+                            uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
+                            float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
+                            uint32_t *__restrict__ leaf_cell) {
+  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= T) return;
+  uint32_t s = cell_start[b], e = cell_start[b + 1];
+  uint32_t cntb = e - s;
+  uint32_t first = padded ? b * cap : s;
+  uint32_t l = padded ? b * lpc : cell_leaf[b];
+  uint32_t nl = padded ? lpc : (cntb + kLeaf - 1) / kLeaf;
+  uint32_t packed = 0;
+  if (cntb) {
+    float4 p = P4[first];
+    packed = cell_axis(r, 0, p.x) | (cell_axis(r, 1, p.y) << 10) | (cell_axis(r, 2, p.z) << 20);
+  }
+  for (uint32_t k = 0; k < nl; ++k, ++l) {
+    uint32_t off = k * kLeaf;
+    uint32_t cnt = cntb > off ? (cntb - off < kLeaf ? cntb - off : kLeaf) : 0u;
+    leaf_lo[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(first + off));
+    leaf_hi[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(cnt));
+    leaf_cell[l] = packed;
+  }
+}
+
+// Leaf bounding boxes and initial keys (FLT_MAX with the smallest rank of the
+// leaf); empty leaves get an empty box and key 0.  One wave per leaf.
+__global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float4 *__restrict__ P4,
+                                                   const uint2 *__restrict__ RO,
+                                                   float4 *__restrict__ leaf_lo,
+                                                   float4 *__restrict__ leaf_hi,
+                                                   uint64_t *__restrict__ leaf_key,
+                                                   float4 *__restrict__ leaf_pos) {
+  uint32_t leaf = blockIdx.x * 4 + (threadIdx.x >> 6);
+  uint32_t lane = lane_id();
+  if (leaf >= nleaves) return;
+  float4 lo = leaf_lo[leaf], hi = leaf_hi[leaf];
+  uint32_t start = __float_as_uint(lo.w), cnt = __float_as_uint(hi.w);
+  bool act = lane < cnt;
+  float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+  uint2 ro = make_uint2(0u, 0u);
+  if (act) {
+    p = P4[start + lane];
+    ro = RO[start + lane];
+  }
+  float mnx = act ? p.x : INFINITY, mny = act ? p.y : INFINITY, mnz = act ? p.z : INFINITY;
+  float mxx = act ? p.x : -INFINITY, mxy = act ? p.y : -INFINITY, mxz = act ? p.z : -INFINITY;
+  uint64_t k = act ? make_key(FLT_MAX, ro.x) : 0ull;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mnx = fminf(mnx, __shfl_xor(mnx, off, 64));
+    mny = fminf(mny, __shfl_xor(mny, off, 64));
+    mnz = fminf(mnz, __shfl_xor(mnz, off, 64));
+    mxx = fmaxf(mxx, __shfl_xor(mxx, off, 64));
+    mxy = fmaxf(mxy, __shfl_xor(mxy, off, 64));
+    mxz = fmaxf(mxz, __shfl_xor(mxz, off, 64));
+  }
+  uint64_t km = wave_max_u64(k);
+  uint32_t wl = argmax_lane(k, km, act);
+  if (lane == 0) {
+    leaf_lo[leaf] = make_float4(mnx, mny, mnz, lo.w);
+    leaf_hi[leaf] = make_float4(mxx, mxy, mxz, hi.w);
+    leaf_key[leaf] = km;
+  }
+  if (cnt == 0) {
+    if (lane == 0) leaf_pos[leaf] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else if (lane == wl) {
+    leaf_pos[leaf] = make_float4(p.x, p.y, p.z, __uint_as_float(ro.y));
+  }
+}
+
+// Level-1 nodes from the initial leaves: max key, its position, and the union
+// of the leaf boxes.  One wave per node.
+__global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
+                                                 const uint64_t *__restrict__ leaf_key,
+                                                 const float4 *__restrict__ leaf_pos,
+                                                 const float4 *__restrict__ leaf_lo,
+                                                 const float4 *__restrict__ leaf_hi,
+                                                 uint64_t *__restrict__ l1_key,
+                                                 float4 *__restrict__ l1_pos,
+                                                 float4 *__restrict__ l1_lo,
+                                                 float4 *__restrict__ l1_hi) {
+  uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+  uint32_t lane = lane_id();
+  if (g >= nl1) return;
+  uint32_t j = g * kFan + lane;
+  bool v = j < nleaves;
+  uint64_t k = v ? leaf_key[j] : 0ull;
+  float4 lo = v ? leaf_lo[j] : make_float4(INFINITY, INFINITY, INFINITY, 0.f);
+  float4 hi = v ? leaf_hi[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, 0.f);
+  float mnx = lo.x, mny = lo.y, mnz = lo.z, mxx = hi.x, mxy = hi.y, mxz = hi.z;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mnx = fminf(mnx, __shfl_xor(mnx, off, 64));
+    mny = fminf(mny, __shfl_xor(mny, off, 64));
+    mnz = fminf(mnz, __shfl_xor(mnz, off, 64));
+    mxx = fmaxf(mxx, __shfl_xor(mxx, off, 64));
+    mxy = fmaxf(mxy, __shfl_xor(mxy, off, 64));
+    mxz = fmaxf(mxz, __shfl_xor(mxz, off, 64));
+  }
+  uint64_t km = wave_max_u64(k);
+  uint32_t wl = argmax_lane(k, km, v);
+  if (lane == 0) {
+    l1_key[g] = km;
+    l1_pos[g] = leaf_pos[g * kFan + wl];
+    l1_lo[g] = make_float4(mnx, mny, mnz, 0.f);
+    l1_hi[g] = make_float4(mxx, mxy, mxz, 0.f);
+  }
+}
+
+__global__ void k_init_state(CloudDev c, const uint32_t *__restrict__ phys0) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    *c.iter = 0;
+    *c.done = 0;
+    *c.counter = 0;
+    *c.root_key = 0;
+    *c.root_pos = c.P4[*phys0];
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+
+static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
+                            uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
+                            hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  k_cell_keys<<<cdiv(n, 256), 256, 0, st>>>(xyz, n, r, lut, bucket, fine, counts, bad);
+  return hipGetLastError();
+}
+
+hipError_t launch_scan(uint32_t *data, uint32_t len, hipStream_t st) {
+  k_scan_excl<<<1, 1024, 0, st>>>(data, len);
+  return hipGetLastError();
+}
+
+uint32_t radix_hist_len(uint32_t n) { return 256u * cdiv(n, kSortTile) + 1; }
+
+hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
+                             uint32_t *vals_tmp, uint32_t n, int key_bits, uint32_t *hist,
+                             bool iota_values, uint32_t **keys_out, uint32_t **vals_out,
+                             hipStream_t st) {
+  if (key_bits <= 0) return hipErrorInvalidValue;
+  uint32_t nb = cdiv(n, kSortTile);
+  uint32_t *ka = keys, *va = vals, *kb = keys_tmp, *vb = vals_tmp;
+  bool first = true;
+  for (int shift = 0; shift < key_bits; shift += 8) {
+    k_radix_hist<<<nb, kSortThreads, 0, st>>>(ka, n, shift, hist, nb);
+    k_scan_excl<<<1, 1024, 0, st>>>(hist, 256u * nb);
+    k_radix_scatter<<<nb, kSortThreads, 0, st>>>(ka, (first && iota_values) ? nullptr : va, kb,
+                                                 vb, n, shift, hist, nb);
+    first = false;
+    uint32_t *t = ka;
+    ka = kb;
+    kb = t;
+    t = va;
+    va = vb;
+    vb = t;
+  }
+  *keys_out = ka;
+  *vals_out = va;
+  return hipGetLastError();
+}
+
+hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,
+                       uint32_t n, int fine_shift, int fine_bits, uint32_t *key2,
+                       hipStream_t st) {
+  k_key2<<<cdiv(n, 256), 256, 0, st>>>(lorig, bucket, fine, n, fine_shift, fine_bits, key2);
+  return hipGetLastError();
+}
+
+hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
+                              hipStream_t st) {
+  k_leaf_counts<<<cdiv(T, 256), 256, 0, st>>>(counts, T, lc, maxocc);
+  return hipGetLastError();
+}
+
+hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
+                            uint2 *info, hipStream_t st) {
+  k_cell_info<<<cdiv((uint64_t)T + 1, 256), 256, 0, st>>>(cell_start, cell_leaf, T, info);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, const uint32_t *bucket,
+                         const uint32_t *cell_start, const float *xyz, uint32_t n,
+                         uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO, uint32_t *phys0,
+                         hipStream_t st) {
+  k_gather<<<cdiv(n, 256), 256, 0, st>>>(prank, lorig, bucket, cell_start, xyz, n, padded, cap, P4,
+                                         RO, phys0);
+  return hipGetLastError();
+}
+
+hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
+                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
+                             const RangeDev &r, const float4 *P4, const uint2 *RO,
+                             float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
+                             uint64_t *leaf_key, float4 *leaf_pos, hipStream_t st) {
+  k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
+                                            leaf_lo, leaf_hi, leaf_cell);
+  if (nleaves)
+    k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
+                                                  leaf_pos);
+  return hipGetLastError();
+}
+
+hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st) {
+  if (c.nl1)
+    k_l1_init<<<cdiv(c.nl1, 4), 256, 0, st>>>(c.nleaves, c.nl1, c.leaf_key, c.leaf_pos, c.leaf_lo,
+                                              c.leaf_hi, c.l1_key, c.l1_pos,
+                                              const_cast<float4 *>(c.l1_lo),
+                                              const_cast<float4 *>(c.l1_hi));
+  k_init_state<<<1, 64, 0, st>>>(c, d_phys0);
+  return hipGetLastError();
+}
+
+}  // namespace nsfps

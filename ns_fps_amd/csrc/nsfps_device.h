@@ -1,0 +1,197 @@
+// Device helpers shared by the build and sampling kernels.  Every fp32
+// expression here is evaluated without contraction (the translation units are
+// compiled with -ffp-contract=off and this header repeats the pragma).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "nsfps_internal.h"
+
+#pragma clang fp contract(off)
+
+// Global address space.  Pointers read from a struct are generic, and generic
+// (flat) accesses also count against the LDS wait counter, so every LDS wait
+// would also wait for outstanding HBM loads; device code therefore accesses
+// global memory through gptr().
+// (The host compilation pass of these device functions keeps generic pointers.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define NSFPS_GLOBAL __attribute__((address_space(1)))
+#else
+#define NSFPS_GLOBAL
+#endif
+
+namespace nsfps {
+
+template <class T>
+__device__ __forceinline__ NSFPS_GLOBAL T *gptr(T *p) {
+  return (NSFPS_GLOBAL T *)p;
+}
+template <class T>
+__device__ __forceinline__ const NSFPS_GLOBAL T *gptr(const T *p) {
+  return (const NSFPS_GLOBAL T *)p;
+}
+
+// std::min(v, hi) / std::max(lo, v) with <algorithm>'s comparison order.
+__device__ __forceinline__ float std_min(float a, float b) { return (b < a) ? b : a; }
+__device__ __forceinline__ float std_max(float a, float b) { return (a < b) ? b : a; }
+
+// Point3D::compute_block_indices, one axis (src/yuezu_fps.cpp:170-193):
+// clamp into [min, max - 1e-6], scale by the stored reciprocal, truncate,
+// clamp to the last block.
+__device__ __forceinline__ uint32_t cell_axis(const RangeDev &r, int a, float v) {
+  float c = std_max(r.mn[a], std_min(v, r.hiclamp[a]));
+  uint32_t i = (uint32_t)((c - r.mn[a]) * r.inv_bs[a]);
+  return i < r.blocks[a] - 1 ? i : r.blocks[a] - 1;
+}
+
+// Bucket of a cell: LUT Morton code, % total_blocks (src/yuezu_fps.cpp:195-199,
+// 411-416, 592).  The modulo is the identity when every axis has 2^k >= 2
+// blocks.
+__device__ __forceinline__ uint32_t bucket_of(const RangeDev &r, const uint32_t *lut, uint32_t ix,
+                                              uint32_t iy, uint32_t iz) {
+  uint32_t code = lut[r.lut_off[0] + ix] | lut[r.lut_off[1] + iy] | lut[r.lut_off[2] + iz];
+  return r.bijective ? code : code % r.T;
+}
+
+// squared_distance (src/yuezu_fps.cpp:205-209): ((dx*dx + dy*dy) + dz*dz).
+__device__ __forceinline__ float sqdist(float px, float py, float pz, float qx, float qy,
+                                        float qz) {
+  float dx = px - qx, dy = py - qy, dz = pz - qz;
+  float s = dx * dx + dy * dy;
+  return s + dz * dz;
+}
+
+// Lower bound of sqdist over a box with the same operation order.  Rounding
+// is monotone, so it never exceeds sqdist(p, q) for a p inside the box; an
+// empty box (lo > hi) gives +inf.
+__device__ __forceinline__ float box_lb(float qx, float qy, float qz, float4 lo, float4 hi) {
+  if (lo.x > hi.x) return INFINITY;
+  float gx = qx < lo.x ? lo.x - qx : (qx > hi.x ? qx - hi.x : 0.0f);
+  float gy = qy < lo.y ? lo.y - qy : (qy > hi.y ? qy - hi.y : 0.0f);
+  float gz = qz < lo.z ? lo.z - qz : (qz > hi.z ? qz - hi.z : 0.0f);
+  float s = gx * gx + gy * gy;
+  return s + gz * gz;
+}
+
+// Cube half-width of get_morton_codes_in_range (src/yuezu_fps.cpp:564-570):
+// (int)ceil(sqrtf(D) / block_size), clamped to the grid size (larger values
+// cover the same cells).
+__device__ __forceinline__ int cube_half(float D, float bs, uint32_t blocks) {
+  float rad = sqrtf(D < 0.0f ? 0.0f : D);
+  float f = ceilf(rad / bs);
+  if (!(f < (float)blocks)) return (int)blocks;
+  return (int)f;
+}
+
+struct Cube {
+  int lo[3], hi[3];
+};
+
+__device__ __forceinline__ Cube make_cube(const RangeDev &r, float D, float qx, float qy,
+                                          float qz) {
+  Cube cb;
+  const float q[3] = {qx, qy, qz};
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    int h = cube_half(D, r.bsize[a], r.blocks[a]);
+    int qc = (int)cell_axis(r, a, q[a]);
+    int lo = qc - h, hi = qc + h;
+    cb.lo[a] = lo < 0 ? 0 : lo;
+    cb.hi[a] = hi > (int)r.blocks[a] - 1 ? (int)r.blocks[a] - 1 : hi;
+  }
+  return cb;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+// ---- wave64 reductions on the VALU (DPP row permutes + readlane), no LDS
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_or0(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+
+constexpr int kDppQuad1032 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppShr1 = 0x111, kDppShr2 = 0x112, kDppShr4 = 0x114, kDppShr8 = 0x118;
+
+template <int CTRL>
+__device__ __forceinline__ void max_step(uint32_t &hi, uint32_t &lo) {
+  uint32_t oh = dpp<CTRL>(hi), ol = dpp<CTRL>(lo);
+  bool take = oh > hi || (oh == hi && ol > lo);
+  hi = take ? oh : hi;
+  lo = take ? ol : lo;
+}
+
+__device__ __forceinline__ uint32_t rdlane(uint32_t v, uint32_t l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+
+// Maximum of a u64 over the 64 lanes (all lanes must be active); the result
+// is wave-uniform.  Rows of 16 lanes by DPP, then the four row maxima.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+  max_step<kDppQuad1032>(hi, lo);
+  max_step<kDppQuad2301>(hi, lo);
+  max_step<kDppHalfMirror>(hi, lo);
+  max_step<kDppMirror>(hi, lo);
+  uint64_t best = ((uint64_t)rdlane(hi, 0) << 32) | rdlane(lo, 0);
+#pragma unroll
+  for (uint32_t r = 16; r < 64; r += 16) {
+    uint64_t v = ((uint64_t)rdlane(hi, r) << 32) | rdlane(lo, r);
+    best = v > best ? v : best;
+  }
+  return best;
+}
+
+// Inclusive prefix sum over the 64 lanes (all lanes active).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_or0<kDppShr1>(v);
+  v += dpp_or0<kDppShr2>(v);
+  v += dpp_or0<kDppShr4>(v);
+  v += dpp_or0<kDppShr8>(v);
+  const uint32_t t0 = rdlane(v, 15), t1 = rdlane(v, 31), t2 = rdlane(v, 47);
+  const uint32_t row = lane_id() >> 4;
+  v += (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
+  return v;
+}
+
+// Lane holding the wave maximum (keys are unique among active lanes).
+__device__ __forceinline__ uint32_t argmax_lane(uint64_t k, uint64_t km, bool active) {
+  uint64_t who = __ballot(active && k == km);
+  return who ? (uint32_t)__ffsll((long long)who) - 1 : 0u;
+}
+
+// Wave-uniform values moved to scalar registers.
+__device__ __forceinline__ float uni(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ uint32_t uni(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+__device__ __forceinline__ uint64_t uni(uint64_t v) {
+  return ((uint64_t)uni((uint32_t)(v >> 32)) << 32) | uni((uint32_t)v);
+}
+__device__ __forceinline__ float4 uni(float4 v) {
+  return make_float4(uni(v.x), uni(v.y), uni(v.z), uni(v.w));
+}
+
+// Value of lane src (wave-uniform src) for every lane.
+__device__ __forceinline__ float4 shfl_f4(float4 v, uint32_t src) {
+  return make_float4(__uint_as_float(rdlane(__float_as_uint(v.x), src)),
+                     __uint_as_float(rdlane(__float_as_uint(v.y), src)),
+                     __uint_as_float(rdlane(__float_as_uint(v.z), src)),
+                     __uint_as_float(rdlane(__float_as_uint(v.w), src)));
+}
+
+}  // namespace nsfps

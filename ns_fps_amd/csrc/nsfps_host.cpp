@@ -30,6 +30,7 @@ constexpr float kBoundaryEps = 1e-6f;  // BOUNDARY_EPS, src/yuezu_fps.h:43-45
 
 thread_local std::string g_err;
 thread_local nsfps_stats g_stats;
+thread_local uint64_t g_prof[kProfWords];
 
 nsfps_status fail(nsfps_status s, const char *fmt, ...) {
   char buf[512];
@@ -127,6 +128,7 @@ void derive(const nsfps_range &r, HostRange &h) {
     off += 1u << h.info.bits[a];
     if (bl[a] != (1u << h.info.bits[a])) bij = false;  // not a power of two, or 1
   }
+  d.lut_total = off;
   d.T = (uint32_t)h.info.total_blocks;
   d.bijective = bij ? 1u : 0u;
 }
@@ -156,7 +158,7 @@ struct Arena {
   char *base = nullptr;
   size_t cap = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   int device = -1;
 };
 
@@ -217,16 +219,15 @@ nsfps_status arena_reserve(Arena &a, size_t bytes) {
 struct CloudPlan {
   uint32_t n = 0, m = 0;
   HostRange rng;
-  const float *d_xyz_in = nullptr;  // device input (external) or staged copy
-  const float *h_xyz = nullptr;     // host input to stage, or null
+  const float *d_xyz_in = nullptr;  // device input, or null to stage h_xyz
+  const float *h_xyz = nullptr;
   CloudDev dev{};
-  uint32_t *d_lut = nullptr;
-  uint32_t *d_bad = nullptr;
-  uint32_t *d_nleaves = nullptr;    // cell_leaf[T]
-  uint32_t *d_counts = nullptr, *d_lc = nullptr;
-  uint32_t *d_phys0 = nullptr;
+  uint32_t slots_ub = 0, leaves_ub = 0, l1_ub = 0;
+  // build-time buffers
   float *d_xyz_stage = nullptr;
-  uint32_t leaf_ub = 0;
+  uint32_t *d_lut = nullptr, *d_counts = nullptr, *d_lc = nullptr;
+  uint32_t *d_small = nullptr;  // [0] non-finite flag, [1] max occupancy, [2] phys0
+  uint2 *d_cell_info = nullptr;
 };
 
 struct Scratch {
@@ -239,38 +240,46 @@ int key_bits_for(uint32_t T) {
   return b;
 }
 
-// Lays out the persistent buffers of one cloud.
+// Padded layout (slot = bucket * cap + j) is used when the largest bucket
+// rounded up to whole leaves, times the bucket count, stays within this many
+// slots: cell -> leaf becomes arithmetic, no table lookup per iteration.
+uint64_t padded_slot_limit(uint32_t n) { return std::max<uint64_t>(4ull * n, 65536ull); }
+
+// Lays out the persistent buffers of one cloud (upper bounds: the padded /
+// dense decision is made on the device data during the build).
 void layout_cloud(Bump &bp, CloudPlan &p) {
   const uint32_t n = p.n, T = p.rng.dev.T;
-  p.leaf_ub = n / kLeaf + 1 + std::min<uint32_t>(T, n);
-  uint32_t l1_ub = (p.leaf_ub + kFan - 1) / kFan;
+  uint64_t slots = std::max<uint64_t>(n, padded_slot_limit(n));
+  uint64_t leaves = std::max<uint64_t>(n / kLeaf + 1 + std::min<uint32_t>(T, n), slots / kLeaf);
+  p.slots_ub = (uint32_t)slots;
+  p.leaves_ub = (uint32_t)leaves;
+  p.l1_ub = (uint32_t)((leaves + kFan - 1) / kFan);
   CloudDev &c = p.dev;
   if (p.h_xyz) p.d_xyz_stage = bp.take<float>((size_t)n * 3);
-  p.d_lut = bp.take<uint32_t>(3 * 1024 + 16);
-  c.X = bp.take<float>(n);
-  c.Y = bp.take<float>(n);
-  c.Z = bp.take<float>(n);
-  c.C = bp.take<float>(n);
-  c.RANK = bp.take<uint32_t>(n);
-  c.ORIG = bp.take<uint32_t>(n);
+  p.d_lut = bp.take<uint32_t>(p.rng.dev.lut_total + 16);
+  c.P4 = bp.take<float4>(slots);
+  c.RO = bp.take<uint2>(slots);
   p.d_counts = bp.take<uint32_t>((size_t)T + 1);
   p.d_lc = bp.take<uint32_t>((size_t)T + 1);
-  c.cell_leaf = p.d_lc;
-  c.leaf_lo = bp.take<float4>(p.leaf_ub);
-  c.leaf_hi = bp.take<float4>(p.leaf_ub);
-  c.leaf_cell = bp.take<uint32_t>(p.leaf_ub);
-  c.leaf_key = bp.take<uint64_t>(p.leaf_ub);
-  c.leaf_win = bp.take<uint32_t>(p.leaf_ub);
-  c.l1_key = bp.take<uint64_t>(l1_ub);
-  c.l1_win = bp.take<uint32_t>(l1_ub);
+  p.d_cell_info = bp.take<uint2>((size_t)T + 1);
+  c.cell_info = p.d_cell_info;
+  c.leaf_lo = bp.take<float4>(leaves);
+  c.leaf_hi = bp.take<float4>(leaves);
+  c.leaf_cell = bp.take<uint32_t>(leaves);
+  c.leaf_key = bp.take<uint64_t>(leaves);
+  c.leaf_pos = bp.take<float4>(leaves);
+  c.l1_key = bp.take<uint64_t>(p.l1_ub);
+  c.l1_pos = bp.take<float4>(p.l1_ub);
+  c.l1_lo = bp.take<float4>(p.l1_ub);
+  c.l1_hi = bp.take<float4>(p.l1_ub);
   c.root_key = bp.take<uint64_t>(1);
-  c.root_win = bp.take<uint32_t>(1);
+  c.root_pos = bp.take<float4>(1);
   c.iter = bp.take<uint32_t>(1);
   c.done = bp.take<uint32_t>(1);
   c.counter = bp.take<uint32_t>(1);
-  p.d_bad = bp.take<uint32_t>(1);
-  p.d_phys0 = bp.take<uint32_t>(1);
+  p.d_small = bp.take<uint32_t>(4);
   c.out = bp.take<int32_t>(p.m);
+  c.prof = bp.take<uint64_t>(kProfWords);
   c.lut = p.d_lut;
   c.n = n;
   c.m = p.m;
@@ -288,12 +297,54 @@ void layout_scratch(Bump &bp, uint32_t n, Scratch &s) {
   s.hist = bp.take<uint32_t>(radix_hist_len(n) + 16);
 }
 
-// Device build of one cloud up to (and including) the initial tree.  Leaves
-// the leaf count in p.dev.nleaves (one synchronising read-back).
+// LDS layout of the single-workgroup loop for one cloud: required regions,
+// then the cell table (table mode) and level-1 boxes when they fit, then as
+// many staging slots as the rest allows (at most 64).
+LdsPlan plan_lds(const CloudDev &c) {
+  LdsPlan pl{};
+  uint32_t off = 0;
+  auto take = [&](uint64_t bytes) {
+    off = (off + 15u) & ~15u;
+    uint32_t o = off;
+    off += (uint32_t)bytes;
+    return o;
+  };
+  const uint32_t nl1 = std::max<uint32_t>(c.nl1, 1);
+  pl.l1k = take((uint64_t)nl1 * 8);
+  pl.l1p = take((uint64_t)nl1 * 16);
+  pl.l2k = take(64 * 8);
+  pl.l2p = take(64 * 16);
+  pl.lut = take((uint64_t)c.r.lut_total * 4);
+  pl.cand = take((uint64_t)kCandCap * 12);
+  pl.slot = take((uint64_t)nl1 * 4);
+  pl.m1 = take(((nl1 + 31) / 32) * 4);
+  pl.dl1 = take((uint64_t)nl1 * 4);
+  pl.m2 = take(8);
+  pl.dl2 = take(64 * 4);
+  const uint32_t slot_bytes = kFan * (8 + 16);
+  pl.ctab = kNone;
+  if (!c.padded) {
+    uint64_t need = ((uint64_t)c.r.T + 1) * 8;
+    if (off + need + 16 + 8 * slot_bytes <= kLdsBudget) pl.ctab = take(need);
+  }
+  pl.l1lo = pl.l1hi = kNone;
+  if (off + 2ull * nl1 * 16 + 32 + 4 * slot_bytes <= kLdsBudget) {
+    pl.l1lo = take((uint64_t)nl1 * 16);
+    pl.l1hi = take((uint64_t)nl1 * 16);
+  }
+  uint32_t room = kLdsBudget > off + 64 ? kLdsBudget - off - 64 : 0;
+  pl.dcap = std::min<uint32_t>(64, room / slot_bytes);
+  pl.sk = take((uint64_t)pl.dcap * kFan * 8);
+  pl.sp = take((uint64_t)pl.dcap * kFan * 16);
+  pl.total = (off + 255u) & ~255u;
+  return pl;
+}
+
+// Device build of one cloud up to the initial tree.  Two synchronising
+// read-backs of a few words (sizes decided on device data).
 nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   CloudDev &c = p.dev;
   const uint32_t n = p.n, T = p.rng.dev.T;
-  // LUTs
   std::vector<uint32_t> lut;
   for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
   HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
@@ -303,56 +354,60 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
     xyz = p.d_xyz_stage;
   }
   HIP_TRY(hipMemsetAsync(p.d_counts, 0, ((size_t)T + 1) * 4, st));
-  HIP_TRY(hipMemsetAsync(p.d_bad, 0, 4, st));
-  HIP_TRY(launch_cell_keys(xyz, n, p.rng.dev, p.d_lut, s.bucket, s.fine, p.d_counts, p.d_bad, st));
+  HIP_TRY(hipMemsetAsync(p.d_small, 0, 16, st));
+  HIP_TRY(launch_cell_keys(xyz, n, p.rng.dev, p.d_lut, s.bucket, s.fine, p.d_counts, p.d_small,
+                           st));
+  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, st));
+  HIP_TRY(launch_scan(p.d_counts, T, st));  // -> first dense position per bucket
+  HIP_TRY(launch_scan(p.d_lc, T, st));      // -> first leaf per bucket (dense)
+  uint32_t hs[3] = {0, 0, 0};
+  HIP_TRY(hipMemcpyAsync(&hs[0], p.d_small, 8, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&hs[2], p.d_lc + T, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (hs[0]) return fail(NSFPS_EINVAL, "points must be finite");
+  const uint32_t maxocc = hs[1], dense_leaves = hs[2];
+  // layout decision
+  uint64_t cap = (uint64_t)((maxocc + kLeaf - 1) / kLeaf) * kLeaf;
+  uint64_t padded_slots = cap * T;
+  bool padded = getenv("NSFPS_NO_PADDED") == nullptr && cap > 0 &&
+                padded_slots <= padded_slot_limit(n) && padded_slots <= p.slots_ub;
+  c.padded = padded ? 1u : 0u;
+  c.lpc = padded ? (uint32_t)(cap / kLeaf) : 0u;
+  c.nslots = padded ? (uint32_t)padded_slots : n;
+  c.nleaves = padded ? T * c.lpc : dense_leaves;
+  if (c.nleaves > p.leaves_ub)
+    return fail(NSFPS_EDEVICE, "internal: leaf count %u exceeds bound %u", c.nleaves, p.leaves_ub);
+  c.nl1 = (c.nleaves + kFan - 1) / kFan;
+  if (c.nl1 > kMaxL1)
+    return fail(NSFPS_EUNSUPPORTED, "cloud needs %u level-1 nodes (max %u)", c.nl1, kMaxL1);
   // sort 1: bucket order (stable) -> logical order
-  int bt = key_bits_for(T);
+  const int bt = std::max(1, key_bits_for(T));
   uint32_t *lorig = nullptr, *ko = nullptr;
-  if (bt == 0) {
-    // single bucket: logical order is the input order; sort by nothing
-    HIP_TRY(hipMemsetAsync(s.kA, 0, (size_t)n * 4, st));
-    // identity values via a one-pass sort on a zero key
-    HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, 8, s.hist, true, &ko, &lorig, st));
-  } else {
-    HIP_TRY(hipMemcpyAsync(s.kA, s.bucket, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, true, &ko, &lorig, st));
-  }
+  HIP_TRY(hipMemcpyAsync(s.kA, s.bucket, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+  HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, true, &ko, &lorig, st));
   // sort 2: (bucket, sub-cell) inside the logical order; values = logical rank
-  int fb = std::min<int>((int)kFineBits, 32 - bt);
-  int fshift = (int)kFineBits - fb;
+  const int fb = std::min<int>((int)kFineBits, 32 - bt);
+  const int fshift = (int)kFineBits - fb;
   uint32_t *k2 = (ko == s.kA) ? s.kB : s.kA;
   uint32_t *k2tmp = (k2 == s.kA) ? s.kB : s.kA;
   uint32_t *v2 = (lorig == s.vA) ? s.vB : s.vA;
   HIP_TRY(launch_key2(lorig, s.bucket, s.fine, n, fshift, fb, k2, st));
   uint32_t *prank = nullptr, *kdummy = nullptr;
-  int k2bits = bt + fb;
-  if (k2bits == 0) k2bits = 8;
-  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, k2bits, s.hist, true, &kdummy, &prank, st));
-  uint32_t *RANK = const_cast<uint32_t *>(c.RANK), *ORIG = const_cast<uint32_t *>(c.ORIG);
-  HIP_TRY(launch_gather(prank, lorig, xyz, n, const_cast<float *>(c.X), const_cast<float *>(c.Y),
-                        const_cast<float *>(c.Z), c.C, RANK, ORIG, p.d_phys0, st));
-  // cell table and leaves
-  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, st));
-  HIP_TRY(launch_scan(p.d_counts, T, st));  // -> cell_start (T + 1)
-  HIP_TRY(launch_scan(p.d_lc, T, st));      // -> cell_leaf (T + 1)
-  uint32_t host_small[2] = {0, 0};
-  HIP_TRY(hipMemcpyAsync(&host_small[0], p.d_lc + T, 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(&host_small[1], p.d_bad, 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  if (host_small[1]) return fail(NSFPS_EINVAL, "points must be finite");
-  c.nleaves = host_small[0];
-  if (c.nleaves > p.leaf_ub)
-    return fail(NSFPS_EDEVICE, "internal: leaf count %u exceeds bound %u", c.nleaves, p.leaf_ub);
-  c.nl1 = (c.nleaves + kFan - 1) / kFan;
-  if (c.nl1 > kMaxL1)
-    return fail(NSFPS_EUNSUPPORTED, "cloud needs %u level-1 nodes (max %u)", c.nl1, kMaxL1);
-  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.nleaves, p.rng.dev, c.X, c.Y, c.Z, c.RANK,
-                            const_cast<float4 *>(c.leaf_lo), const_cast<float4 *>(c.leaf_hi),
-                            const_cast<uint32_t *>(c.leaf_cell), c.leaf_key, c.leaf_win, st));
-  // phys0 -> CloudDev (read back; the kernels take it by value)
-  HIP_TRY(hipMemcpyAsync(&c.phys0, p.d_phys0, 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  HIP_TRY(launch_init_state(c, st));
+  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, bt + fb, s.hist, true, &kdummy, &prank, st));
+  if (padded) {
+    HIP_TRY(hipMemsetAsync(c.P4, 0, (size_t)c.nslots * sizeof(float4), st));
+    HIP_TRY(hipMemsetAsync(const_cast<uint2 *>(c.RO), 0, (size_t)c.nslots * sizeof(uint2), st));
+  }
+  HIP_TRY(launch_gather(prank, lorig, s.bucket, p.d_counts, xyz, n, c.padded,
+                        (uint32_t)(padded ? cap : 0), c.P4, const_cast<uint2 *>(c.RO),
+                        p.d_small + 2, st));
+  HIP_TRY(launch_cell_info(p.d_counts, p.d_lc, T, p.d_cell_info, st));
+  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)cap, c.lpc, c.nleaves,
+                            p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
+                            const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
+                            c.leaf_key, c.leaf_pos, st));
+  HIP_TRY(launch_init_state(c, p.d_small + 2, st));
+  c.lds = plan_lds(c);
   return NSFPS_OK;
 }
 
@@ -363,9 +418,9 @@ uint32_t wide_iters_for(const CloudPlan &p) {
   if (env) {
     e = strtoull(env, nullptr, 10);
   } else {
-    e = p.n / 1024;
-    e = std::max<uint64_t>(e, 16);
-    e = std::min<uint64_t>(e, 2048);
+    e = p.n / 4096;
+    e = std::max<uint64_t>(e, 8);
+    e = std::min<uint64_t>(e, 1024);
   }
   return (uint32_t)std::min<uint64_t>(e, p.m);
 }
@@ -376,7 +431,8 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
   return ms;
 }
 
-// Runs a list of clouds: builds each, then one sampling launch for all.
+// Builds every cloud, then samples: grid-wide steps for the first iterations
+// of a single cloud, then one single-workgroup loop launch for all clouds.
 nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, bool out_on_host,
                         int32_t *h_out, uint64_t out_stride, uint64_t *out_lens) {
   auto t0 = std::chrono::steady_clock::now();
@@ -385,49 +441,46 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   if (rc) return rc;
   Arena &a = *ap;
   hipStream_t st = user_stream ? user_stream : a.stream;
-  // measure
   uint32_t nmax = 0;
   for (auto &p : plans) nmax = std::max(nmax, p.n);
   Bump meas(nullptr);
   for (auto &p : plans) layout_cloud(meas, p);
   Scratch sc{};
   layout_scratch(meas, nmax, sc);
-  CloudDev *d_clouds = meas.take<CloudDev>(plans.size());
-  (void)d_clouds;
+  meas.take<CloudDev>(plans.size());
   rc = arena_reserve(a, meas.off + 4096);
   if (rc) return rc;
   Bump bp(a.base);
   for (auto &p : plans) layout_cloud(bp, p);
   layout_scratch(bp, nmax, sc);
-  d_clouds = bp.take<CloudDev>(plans.size());
+  CloudDev *d_clouds = bp.take<CloudDev>(plans.size());
 
   HIP_TRY(hipEventRecord(a.ev[0], st));
   uint64_t leaves = 0, points = 0, wide_total = 0;
-  uint32_t max_nl1 = 1;
+  uint32_t lds_bytes = 0;
   for (auto &p : plans) {
     rc = build_cloud(p, sc, st);
     if (rc) return rc;
     leaves += p.dev.nleaves;
     points += p.n;
-    max_nl1 = std::max(max_nl1, p.dev.nl1);
+    lds_bytes = std::max(lds_bytes, p.dev.lds.total);
   }
   HIP_TRY(hipEventRecord(a.ev[1], st));
-  // sampling
   std::vector<CloudDev> devs;
   for (auto &p : plans) devs.push_back(p.dev);
   if (plans.size() == 1) {
     uint32_t e = wide_iters_for(plans[0]);
     wide_total = e;
-    if (e) {
-      uint32_t grid = std::max<uint32_t>(1, plans[0].dev.nl1);
-      HIP_TRY(launch_wide_steps(plans[0].dev, e, grid, st));
-    }
+    if (e) HIP_TRY(launch_wide_steps(plans[0].dev, e, std::max<uint32_t>(1, plans[0].dev.nl1), st));
   }
+  HIP_TRY(hipEventRecord(a.ev[3], st));
   HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                          hipMemcpyHostToDevice, st));
-  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), max_nl1, st));
+  HIP_TRY(hipEventRecord(a.ev[4], st));
+  const bool profile = getenv("NSFPS_PROFILE") != nullptr;
+  if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
+  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, st));
   HIP_TRY(hipEventRecord(a.ev[2], st));
-  // results
   std::vector<uint32_t> lens(plans.size());
   for (size_t i = 0; i < plans.size(); ++i)
     HIP_TRY(hipMemcpyAsync(&lens[i], plans[i].dev.iter, 4, hipMemcpyDeviceToHost, st));
@@ -436,16 +489,21 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   for (size_t i = 0; i < plans.size(); ++i) {
     out_lens[i] = lens[i];
     samples += lens[i];
-    if (out_on_host) {
+    if (out_on_host && lens[i])
       HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
                              hipMemcpyDeviceToHost, st));
-    }
   }
+  if (profile)
+    HIP_TRY(hipMemcpyAsync(g_prof, plans[0].dev.prof, sizeof(g_prof), hipMemcpyDeviceToHost, st));
+  else
+    memset(g_prof, 0, sizeof(g_prof));
   HIP_TRY(hipStreamSynchronize(st));
   auto t1 = std::chrono::steady_clock::now();
   nsfps_stats &S = g_stats;
   S.build_ms = ms_between(a.ev[0], a.ev[1]);
   S.sample_ms = ms_between(a.ev[1], a.ev[2]);
+  S.wide_ms = ms_between(a.ev[1], a.ev[3]);
+  S.late_ms = ms_between(a.ev[4], a.ev[2]);
   S.device_ms = S.build_ms + S.sample_ms;
   S.e2e_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   S.n_points = points;
@@ -453,6 +511,8 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   S.n_leaves = leaves;
   S.wide_iters = wide_total;
   S.samples = samples;
+  S.padded = plans.size() == 1 ? plans[0].dev.padded : 0;
+  S.lds_bytes = lds_bytes;
   return NSFPS_OK;
 }
 
@@ -644,6 +704,12 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const 
   if (rc) return rc;
   HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
   HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
+nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords) {
+  if (!words) return fail(NSFPS_EINVAL, "null pointer");
+  for (uint32_t i = 0; i < nwords; ++i) words[i] = i < kProfWords ? g_prof[i] : 0;
   return NSFPS_OK;
 }
 

@@ -1,5 +1,5 @@
 // Internal types shared by the host library (nsfps_host.cpp) and the HIP
-// kernels (nsfps_kernels.hip).  Not part of the C ABI.
+// kernels (nsfps_build.hip, nsfps_sample.hip).  Not part of the C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,10 +14,15 @@ constexpr uint32_t kFan = 64;
 // Sub-cell Morton bits (3 per axis) used to order points physically inside a
 // cell so that leaf bounding boxes are tight; results do not depend on it.
 constexpr uint32_t kFineBits = 9;
-// Largest number of level-1 tree nodes the single-workgroup loop keeps in LDS.
-constexpr uint32_t kMaxL1 = 8192;
-// Cube cells enumerated per chunk by the single-workgroup loop.
-constexpr uint32_t kCellChunk = 1024;
+// Level-1 nodes the single-workgroup loop can hold (level 2 then fits one wave).
+constexpr uint32_t kMaxL1 = 4096;
+// Threads of the single-workgroup loop (one cube cell per thread per chunk).
+constexpr uint32_t kLateThreads = 512;
+// Candidate leaves flattened into LDS per round.
+constexpr uint32_t kCandCap = 1024;
+// Dynamic LDS budget of the single-workgroup loop (gfx950: 160 KiB per CU).
+constexpr uint32_t kLdsBudget = 160 * 1024 - 1024;
+constexpr uint32_t kNone = 0xffffffffu;
 
 // Range values the kernels need, all derived on the host exactly as the
 // reference derives them (src/yuezu_fps.cpp:7-11, 136-161, 170-193).
@@ -27,40 +32,62 @@ struct RangeDev {
   float inv_bs[3];
   float bsize[3];
   uint32_t blocks[3];
-  uint32_t lut_off[3];  // offsets of the x/y/z LUTs in CloudDev::lut
+  uint32_t lut_off[3];  // offsets of the x/y/z LUTs in the concatenated LUT
+  uint32_t lut_total;
   uint32_t T;           // total blocks = number of buckets
   uint32_t bijective;   // 1 when bucket <-> cell is one-to-one
 };
 
+// Byte offsets inside the dynamic LDS of the single-workgroup loop; kNone
+// marks an optional region that did not fit.
+struct LdsPlan {
+  uint32_t l1k, l1p;      // level-1 keys (u64) and winner positions (float4)
+  uint32_t l1lo, l1hi;    // level-1 bounding boxes (float4), optional
+  uint32_t l2k, l2p;      // level-2 (<= 64 nodes)
+  uint32_t lut;           // concatenated Morton LUTs (u32)
+  uint32_t ctab;          // cell table (uint2, T + 1), optional
+  uint32_t cand;          // kCandCap x 3 u32: leaf, first slot, count
+  uint32_t slot;          // u32 per level-1 node: staging slot or kNone
+  uint32_t m1, dl1;       // dirty level-1 bitmask / list
+  uint32_t m2, dl2;       // dirty level-2 bitmask / list
+  uint32_t sk, sp;        // staging: dcap x 64 keys (u64) / positions (float4)
+  uint32_t dcap;          // staging slots (level-1 nodes per fast iteration)
+  uint32_t total;         // bytes
+};
+
 // Everything one cloud's kernels touch.  Device pointers; passed by value to
-// single-cloud kernels and as an array to the batched loop.
+// the grid-wide step and as an array to the single-workgroup loop.
 struct CloudDev {
   uint32_t n;        // points
-  uint32_t m;        // samples requested (1 <= m < n)
+  uint32_t m;        // samples requested (2 <= m < n)
+  uint32_t nslots;   // physical slots (n, or T * cap when padded)
   uint32_t nleaves;
   uint32_t nl1;      // level-1 tree nodes = ceil(nleaves / kFan)
   uint32_t phys0;    // physical slot of input row 0 (the first sample)
-  uint32_t pad_;
+  uint32_t padded;   // 1: slot = bucket * cap + j, leaf = bucket * lpc + k
+  uint32_t lpc;      // leaves per bucket when padded
   RangeDev r;
+  LdsPlan lds;
   const uint32_t *lut;
-  const float *X, *Y, *Z;
-  float *C;                  // min squared distance per physical slot
-  const uint32_t *RANK;      // logical rank per physical slot
-  const uint32_t *ORIG;      // input row per physical slot
-  const uint32_t *cell_leaf; // T + 1 entries: first leaf of each bucket
-  const float4 *leaf_lo;     // bbox min xyz, w = first physical slot (bits)
-  const float4 *leaf_hi;     // bbox max xyz, w = point count (bits)
-  const uint32_t *leaf_cell; // ix | iy << 10 | iz << 20
-  uint64_t *leaf_key;        // max key of the leaf
-  uint32_t *leaf_win;        // physical slot holding that key
+  float4 *P4;                 // x, y, z, min squared distance per slot
+  const uint2 *RO;            // logical rank, input row per slot
+  const uint2 *cell_info;     // T + 1 entries: first slot, first leaf
+  const float4 *leaf_lo;      // bbox min xyz, w = first slot (bits)
+  const float4 *leaf_hi;      // bbox max xyz, w = point count (bits)
+  const uint32_t *leaf_cell;  // ix | iy << 10 | iz << 20
+  uint64_t *leaf_key;         // max key of the leaf
+  float4 *leaf_pos;           // x, y, z, input row (bits) of that key
   uint64_t *l1_key;
-  uint32_t *l1_win;
-  uint64_t *root_key;        // 1 entry
-  uint32_t *root_win;        // 1 entry
-  uint32_t *iter;            // samples emitted so far (1 entry)
-  uint32_t *done;            // set once sampling finished (1 entry)
-  uint32_t *counter;         // arrival counter of the grid-wide step
-  int32_t *out;              // m entries
+  float4 *l1_pos;
+  const float4 *l1_lo;        // level-1 bounding boxes
+  const float4 *l1_hi;
+  uint64_t *root_key;         // 1 entry
+  float4 *root_pos;           // 1 entry
+  uint32_t *iter;             // samples emitted so far (1 entry)
+  uint32_t *done;             // set once sampling finished (1 entry)
+  uint32_t *counter;          // arrival counter of the grid-wide step
+  int32_t *out;               // m entries
+  uint64_t *prof;             // loop phase clocks / counters, or null
 };
 
 // Argmax key: larger min-distance wins, equal distances go to the smaller

@@ -1,4 +1,5 @@
-// Kernel launchers (defined in nsfps_kernels.hip, called by nsfps_host.cpp).
+// Kernel launchers (defined in nsfps_build.hip / nsfps_sample.hip, called by
+// nsfps_host.cpp).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -9,6 +10,7 @@
 
 namespace nsfps {
 
+// build
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
                             hipStream_t st);
@@ -21,19 +23,25 @@ hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
 hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,
                        uint32_t n, int fine_shift, int fine_bits, uint32_t *key2,
                        hipStream_t st);
-hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, const float *xyz,
-                         uint32_t n, float *X, float *Y, float *Z, float *C, uint32_t *RANK,
-                         uint32_t *ORIG, uint32_t *phys0, hipStream_t st);
-hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, hipStream_t st);
+hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
+                              hipStream_t st);
+hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
+                            uint2 *info, hipStream_t st);
+hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, const uint32_t *bucket,
+                         const uint32_t *cell_start, const float *xyz, uint32_t n,
+                         uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO, uint32_t *phys0,
+                         hipStream_t st);
 hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
-                             uint32_t nleaves, const RangeDev &r, const float *X, const float *Y,
-                             const float *Z, const uint32_t *RANK, float4 *leaf_lo,
-                             float4 *leaf_hi, uint32_t *leaf_cell, uint64_t *leaf_key,
-                             uint32_t *leaf_win, hipStream_t st);
-hipError_t launch_init_state(const CloudDev &c, hipStream_t st);
+                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
+                             const RangeDev &r, const float4 *P4, const uint2 *RO,
+                             float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
+                             uint64_t *leaf_key, float4 *leaf_pos, hipStream_t st);
+hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st);
+
+// sampling
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
-size_t late_lds(uint32_t max_nl1);
-hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                            hipStream_t st);
+hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t lds_bytes,
+                            bool profile, hipStream_t st);
+constexpr uint32_t kProfWords = 24;
 
 }  // namespace nsfps

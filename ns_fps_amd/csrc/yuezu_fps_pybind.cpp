@@ -228,6 +228,10 @@ py::dict last_stats_py() {
   py::dict d;
   d["build_ms"] = s.build_ms;
   d["sample_ms"] = s.sample_ms;
+  d["wide_ms"] = s.wide_ms;
+  d["late_ms"] = s.late_ms;
+  d["padded"] = s.padded;
+  d["lds_bytes"] = s.lds_bytes;
   d["device_ms"] = s.device_ms;
   d["e2e_ms"] = s.e2e_ms;
   d["n_points"] = s.n_points;
@@ -300,6 +304,11 @@ PYBIND11_MODULE(yuezu_fps_module, m) {
         py::arg("y_blocks") = NSFPS_DEFAULT_Y_BLOCKS, py::arg("z_blocks") = NSFPS_DEFAULT_Z_BLOCKS);
 
   m.def("last_stats", &last_stats_py);
+  m.def("last_loop_profile", []() {
+    std::vector<uint64_t> w(24, 0);
+    nsfps_get_loop_profile(w.data(), (uint32_t)w.size());
+    return w;
+  });
   m.def("device_count", []() { return nsfps_device_count(); });
 
   m.attr("DEFAULT_X_BLOCKS") = NSFPS_DEFAULT_X_BLOCKS;

@@ -283,7 +283,8 @@ static inline int cube_half(float D, float bsize, uint32_t blocks) {
 static int fps_core(const float *xyz, uint64_t n, uint64_t m,
                     const float *bounds6, const uint32_t *blocks3,
                     int32_t *out, uint64_t *out_len, orc_census *census,
-                    int audit, float *max_dist, uint32_t *cand_trace) {
+                    int audit, float *max_dist, uint32_t *cand_trace,
+                    uint32_t *leaf_trace) {
   *out_len = 0;
   if (census) memset(census, 0, sizeof(*census));
   if (n == 0 || m == 0) return 0; /* src/yuezu_fps.cpp:678-680 */
@@ -349,6 +350,11 @@ static int fps_core(const float *xyz, uint64_t n, uint64_t m,
   uint64_t len = 1;
   if (max_dist) max_dist[0] = INFINITY;
   if (cand_trace) cand_trace[0] = (uint32_t)n;
+  if (leaf_trace) {
+    uint64_t l0 = 0;
+    for (uint64_t b = 0; b < T; ++b) l0 += (s.start[b + 1] - s.start[b] + ORC_LEAF - 1) / ORC_LEAF;
+    leaf_trace[0] = (uint32_t)l0;
+  }
   for (uint64_t it = 1; it < m; ++it) {
     orc_key top = s.tree[1];
     float D = top.v < 0.0f ? 0.0f : top.v;
@@ -371,13 +377,14 @@ static int fps_core(const float *xyz, uint64_t n, uint64_t m,
       hi[a] = (int)qc[a] + h[a] > (int)s.r.blocks[a] - 1 ? (int)s.r.blocks[a] - 1
                                                           : (int)qc[a] + h[a];
     }
-    uint64_t cand_pts = 0;
+    uint64_t cand_pts = 0, cand_lv = 0;
     for (int bz = lo[2]; bz <= hi[2]; ++bz)
       for (int by = lo[1]; by <= hi[1]; ++by)
         for (int bx = lo[0]; bx <= hi[0]; ++bx) {
           uint64_t b = code_of(&s.r, (uint32_t)bx, (uint32_t)by, (uint32_t)bz) % T;
           uint64_t c = s.start[b + 1] - s.start[b];
           cand_pts += c;
+          cand_lv += (c + ORC_LEAF - 1) / ORC_LEAF;
           if (census) {
             census->cand_cells++;
             census->cand_points += c;
@@ -388,6 +395,7 @@ static int fps_core(const float *xyz, uint64_t n, uint64_t m,
         }
     if (census) census->iterations++;
     if (cand_trace) cand_trace[it] = (uint32_t)(cand_pts > UINT32_MAX ? UINT32_MAX : cand_pts);
+    if (leaf_trace) leaf_trace[it] = (uint32_t)(cand_lv > UINT32_MAX ? UINT32_MAX : cand_lv);
     if (audit && census) {
       for (uint64_t b = 0; b < T; ++b) {
         if (s.stamp[b] == (uint32_t)it) continue;
@@ -406,14 +414,15 @@ int orc_fps(const float *xyz, uint64_t n, uint64_t m, const float *bounds6,
             const uint32_t *blocks3, int32_t *out, uint64_t *out_len,
             orc_census *census, int audit) {
   return fps_core(xyz, n, m, bounds6, blocks3, out, out_len, census, audit,
-                  NULL, NULL);
+                  NULL, NULL, NULL);
 }
 
 int orc_fps_trace(const float *xyz, uint64_t n, uint64_t m,
                   const float *bounds6, const uint32_t *blocks3, int32_t *out,
-                  uint64_t *out_len, float *max_dist, uint32_t *cand_points) {
+                  uint64_t *out_len, float *max_dist, uint32_t *cand_points,
+                  uint32_t *cand_leaves) {
   return fps_core(xyz, n, m, bounds6, blocks3, out, out_len, NULL, 0, max_dist,
-                  cand_points);
+                  cand_points, cand_leaves);
 }
 
 int orc_fps_naive(const float *xyz, uint64_t n, uint64_t m,

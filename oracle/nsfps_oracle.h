@@ -59,11 +59,13 @@ int orc_fps(const float *xyz, uint64_t n, uint64_t m, const float *bounds6,
             const uint32_t *blocks3, int32_t *out, uint64_t *out_len,
             orc_census *census, int audit);
 
-/* Per-iteration record of the same run: selected maximum (fp32 bits) and
- * the number of candidate points.  Arrays hold m entries. */
+/* Per-iteration record of the same run: selected maximum, candidate points
+ * and candidate 16-point leaves (entry 0: the first full pass).  Arrays hold
+ * m entries; cand_leaves may be NULL. */
 int orc_fps_trace(const float *xyz, uint64_t n, uint64_t m,
                   const float *bounds6, const uint32_t *blocks3, int32_t *out,
-                  uint64_t *out_len, float *max_dist, uint32_t *cand_points);
+                  uint64_t *out_len, float *max_dist, uint32_t *cand_points,
+                  uint32_t *cand_leaves);
 
 /* Naive O(N*M) FPS (eval/src_cpu/compare_cpu_test.cpp:10-57 shape):
  * start at row 0, cache initialised to FLT_MAX, full update every iteration,

@@ -120,19 +120,22 @@ class Oracle:
         res = out[:ol.value].copy()
         return (res, c) if (census or audit) else res
 
-    def fps_trace(self, points, n_samples, rng=None, blocks=(16, 16, 16)):
+    def fps_trace(self, points, n_samples, rng=None, blocks=(16, 16, 16), leaves=False):
         p = _pts(points)
         b6, b3 = _range_args(rng, blocks)
         m = max(int(n_samples), 1)
         out = np.zeros(m, np.int32)
         md = np.zeros(m, np.float32)
         cp = np.zeros(m, np.uint32)
+        cl = np.zeros(m, np.uint32)
         ol = ctypes.c_uint64()
         rc = self.lib.orc_fps_trace(_ptr(p), _u64(len(p)), _u64(int(n_samples)), b6, b3,
-                                    _ptr(out), ctypes.byref(ol), _ptr(md), _ptr(cp))
+                                    _ptr(out), ctypes.byref(ol), _ptr(md), _ptr(cp), _ptr(cl))
         if rc:
             raise ValueError(f"orc_fps_trace failed ({rc})")
         k = ol.value
+        if leaves:
+            return out[:k].copy(), md[:k].copy(), cp[:k].copy(), cl[:k].copy()
         return out[:k].copy(), md[:k].copy(), cp[:k].copy()
 
     def fps_naive(self, points, n_samples, tie="index", rng=None, blocks=(16, 16, 16),

@@ -1,0 +1,170 @@
+"""GPU parity: the HIP path against the reference's golden vectors (small
+cases in full, the five workloads by SHA-256 of the int32 output) and against
+the CPU oracle on seeded clouds, through the Python module and through the C
+ABI.  Bit-exact for every index and the output length (integer/index work:
+no tolerance)."""
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN_CASES, GOLDEN_CONFIGS, sha256_f32, sha256_i32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from ns_fps_amd.capi import Lib
+    L = Lib()
+    if L.device_count() < 1:
+        pytest.fail("no HIP device visible: GPU tests need an MI355X")
+    return L
+
+
+def run_module(yf, case):
+    if case.range is None:
+        return yf.fps_with_bbox(case.points, case.n_samples, *case.blocks)
+    return yf.fps(case.points, case.n_samples, yf.make_range(*case.range))
+
+
+@pytest.mark.parametrize("case", GOLDEN_CASES, ids=lambda c: c.name)
+def test_golden_case_module(yf, lib, case):
+    got = run_module(yf, case)
+    assert got.dtype == np.int32
+    assert np.array_equal(got, case.expected), case.name
+
+
+@pytest.mark.parametrize("case", GOLDEN_CASES, ids=lambda c: c.name)
+def test_golden_case_capi(lib, case):
+    if case.range is None:
+        got = lib.fps_bbox(case.points, case.n_samples, case.blocks)
+    else:
+        got = lib.fps(case.points, case.n_samples, case.range)
+    assert np.array_equal(got, case.expected)
+
+
+def run_workload(yf, lib, wname):
+    from ns_fps_amd.workloads import make_workload
+    w = make_workload(wname)
+    g = GOLDEN_CONFIGS[wname]
+    assert sha256_f32(np.concatenate(w["clouds"])) == g["input_sha256"]
+    if len(w["clouds"]) == 1:
+        outs = [yf.fps(w["clouds"][0], w["n_samples"], yf.make_range(*w["range"]))]
+    else:
+        idx, lens = yf.fps_batched(np.stack(w["clouds"]), w["n_samples"], None, *w["blocks"])
+        outs = [idx[b, :lens[b]] for b in range(len(lens))]
+    return w, g, outs
+
+
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes"])
+def test_workload_matches_reference_hash(yf, lib, wname):
+    w, g, outs = run_workload(yf, lib, wname)
+    assert [len(o) for o in outs] == g["lengths"]
+    assert list(outs[0][:16]) == g["head"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
+def test_clustered_workload_matches_reference_hash(yf, lib):
+    if "clustered" not in GOLDEN_CONFIGS:
+        pytest.skip("golden hash for the 8,388,608-point workload not generated")
+    w, g, outs = run_workload(yf, lib, "clustered")
+    assert len(outs[0]) == g["lengths"][0]
+    assert list(outs[0][:16]) == g["head"]
+    assert sha256_i32(outs[0]) == g["output_sha256"][0]
+
+
+@pytest.mark.parametrize("seed,n,m,blocks,scale", [
+    (100, 20000, 3000, (16, 16, 16), 1.0),
+    (101, 50000, 6000, (32, 32, 32), 1.0),
+    (102, 30000, 4000, (32, 16, 8), 3.0),
+    (103, 40000, 5000, (10, 12, 6), 1.0),     # non-power-of-two: general bucket path
+    (104, 25000, 25000 - 1, (8, 8, 8), 1.0),  # every point but one
+])
+def test_random_clouds_match_oracle(yf, oracle, seed, n, m, blocks, scale):
+    rs = np.random.RandomState(seed)
+    pts = (rs.randn(n, 3) * scale).astype(np.float32)
+    pts[: n // 50] = pts[n // 50: 2 * (n // 50)]   # exact duplicates
+    rng = (-3.0 * scale, 3.0 * scale, -3.0 * scale, 3.0 * scale, -3.0 * scale, 3.0 * scale, *blocks)
+    got = yf.fps(pts, m, yf.make_range(*rng))
+    assert np.array_equal(got, oracle.fps(pts, m, rng))
+
+
+def test_batched_matches_per_cloud_calls(yf, oracle):
+    rs = np.random.RandomState(7)
+    clouds = rs.randn(6, 3000, 3).astype(np.float32)
+    clouds[2] *= 50
+    clouds[3, 100:200] = clouds[3, :100]
+    idx, lens = yf.fps_batched(clouds, 500)
+    for b in range(6):
+        assert np.array_equal(idx[b, :lens[b]], oracle.fps(clouds[b], 500, None, (16, 16, 16)))
+        assert np.all(idx[b, lens[b]:] == -1)
+    rngs = [yf.make_range(-4, 4, -4, 4, -4, 4, 8, 8, 8)] * 6
+    clouds2 = np.clip(clouds, -3.9, 3.9)
+    idx2, lens2 = yf.fps_batched(clouds2, 300, rngs)
+    for b in range(6):
+        want = oracle.fps(clouds2[b], 300, (-4, 4, -4, 4, -4, 4, 8, 8, 8))
+        assert np.array_equal(idx2[b, :lens2[b]], want)
+
+
+def test_device_pointer_entry_point(lib):
+    from ns_fps_amd.capi import Hip
+    hip = Hip()
+    case = {c.name: c for c in GOLDEN_CASES}["testpy_10k_1k"]
+    d_xyz = hip.upload(case.points)
+    d_out = hip.malloc(case.n_samples * 4)
+    try:
+        n = lib.fps_device(d_xyz, len(case.points), case.n_samples, case.range, d_out)
+        got = hip.download(d_out, n, np.int32)
+    finally:
+        hip.free(d_xyz)
+        hip.free(d_out)
+    assert np.array_equal(got, case.expected)
+
+
+@pytest.mark.parametrize("env", [
+    {"NSFPS_WIDE_ITERS": "0"}, {"NSFPS_WIDE_ITERS": "1"}, {"NSFPS_WIDE_ITERS": "37"},
+    {"NSFPS_WIDE_ITERS": "100000"}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_PROFILE": "1"},
+])
+def test_schedule_and_layout_do_not_change_results(yf, env, monkeypatch):
+    """Where the grid-wide phase hands over to the single-workgroup loop, the
+    padded or table layout and the profiling build are result-invariant."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    for name in ["testpy_10k_1k", "lattice_ties_16", "granularity_64x64x64", "boundary_aligned"]:
+        case = {c.name: c for c in GOLDEN_CASES}[name]
+        assert np.array_equal(run_module(yf, case), case.expected), name
+
+
+def test_repeated_and_resized_calls(yf):
+    """The cached device workspace is reused and regrown between calls."""
+    by = {c.name: c for c in GOLDEN_CASES}
+    seq = ["trace_100_20", "quickstart_full", "testpy_100_10", "granularity_32x32x32",
+           "trace_100_20"]
+    for name in seq:
+        case = by[name]
+        assert np.array_equal(run_module(yf, case), case.expected), name
+
+
+def test_non_finite_points_are_rejected(yf):
+    pts = np.random.RandomState(0).randn(1000, 3).astype(np.float32)
+    pts[17, 1] = np.nan
+    with pytest.raises(ValueError, match="finite"):
+        yf.fps(pts, 100, yf.make_range(-4, 4, -4, 4, -4, 4, 8, 8, 8))
+    pts[17, 1] = np.inf
+    with pytest.raises(ValueError, match="finite"):
+        yf.fps(pts, 100, yf.make_range(-4, 4, -4, 4, -4, 4, 8, 8, 8))
+
+
+def test_full_size_properties(yf):
+    """Size-independent properties of a full-size run: distinct indices in
+    range, the first sample is row 0, and sampling is deterministic."""
+    from ns_fps_amd.workloads import make_workload
+    w = make_workload("uniform_cube")
+    r = yf.make_range(*w["range"])
+    a = yf.fps(w["clouds"][0], w["n_samples"], r)
+    b = yf.fps(w["clouds"][0], w["n_samples"], r)
+    assert np.array_equal(a, b)
+    assert a[0] == 0 and len(np.unique(a)) == len(a) == w["n_samples"]
+    assert a.min() >= 0 and a.max() < len(w["clouds"][0])

@@ -1,0 +1,175 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every declared entry point, range derivation matches the oracle and the
+reference, the Python module mirrors the reference surface
+(yuezu_fps/yuezu_fps_pybind.cpp:103-150) and its error behaviour, and compute
+calls fail loudly without a device (no CPU fallback)."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+
+class Range(ctypes.Structure):
+    _fields_ = [("min_x", ctypes.c_float), ("max_x", ctypes.c_float),
+                ("min_y", ctypes.c_float), ("max_y", ctypes.c_float),
+                ("min_z", ctypes.c_float), ("max_z", ctypes.c_float),
+                ("x_blocks", ctypes.c_uint32), ("y_blocks", ctypes.c_uint32),
+                ("z_blocks", ctypes.c_uint32)]
+
+
+class RangeInfo(ctypes.Structure):
+    _fields_ = [("inv_bs", ctypes.c_float * 3), ("block_size", ctypes.c_float * 3),
+                ("bits", ctypes.c_uint32 * 3), ("total_bits", ctypes.c_uint32),
+                ("total_blocks", ctypes.c_uint64)]
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "nsfps.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(nsfps_[a-z_]+)\s*\(", text)))
+
+
+def has_gpu(yf):
+    return yf.device_count() > 0
+
+
+def test_capi_exports_every_declared_symbol(capi):
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(capi, s), s
+
+
+def test_capi_range_derive_matches_oracle(capi, oracle):
+    for rng in [(-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 32, 32, 32),
+                (-80.0, 80.0, -80.0, 80.0, -4.0, 4.0, 32, 32, 8),
+                (-5.0, 7.0, 0.0, 1.0, -2.0, 2.0, 10, 3, 1)]:
+        r = Range(*rng)
+        info = RangeInfo()
+        luts = (ctypes.c_uint32 * 4096)()
+        assert capi.nsfps_range_derive(ctypes.byref(r), ctypes.byref(info), luts,
+                                       ctypes.c_uint64(4096)) == 0
+        o = oracle.range(rng)
+        assert list(info.bits) == o["bits"]
+        assert np.array(list(info.inv_bs), np.float32).tobytes() == o["inv_bs"].tobytes()
+        assert np.array(list(info.block_size), np.float32).tobytes() == o["block_size"].tobytes()
+        off = 0
+        for a in range(3):
+            n = 1 << o["bits"][a]
+            assert list(luts[off:off + n]) == list(o["luts"][a])
+            off += n
+        assert info.total_blocks == rng[6] * rng[7] * rng[8]
+
+
+def test_capi_bbox_matches_oracle(capi, oracle):
+    pts = np.random.RandomState(3).randn(777, 3).astype(np.float32) * 5
+    out = Range()
+    assert capi.nsfps_bbox(pts.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint64(len(pts)), 16, 8, 4,
+                           ctypes.byref(out)) == 0
+    got = np.array([out.min_x, out.max_x, out.min_y, out.max_y, out.min_z, out.max_z], np.float32)
+    assert got.tobytes() == oracle.bbox(pts).tobytes()
+    assert (out.x_blocks, out.y_blocks, out.z_blocks) == (16, 8, 4)
+
+
+def test_capi_rejects_bad_arguments(capi):
+    capi.nsfps_last_error.restype = ctypes.c_char_p
+    pts = np.zeros((10, 3), np.float32)
+    out = np.zeros(10, np.int32)
+    n = ctypes.c_uint64()
+    bad = Range(1.0, 1.0, 0.0, 1.0, 0.0, 1.0, 4, 4, 4)  # max == min
+    rc = capi.nsfps_fps(pts.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint64(10), ctypes.c_uint64(5),
+                        ctypes.byref(bad), out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n))
+    assert rc == 1 and b"max > min" in capi.nsfps_last_error()
+    zero = Range(0.0, 1.0, 0.0, 1.0, 0.0, 1.0, 0, 4, 4)
+    rc = capi.nsfps_fps(pts.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint64(10), ctypes.c_uint64(5),
+                        ctypes.byref(zero), out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n))
+    assert rc == 1
+    rc = capi.nsfps_fps(None, ctypes.c_uint64(10), ctypes.c_uint64(5), None,
+                        out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n))
+    assert rc == 1
+
+
+def test_module_surface_mirrors_reference(yf):
+    for name in ["SpaceRange", "make_range", "make_uniform_range", "fps", "fps_with_bbox",
+                 "DEFAULT_X_BLOCKS", "DEFAULT_Y_BLOCKS", "DEFAULT_Z_BLOCKS",
+                 "MORTON_BLOCK_SIZE", "CACHE_BLOCK_SIZE"]:
+        assert hasattr(yf, name), name
+    assert (yf.DEFAULT_X_BLOCKS, yf.MORTON_BLOCK_SIZE, yf.CACHE_BLOCK_SIZE) == (16, 16, 16)
+    r = yf.make_range(-150, 150, -150, 150, -150, 150, 16, 16, 16)   # example.py:115
+    assert (r.min_x, r.max_x, r.x_blocks) == (-150.0, 150.0, 16)
+    assert r.total_bits() == 12 and r.total_blocks() == 4096
+    assert r.block_size_x() == np.float32(300.0 / 16)
+    u = yf.make_uniform_range(-1, 1, -2, 2, -3, 3, 8)
+    assert (u.x_blocks, u.y_blocks, u.z_blocks) == (8, 8, 8)
+    assert (u.x_bits(), u.y_bits(), u.z_bits()) == (3, 3, 3)
+    s = yf.SpaceRange()
+    s.min_x, s.max_x, s.min_y, s.max_y, s.min_z, s.max_z = -1, 1, -1, 1, -1, 1
+    s.x_blocks, s.y_blocks, s.z_blocks = 32, 16, 8
+    assert (s.x_bits(), s.y_bits(), s.z_bits(), s.total_bits()) == (5, 4, 3, 12)
+    # derived values follow field edits (the reference keeps stale ones)
+    s.x_blocks = 64
+    assert s.x_bits() == 6 and s.inv_bs_x == np.float32(32.0)
+
+
+def test_module_trivial_guards_need_no_device(yf):
+    pts = np.random.RandomState(0).randn(5, 3).astype(np.float32)
+    r = yf.make_range(-4, 4, -4, 4, -4, 4, 4, 4, 4)
+    assert list(yf.fps(pts, 5, r)) == [0, 1, 2, 3, 4]           # n >= N: identity
+    assert list(yf.fps(pts, 9, r)) == [0, 1, 2, 3, 4]
+    assert list(yf.fps(pts, 0, r)) == []
+    assert list(yf.fps(pts, 1, r)) == [0]
+    assert list(yf.fps(np.zeros((0, 3), np.float32), 4, r)) == []
+    assert yf.fps(pts, 5, r).dtype == np.int32
+    # keyword spellings: the binding's sample_count and the README's n_samples
+    assert list(yf.fps(pts, sample_count=7, range=r)) == [0, 1, 2, 3, 4]
+    assert list(yf.fps(pts, n_samples=7, range=r)) == [0, 1, 2, 3, 4]
+    assert list(yf.fps_with_bbox(pts, 6)) == [0, 1, 2, 3, 4]
+
+
+def test_module_error_behaviour(yf):
+    pts = np.random.RandomState(0).randn(50, 3).astype(np.float32)
+    with pytest.raises(RuntimeError, match="shape"):          # reference: RuntimeError
+        yf.fps(np.zeros((10, 2), np.float32), 3)
+    with pytest.raises(ValueError):
+        yf.fps(np.zeros((10, 2), np.float32), 3)
+    with pytest.raises(yf.InputError):
+        yf.fps(pts, 10, {"min_x": 0, "max_x": 1})              # incomplete dict
+    with pytest.raises(yf.InputError):
+        yf.fps(pts, 10, yf.make_range(1, 1, 0, 1, 0, 1, 4, 4, 4))
+    with pytest.raises(yf.InputError):
+        yf.fps(pts, 10, yf.make_range(0, 1, 0, 1, 0, 1, 0, 4, 4))
+    with pytest.raises(yf.InputError):
+        yf.fps(pts, 10, 5)
+
+
+def test_module_converts_strided_and_float64_input(yf):
+    """The reference reads a strided view such as pc[:, :3] as if it were
+    contiguous (yuezu_fps/yuezu_fps_pybind.cpp:17-33); here it is converted.
+    Checked through the trivial identity path so it runs without a device."""
+    pc = np.random.RandomState(0).randn(6, 4).astype(np.float32)
+    r = yf.make_range(-4, 4, -4, 4, -4, 4, 4, 4, 4)
+    assert list(yf.fps(pc[:, :3], 10, r)) == list(range(6))
+    assert list(yf.fps(pc[:, :3].astype(np.float64), 10, r)) == list(range(6))
+
+
+def test_compute_fails_loudly_without_device(yf):
+    if has_gpu(yf):
+        pytest.skip("a GPU is present")
+    pts = np.random.RandomState(0).randn(100, 3).astype(np.float32)
+    with pytest.raises(RuntimeError, match="no HIP device"):
+        yf.fps(pts, 10, yf.make_range(-4, 4, -4, 4, -4, 4, 8, 8, 8))
+    with pytest.raises(RuntimeError, match="no HIP device"):
+        yf.fps_batched(np.stack([pts, pts]), 10)
+
+
+def test_dict_range_uses_default_blocks(yf):
+    """A dict range takes the six bounds and optional block counts, default 16
+    (yuezu_fps/yuezu_fps_pybind.cpp:48-58); via the identity path."""
+    pts = np.random.RandomState(0).randn(4, 3).astype(np.float32)
+    d = {"min_x": -4, "max_x": 4, "min_y": -4, "max_y": 4, "min_z": -4, "max_z": 4}
+    assert list(yf.fps(pts, 4, d)) == [0, 1, 2, 3]

@@ -1,0 +1,230 @@
+"""Pins the CPU oracle (oracle/nsfps_oracle.c) before it is trusted as the
+checker of the GPU path.
+
+* golden vectors written by the reference itself (tests/golden/make_golden.py
+  runs src/yuezu_fps.cpp compiled from its own sources, FMA off);
+* closed forms of the range derivation (Morton bit positions, fp32 reciprocal);
+* an independent brute-force FPS (full update every iteration, argmax over the
+  logical key) -- equal whenever the reference's cube rule skips only no-op
+  updates, which the oracle's audit mode checks;
+* test.py's own acceptance check (distance sequences within 1e-3);
+* discrimination: the checks fail on the plausible mistakes (lowest-index ties,
+  FMA contraction).
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN_CASES, GOLDEN_CONFIGS, sha256_f32, sha256_i32
+
+
+def positions(lut, bits):
+    """Target bit of each source bit k, from LUT entry 1 << k."""
+    return [int(lut[1 << k]).bit_length() - 1 for k in range(bits)]
+
+
+@pytest.mark.parametrize("blocks,expect", [
+    ((16, 16, 16), ([0, 3, 6, 9], [1, 4, 7, 10], [2, 5, 8, 11])),
+    ((32, 32, 8), ([0, 3, 6, 9, 11], [1, 4, 7, 10, 12], [2, 5, 8])),
+    ((4, 16, 64), ([0, 3], [1, 4, 6, 8], [2, 5, 7, 9, 10, 11])),
+    ((64, 64, 64), ([0, 3, 6, 9, 12, 15], [1, 4, 7, 10, 13, 16], [2, 5, 8, 11, 14, 17])),
+])
+def test_morton_bit_positions_closed_form(oracle, blocks, expect):
+    # src/yuezu_fps.cpp:69-97: min(bits) rounds of x,y,z, then x,y,z where present
+    r = oracle.range((-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks))
+    for a in range(3):
+        assert positions(r["luts"][a], r["bits"][a]) == expect[a]
+        lut = r["luts"][a]
+        for v in range(len(lut)):
+            want = sum(1 << expect[a][k] for k in range(r["bits"][a]) if v >> k & 1)
+            assert lut[v] == want
+
+
+@pytest.mark.parametrize("blocks", [(16, 16, 16), (32, 32, 8), (64, 64, 64), (8, 4, 2)])
+def test_power_of_two_codes_are_a_bijection(oracle, blocks):
+    r = oracle.range((-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks))
+    x, y, z = r["luts"]
+    codes = (x[:blocks[0], None, None] | y[None, :blocks[1], None] | z[None, None, :blocks[2]])
+    T = blocks[0] * blocks[1] * blocks[2]
+    assert codes.max() < T and len(np.unique(codes)) == T
+
+
+@pytest.mark.parametrize("rng", [
+    (-100.0, 100.0, -100.0, 100.0, -100.0, 100.0, 16, 16, 16),
+    (-80.0, 80.0, -80.0, 80.0, -4.0, 4.0, 32, 32, 8),
+    (-600.0, 600.0, -600.0, 600.0, -600.0, 600.0, 64, 64, 64),
+    (-0.3, 1.7, 2.0, 9.0, -1e-3, 1e-3, 10, 3, 7),
+])
+def test_inverse_block_size_is_fp32_reciprocal(oracle, rng):
+    # src/yuezu_fps.cpp:140-142: 1.0f / ((max - min) / (float)blocks), all fp32
+    r = oracle.range(rng)
+    for a in range(3):
+        lo, hi, b = np.float32(rng[2 * a]), np.float32(rng[2 * a + 1]), np.float32(rng[6 + a])
+        bs = np.float32(hi - lo) / b
+        assert r["block_size"][a].tobytes() == np.float32(bs).tobytes()
+        assert r["inv_bs"][a].tobytes() == (np.float32(1.0) / bs).tobytes()
+
+
+def numpy_cells(points, rng):
+    """src/yuezu_fps.cpp:170-199 restated with NumPy float32 ops."""
+    p = np.asarray(points, np.float32)
+    out = np.zeros((len(p), 3), np.uint32)
+    for a in range(3):
+        lo, hi, b = np.float32(rng[2 * a]), np.float32(rng[2 * a + 1]), rng[6 + a]
+        inv = np.float32(1.0) / (np.float32(hi - lo) / np.float32(b))
+        v = p[:, a]
+        hic = np.float32(hi - np.float32(1e-6))
+        c = np.where(hic < v, hic, v)           # std::min(v, hi - eps)
+        c = np.where(lo < c, c, lo)             # std::max(lo, c)
+        i = ((c - lo) * inv).astype(np.float32).astype(np.uint32)
+        out[:, a] = np.minimum(i, b - 1)
+    return out
+
+
+def test_cell_indices_match_numpy_and_special_values(oracle):
+    rng = (-1.0, 1.0, -2.0, 2.0, 0.0, 8.0, 32, 16, 8)
+    pts = np.random.RandomState(0).uniform(-1.5, 1.5, (5000, 3)).astype(np.float32)
+    pts[:, 1] *= 2
+    pts[:, 2] = pts[:, 2] * 4 + 4
+    special = np.array([[-1, -2, 0], [1, 2, 8], [0, 0, 4], [-5, 7, -3], [0.9999999, 1.9999999, 7.9999999],
+                        [-1 + 2 / 32, -2 + 4 / 16, 1.0], [1e-8, -1e-8, 4 - 1e-7]], np.float32)
+    pts = np.concatenate([pts, special])
+    cells, codes = oracle.cell_code(pts, rng)
+    assert np.array_equal(cells, numpy_cells(pts, rng))
+    # hand values: the top corner clamps into the last cell, below-range into 0
+    assert tuple(cells[-6]) == (31, 15, 7)
+    assert tuple(cells[-7]) == (0, 0, 0)
+    assert tuple(cells[-4]) == (0, 15, 0)
+    r = oracle.range(rng)
+    x, y, z = r["luts"]
+    assert np.array_equal(codes, x[cells[:, 0]] | y[cells[:, 1]] | z[cells[:, 2]])
+
+
+def test_layout_is_stable_bucket_order(oracle):
+    pts = np.random.RandomState(1).randn(3000, 3).astype(np.float32)
+    rng = (-3.0, 3.0, -3.0, 3.0, -3.0, 3.0, 8, 8, 8)
+    bucket, order = oracle.layout(pts, rng)
+    assert np.array_equal(order, np.argsort(bucket, kind="stable"))
+
+
+@pytest.mark.parametrize("case", GOLDEN_CASES, ids=lambda c: c.name)
+def test_oracle_matches_reference_golden(oracle, case):
+    got = oracle.fps(case.points, case.n_samples, case.range, case.blocks)
+    assert np.array_equal(got, case.expected)
+
+
+def test_reference_library_matches_golden_when_built(oracle):
+    from oracle import REF_SO, Reference
+    if not os.path.exists(REF_SO):
+        pytest.skip("oracle/_ref not built here")
+    ref = Reference()
+    for case in GOLDEN_CASES[:12]:
+        assert np.array_equal(ref.fps(case.points, case.n_samples, case.range, case.blocks),
+                              case.expected), case.name
+
+
+@pytest.mark.parametrize("seed,n,m,blocks", [
+    (0, 200, 40, (4, 4, 4)), (1, 500, 120, (8, 8, 8)), (2, 800, 300, (16, 16, 16)),
+    (3, 600, 200, (16, 8, 4)), (4, 700, 250, (10, 10, 10)), (5, 400, 399, (2, 2, 2)),
+])
+def test_oracle_equals_brute_force_fps(oracle, seed, n, m, blocks):
+    """Independent check: full update every iteration, argmax over the logical
+    key (bucket, index).  Equal whenever the cube rule only skips no-op updates
+    (audit count 0)."""
+    pts = np.random.RandomState(seed).randn(n, 3).astype(np.float32)
+    pts[: n // 10] = pts[n // 10: 2 * (n // 10)]  # exact duplicates
+    rng = (-4.0, 4.0, -4.0, 4.0, -4.0, 4.0, *blocks)
+    got, census = oracle.fps(pts, m, rng, audit=True)
+    assert census.audit_violations == 0
+    naive = oracle.fps_naive(pts, m, tie="logical", rng=rng)
+    assert np.array_equal(got, naive)
+
+
+def test_tie_rule_is_discriminated_by_the_fixtures(oracle):
+    """Lowest-index ties (the north-star wording) differ from the reference's
+    bucket-order ties on the hand-made case and on the lattice: the fixtures
+    pin the rule."""
+    by_name = {c.name: c for c in GOLDEN_CASES}
+    tie = by_name["tie_bucket_order"]
+    assert list(tie.expected) == [0, 2]
+    assert list(oracle.fps_naive(tie.points, 2, tie="index")) == [0, 1]
+    lat = by_name["lattice_ties_16"]
+    lowest = oracle.fps_naive(lat.points, lat.n_samples, tie="index")
+    assert not np.array_equal(lowest, lat.expected)
+    logical = oracle.fps_naive(lat.points, lat.n_samples, tie="logical", rng=lat.range)
+    assert np.array_equal(logical, lat.expected)
+
+
+def test_fma_contraction_is_discriminated_when_reference_built():
+    """The reference built with its own setup.py flags (FMA contraction) gives
+    different indices on the LiDAR workload: the golden hash pins the
+    no-contraction arithmetic."""
+    from oracle import REF_ASBUILT_SO, Reference
+    from ns_fps_amd.workloads import make_workload
+    if not os.path.exists(REF_ASBUILT_SO):
+        pytest.skip("oracle/_ref not built here")
+    w = make_workload("lidar_scan")
+    fma = Reference(REF_ASBUILT_SO).fps(w["clouds"][0], w["n_samples"], w["range"])
+    assert sha256_i32(fma) != GOLDEN_CONFIGS["lidar_scan"]["output_sha256"][0]
+
+
+def distance_sequence(points, idx):
+    """test.py:65-81 compute_distance_sequence (float32)."""
+    p = points.astype(np.float32)
+    mind = np.full(len(p), np.inf, np.float32)
+    out = np.zeros(len(idx), np.float32)
+    out[0] = np.inf
+    for i in range(1, len(idx)):
+        d = np.sum((p - p[idx[i - 1]]) ** 2, axis=1)
+        mind = np.minimum(mind, d)
+        out[i] = mind.max()
+    return out
+
+
+@pytest.mark.parametrize("name", ["testpy_100_10", "testpy_1k_100", "testpy_nonuniform_5k_500",
+                                  "granularity_4x16x64", "manual_bbox_16x16x8"])
+def test_testpy_distance_sequence_acceptance(oracle, name):
+    """test.py:125-138: per-step maximum distances of the C++ result within 1e-3
+    of NumPy brute-force FPS, lengths within 1.  Here the oracle's own trace
+    must also equal the recomputed sequence exactly."""
+    case = {c.name: c for c in GOLDEN_CASES}[name]
+    idx, md, _ = oracle.fps_trace(case.points, case.n_samples, case.range, case.blocks)
+    seq = distance_sequence(case.points, idx)
+    assert np.array_equal(md[1:], seq[1:])
+    p = case.points.astype(np.float32)
+    mind = np.full(len(p), np.inf, np.float32)
+    bf = [0]
+    for _ in range(1, case.n_samples):
+        mind = np.minimum(mind, np.sum((p - p[bf[-1]]) ** 2, axis=1))
+        if mind.max() == 0:
+            break
+        bf.append(int(np.argmax(mind)))
+    bfs = distance_sequence(case.points, np.array(bf))
+    k = min(len(bfs), len(seq))
+    assert abs(len(bfs) - len(seq)) <= 1
+    assert np.max(np.abs(bfs[1:k] - seq[1:k])) < 1e-3
+
+
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes"])
+def test_oracle_matches_reference_on_workloads(oracle, wname):
+    from ns_fps_amd.workloads import make_workload
+    g = GOLDEN_CONFIGS[wname]
+    w = make_workload(wname)
+    assert sha256_f32(np.concatenate(w["clouds"])) == g["input_sha256"]
+    clouds = w["clouds"] if wname != "batched_shapes" else w["clouds"][:16]
+    for i, P in enumerate(clouds):
+        got = oracle.fps(P, w["n_samples"], w["range"], w["blocks"])
+        assert len(got) == g["lengths"][i]
+        assert sha256_i32(got) == g["output_sha256"][i]
+
+
+def test_census_counts_first_pass_and_candidates(oracle):
+    case = {c.name: c for c in GOLDEN_CASES}["testpy_1k_100"]
+    _, c = oracle.fps(case.points, case.n_samples, case.range, census=True)
+    assert c.first_pass_points == len(case.points)
+    assert c.iterations == case.n_samples - 1
+    assert c.cand_points >= c.iterations  # the sample's own bucket at least
+    assert c.alg_bytes() == 16 * (c.cand_points + c.first_pass_points) + 8 * (
+        c.cand_leaves + c.first_pass_leaves)
