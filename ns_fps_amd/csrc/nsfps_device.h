@@ -137,6 +137,31 @@ __device__ __forceinline__ uint32_t rdlane(uint32_t v, uint32_t l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
 }
 
+// Maximum of a u32 over the 64 lanes (all lanes must be active); the result
+// is wave-uniform.  Rows of 16 lanes by DPP, then the four row maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp<kDppQuad1032>(v));
+  v = max(v, dpp<kDppQuad2301>(v));
+  v = max(v, dpp<kDppHalfMirror>(v));
+  v = max(v, dpp<kDppMirror>(v));
+  return max(max(rdlane(v, 0), rdlane(v, 16)), max(rdlane(v, 32), rdlane(v, 48)));
+}
+
+// Lane holding the largest key (hi << 32 | lo) among active lanes, or 64 when
+// none is active; mhi receives the largest hi.  Keys of active lanes are
+// unique, so the winner is unique.  The common case reduces hi only; lo is
+// reduced among the lanes tied on hi.
+__device__ __forceinline__ uint32_t key_winner(uint32_t hi, uint32_t lo, bool act, uint32_t &mhi) {
+  const uint32_t m = wave_max_u32(act ? hi : 0u);
+  uint64_t t = __ballot(act && hi == m);
+  if (__popcll(t) > 1) {
+    const uint32_t l = wave_max_u32((act && hi == m) ? lo : 0u);
+    t = __ballot(act && hi == m && lo == l);
+  }
+  mhi = m;
+  return t ? (uint32_t)__ffsll((long long)t) - 1 : 64u;
+}
+
 // Maximum of a u64 over the 64 lanes (all lanes must be active); the result
 // is wave-uniform.  Rows of 16 lanes by DPP, then the four row maxima.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {

@@ -320,8 +320,7 @@ LdsPlan plan_lds(const CloudDev &c) {
   pl.m1 = take(((nl1 + 31) / 32) * 4);
   pl.dl1 = take((uint64_t)nl1 * 4);
   pl.m2 = take(8);
-  pl.dl2 = take(64 * 4);
-  const uint32_t slot_bytes = kFan * (8 + 16);
+  const uint32_t slot_bytes = kFan * (8 + 16) + 8;  // staging entries + candidate mask
   pl.ctab = kNone;
   if (!c.padded) {
     uint64_t need = ((uint64_t)c.r.T + 1) * 8;
@@ -332,8 +331,9 @@ LdsPlan plan_lds(const CloudDev &c) {
     pl.l1lo = take((uint64_t)nl1 * 16);
     pl.l1hi = take((uint64_t)nl1 * 16);
   }
-  uint32_t room = kLdsBudget > off + 64 ? kLdsBudget - off - 64 : 0;
+  uint32_t room = kLdsBudget > off + 96 ? kLdsBudget - off - 96 : 0;
   pl.dcap = std::min<uint32_t>(64, room / slot_bytes);
+  pl.cm = take((uint64_t)std::max<uint32_t>(pl.dcap, 1) * 8);
   pl.sk = take((uint64_t)pl.dcap * kFan * 8);
   pl.sp = take((uint64_t)pl.dcap * kFan * 16);
   pl.total = (off + 255u) & ~255u;
@@ -479,7 +479,9 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   HIP_TRY(hipEventRecord(a.ev[4], st));
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
   if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
-  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, st));
+  const char *lt = getenv("NSFPS_LATE_THREADS");
+  const uint32_t late_threads = (lt && atoi(lt) == 1024) ? 1024u : kLateThreads;
+  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, late_threads, st));
   HIP_TRY(hipEventRecord(a.ev[2], st));
   std::vector<uint32_t> lens(plans.size());
   for (size_t i = 0; i < plans.size(); ++i)

@@ -16,7 +16,8 @@ constexpr uint32_t kFan = 64;
 constexpr uint32_t kFineBits = 9;
 // Level-1 nodes the single-workgroup loop can hold (level 2 then fits one wave).
 constexpr uint32_t kMaxL1 = 4096;
-// Threads of the single-workgroup loop (one cube cell per thread per chunk).
+// Threads of the single-workgroup loop (one cube cell per thread per chunk):
+// 512 by default, 1024 selectable.
 constexpr uint32_t kLateThreads = 512;
 // Candidate leaves flattened into LDS per round.
 constexpr uint32_t kCandCap = 1024;
@@ -49,7 +50,8 @@ struct LdsPlan {
   uint32_t cand;          // kCandCap x 3 u32: leaf, first slot, count
   uint32_t slot;          // u32 per level-1 node: staging slot or kNone
   uint32_t m1, dl1;       // dirty level-1 bitmask / list
-  uint32_t m2, dl2;       // dirty level-2 bitmask / list
+  uint32_t m2;            // dirty level-2 bitmask (64 bits)
+  uint32_t cm;            // per staging slot: 64-bit mask of candidate children
   uint32_t sk, sp;        // staging: dcap x 64 keys (u64) / positions (float4)
   uint32_t dcap;          // staging slots (level-1 nodes per fast iteration)
   uint32_t total;         // bytes

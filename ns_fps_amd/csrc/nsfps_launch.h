@@ -41,7 +41,7 @@ hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStre
 // sampling
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
 hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t lds_bytes,
-                            bool profile, hipStream_t st);
+                            bool profile, uint32_t threads, hipStream_t st);
 constexpr uint32_t kProfWords = 24;
 
 }  // namespace nsfps
