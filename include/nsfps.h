@@ -61,7 +61,7 @@ typedef struct {
   double build_ms;   /* device time: cell keys, sorts, leaves (hipEvents) */
   double sample_ms;  /* device time: the sampling loop (hipEvents) */
   double wide_ms;    /* part of sample_ms spent in grid-wide iterations */
-  double late_ms;    /* the single-workgroup loop kernel alone */
+  double late_ms;    /* the single-workgroup loop kernel alone, or all rounds of runs */
   double device_ms;  /* build_ms + sample_ms */
   double e2e_ms;     /* host wall time of the whole call incl. copies */
   uint64_t n_points;
@@ -71,6 +71,9 @@ typedef struct {
   uint64_t samples;     /* samples produced (sum over clouds) */
   uint32_t padded;      /* 1 when the single cloud used the padded cell layout */
   uint32_t lds_bytes;   /* dynamic LDS of the single-workgroup loop */
+  uint64_t rounds;      /* speculative-run rounds (max over clouds; 0 for the tree loop) */
+  uint32_t engine;      /* 1: speculative runs, 0: grid-wide steps + tree loop */
+  uint32_t reserved;
 } nsfps_stats;
 
 /* Library constants mirrored from src/yuezu_fps.h:19-50. */

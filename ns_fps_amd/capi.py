@@ -37,7 +37,9 @@ class Stats(ctypes.Structure):
                 ("e2e_ms", ctypes.c_double), ("n_points", ctypes.c_uint64),
                 ("n_clouds", ctypes.c_uint64), ("n_leaves", ctypes.c_uint64),
                 ("wide_iters", ctypes.c_uint64), ("samples", ctypes.c_uint64),
-                ("padded", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32)]
+                ("padded", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32),
+                ("rounds", ctypes.c_uint64), ("engine", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

@@ -57,6 +57,24 @@ __device__ __forceinline__ uint32_t bucket_of(const RangeDev &r, const uint32_t 
   return r.bijective ? code : code % r.T;
 }
 
+// Morton code of a cell from the concatenated LUTs.
+__device__ __forceinline__ uint32_t cell_code(const RangeDev &r, const uint32_t *lut, uint32_t ix,
+                                              uint32_t iy, uint32_t iz) {
+  return lut[r.lut_off[0] + ix] | lut[r.lut_off[1] + iy] | lut[r.lut_off[2] + iz];
+}
+
+// Axis value whose Morton bits are `part`: the LUT is increasing, so a binary
+// search finds it; kNone when no value has exactly these bits.
+__device__ __forceinline__ uint32_t lut_inverse(const uint32_t *lut, uint32_t size, uint32_t part) {
+  uint32_t lo = 0, hi = size;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (lut[mid] < part) lo = mid + 1;
+    else hi = mid;
+  }
+  return (lo < size && lut[lo] == part) ? lo : 0xffffffffu;
+}
+
 // squared_distance (src/yuezu_fps.cpp:205-209): ((dx*dx + dy*dy) + dz*dz).
 __device__ __forceinline__ float sqdist(float px, float py, float pz, float qx, float qy,
                                         float qz) {
@@ -104,6 +122,27 @@ __device__ __forceinline__ Cube make_cube(const RangeDev &r, float D, float qx, 
     cb.hi[a] = hi > (int)r.blocks[a] - 1 ? (int)r.blocks[a] - 1 : hi;
   }
   return cb;
+}
+
+// When bucket = code % T is not one-to-one, several cells share a bucket.  A
+// cube cell stands for its bucket only if no cell of the cube has a smaller
+// code of the same bucket, so that every bucket of the cube is visited once
+// (the reference visits each bucket of its code list once,
+// src/yuezu_fps.cpp:573-597).
+__device__ __forceinline__ bool bucket_first_in_cube(const RangeDev &r, const uint32_t *lut,
+                                                     uint32_t code, const Cube &cb) {
+  const uint32_t sz[3] = {r.lut_off[1] - r.lut_off[0], r.lut_off[2] - r.lut_off[1],
+                          r.lut_total - r.lut_off[2]};
+  for (uint32_t k = code % r.T; k < code; k += r.T) {
+    bool inside = true;
+    for (int a = 0; a < 3 && inside; ++a) {
+      const uint32_t mask = lut[r.lut_off[a] + sz[a] - 1];
+      const uint32_t v = lut_inverse(lut + r.lut_off[a], sz[a], k & mask);
+      inside = v != 0xffffffffu && (int)v >= cb.lo[a] && (int)v <= cb.hi[a];
+    }
+    if (inside) return false;
+  }
+  return true;
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
@@ -189,6 +228,32 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   const uint32_t row = lane_id() >> 4;
   v += (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
   return v;
+}
+
+// Block-wide exclusive scan of one value per thread with a single barrier:
+// every wave reads all wave totals.  Consecutive calls must alternate wsum
+// buffers (kLW entries each) unless a barrier separates them.
+template <uint32_t kLW>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum, uint32_t *total) {
+  const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
+  const uint32_t x = wave_incl_scan(v);
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kLW; ++w) {
+    uint32_t t = wsum[w];
+    before += w < wave ? t : 0u;
+    all += t;
+  }
+  *total = all;
+  return x - v + before;
+}
+
+// Lanes below this one whose bit is set in mask.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
 // Lane holding the wave maximum (keys are unique among active lanes).

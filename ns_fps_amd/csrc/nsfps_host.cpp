@@ -62,6 +62,7 @@ struct HostRange {
   nsfps_range prim;
   nsfps_range_info info;
   std::vector<uint32_t> lut[3];
+  std::vector<float> cube_t;  // 3 x kCubeTab half-width thresholds
   RangeDev dev;
 };
 
@@ -77,6 +78,38 @@ nsfps_status check_range(const nsfps_range &r) {
     if (v > 1024) return fail(NSFPS_EUNSUPPORTED, "block counts above 1024 per axis are not supported");
   }
   return NSFPS_OK;
+}
+
+// Cube half-width of get_morton_codes_in_range (src/yuezu_fps.cpp:564-570)
+// for one axis, evaluated like the device's cube_half: IEEE sqrtf and
+// division, ceil, clamped to the grid.
+uint32_t cube_half_host(float D, float bs, uint32_t blocks) {
+  volatile float rad = std::sqrt(D < 0.0f ? 0.0f : D);
+  volatile float q = rad / bs;
+  float f = std::ceil(q);
+  if (!(f < (float)blocks)) return blocks;
+  return (uint32_t)f;
+}
+
+// t[a * kCubeTab + k] = smallest D >= 0 whose half-width on axis a is >= k
+// (k = 1..blocks; +inf if none).  The half-width is monotone in D, so a
+// non-increasing sequence of D walks down this table.
+void cube_thresholds(const RangeDev &d, std::vector<float> &t) {
+  t.assign(3 * kCubeTab, INFINITY);
+  for (int a = 0; a < 3; ++a) {
+    t[a * kCubeTab] = 0.0f;
+    for (uint32_t k = 1; k <= d.blocks[a]; ++k) {
+      uint32_t lo = 0, hi = 0x7f800000u;  // [0, +inf]
+      auto val = [](uint32_t u) { float f; memcpy(&f, &u, 4); return f; };
+      if (cube_half_host(val(hi), d.bsize[a], d.blocks[a]) < k) continue;
+      while (lo < hi) {
+        uint32_t mid = lo + (hi - lo) / 2;
+        if (cube_half_host(val(mid), d.bsize[a], d.blocks[a]) >= k) hi = mid;
+        else lo = mid + 1;
+      }
+      t[a * kCubeTab + k] = val(lo);
+    }
+  }
 }
 
 // make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
@@ -131,6 +164,7 @@ void derive(const nsfps_range &r, HostRange &h) {
   d.lut_total = off;
   d.T = (uint32_t)h.info.total_blocks;
   d.bijective = bij ? 1u : 0u;
+  cube_thresholds(d, h.cube_t);
 }
 
 void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) {
@@ -226,6 +260,7 @@ struct CloudPlan {
   // build-time buffers
   float *d_xyz_stage = nullptr;
   uint32_t *d_lut = nullptr, *d_counts = nullptr, *d_lc = nullptr;
+  float *d_cube_t = nullptr;
   uint32_t *d_small = nullptr;  // [0] non-finite flag, [1] max occupancy, [2] phys0
   uint2 *d_cell_info = nullptr;
 };
@@ -280,6 +315,15 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   p.d_small = bp.take<uint32_t>(4);
   c.out = bp.take<int32_t>(p.m);
   c.prof = bp.take<uint64_t>(kProfWords);
+  c.rs = bp.take<RunState>(1);
+  c.hist = bp.take<uint32_t>((size_t)kHists * kHistBins);
+  c.pick_p = bp.take<float4>(kListCap);
+  c.pick_c = bp.take<uint2>(kListCap);
+  c.list_p = bp.take<float4>(kListCap);
+  c.list_r = bp.take<uint2>(kListCap);
+  c.list_c = bp.take<uint32_t>(kListCap);
+  p.d_cube_t = bp.take<float>(3 * kCubeTab);
+  c.cube_t = p.d_cube_t;
   c.lut = p.d_lut;
   c.n = n;
   c.m = p.m;
@@ -348,6 +392,8 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   std::vector<uint32_t> lut;
   for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
   HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(p.d_cube_t, p.rng.cube_t.data(), p.rng.cube_t.size() * 4,
+                         hipMemcpyHostToDevice, st));
   const float *xyz = p.d_xyz_in;
   if (p.h_xyz) {
     HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)n * 12, hipMemcpyHostToDevice, st));
@@ -431,6 +477,53 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
   return ms;
 }
 
+// Speculative-run rounds until every cloud is done.  Rounds are enqueued in
+// growing batches; a round of a finished cloud returns at once.  Between
+// batches the host reads each cloud's done flag, sample count and list
+// overflow flag.
+nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds, hipStream_t st,
+                        uint64_t *rounds_out) {
+  uint32_t max_nl1 = 1;
+  for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
+  const uint32_t nc = (uint32_t)plans.size();
+  HIP_TRY(launch_runs_init(d_clouds, nc, st));
+  struct Probe {
+    uint32_t done, iter;
+    RunState rs;
+  };
+  std::vector<Probe> pr(nc);
+  uint64_t last_samples = 0, enqueued = 0;
+  uint32_t batch = 4, stalled = 0;
+  while (true) {
+    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, st));
+    enqueued += batch;
+    for (uint32_t i = 0; i < nc; ++i) {
+      const CloudDev &c = plans[i].dev;
+      HIP_TRY(hipMemcpyAsync(&pr[i].done, c.done, 4, hipMemcpyDeviceToHost, st));
+      HIP_TRY(hipMemcpyAsync(&pr[i].iter, c.iter, 4, hipMemcpyDeviceToHost, st));
+      HIP_TRY(hipMemcpyAsync(&pr[i].rs, c.rs, sizeof(RunState), hipMemcpyDeviceToHost, st));
+    }
+    HIP_TRY(hipStreamSynchronize(st));
+    bool all = true;
+    uint64_t samples = 0, rounds = 0;
+    for (auto &q : pr) {
+      if (q.rs.err) return fail(NSFPS_EDEVICE, "internal: speculative list overflow");
+      all = all && q.done;
+      samples += q.iter;
+      rounds = std::max<uint64_t>(rounds, q.rs.rounds);
+    }
+    *rounds_out = rounds;
+    if (all) break;
+    // every round takes at least one sample of every unfinished cloud
+    stalled = samples == last_samples ? stalled + 1 : 0;
+    if (stalled >= 2) return fail(NSFPS_EDEVICE, "internal: sampling made no progress");
+    last_samples = samples;
+    batch = std::min<uint32_t>(batch * 2, 64);
+  }
+  (void)enqueued;
+  return NSFPS_OK;
+}
+
 // Builds every cloud, then samples: grid-wide steps for the first iterations
 // of a single cloud, then one single-workgroup loop launch for all clouds.
 nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, bool out_on_host,
@@ -468,20 +561,37 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   HIP_TRY(hipEventRecord(a.ev[1], st));
   std::vector<CloudDev> devs;
   for (auto &p : plans) devs.push_back(p.dev);
-  if (plans.size() == 1) {
-    uint32_t e = wide_iters_for(plans[0]);
-    wide_total = e;
-    if (e) HIP_TRY(launch_wide_steps(plans[0].dev, e, std::max<uint32_t>(1, plans[0].dev.nl1), st));
-  }
-  HIP_TRY(hipEventRecord(a.ev[3], st));
-  HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
-                         hipMemcpyHostToDevice, st));
-  HIP_TRY(hipEventRecord(a.ev[4], st));
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
-  if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
-  const char *lt = getenv("NSFPS_LATE_THREADS");
-  const uint32_t late_threads = (lt && atoi(lt) == 1024) ? 1024u : kLateThreads;
-  HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, late_threads, st));
+  bool runs = true;
+  for (auto &p : plans) runs = runs && p.rng.dev.bijective;
+  const char *eng = getenv("NSFPS_ENGINE");
+  if (eng && strcmp(eng, "tree") == 0) runs = false;
+  uint64_t rounds = 0;
+  if (runs) {
+    HIP_TRY(hipEventRecord(a.ev[3], st));
+    HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipEventRecord(a.ev[4], st));
+    rc = run_rounds(plans, d_clouds, st, &rounds);
+    if (rc) return rc;
+    memset(g_prof, 0, sizeof(g_prof));
+  } else {
+    if (plans.size() == 1) {
+      uint32_t e = wide_iters_for(plans[0]);
+      wide_total = e;
+      if (e)
+        HIP_TRY(launch_wide_steps(plans[0].dev, e, std::max<uint32_t>(1, plans[0].dev.nl1), st));
+    }
+    HIP_TRY(hipEventRecord(a.ev[3], st));
+    HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipEventRecord(a.ev[4], st));
+    if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
+    const char *lt = getenv("NSFPS_LATE_THREADS");
+    const uint32_t late_threads = (lt && atoi(lt) == 1024) ? 1024u : kLateThreads;
+    HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, late_threads,
+                             st));
+  }
   HIP_TRY(hipEventRecord(a.ev[2], st));
   std::vector<uint32_t> lens(plans.size());
   for (size_t i = 0; i < plans.size(); ++i)
@@ -495,7 +605,7 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
       HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
                              hipMemcpyDeviceToHost, st));
   }
-  if (profile)
+  if (profile && !runs)
     HIP_TRY(hipMemcpyAsync(g_prof, plans[0].dev.prof, sizeof(g_prof), hipMemcpyDeviceToHost, st));
   else
     memset(g_prof, 0, sizeof(g_prof));
@@ -514,7 +624,9 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   S.wide_iters = wide_total;
   S.samples = samples;
   S.padded = plans.size() == 1 ? plans[0].dev.padded : 0;
-  S.lds_bytes = lds_bytes;
+  S.lds_bytes = runs ? 0 : lds_bytes;
+  S.rounds = rounds;
+  S.engine = runs ? 1u : 0u;
   return NSFPS_OK;
 }
 

@@ -24,6 +24,15 @@ constexpr uint32_t kCandCap = 1024;
 // Dynamic LDS budget of the single-workgroup loop (gfx950: 160 KiB per CU).
 constexpr uint32_t kLdsBudget = 160 * 1024 - 1024;
 constexpr uint32_t kNone = 0xffffffffu;
+// Speculative-run engine: list entries (one per thread of the run kernel; also
+// the most picks one run can accept), bins per key histogram, histograms per
+// round (fine and coarse from the update pass, then two refinement passes).
+constexpr uint32_t kListCap = 1024;
+constexpr uint32_t kHistBins = 4096;
+constexpr uint32_t kHists = 4;
+constexpr uint32_t kRefinePasses = 2;
+// Entries per axis of the cube half-width threshold table (blocks <= 1024).
+constexpr uint32_t kCubeTab = 1025;
 
 // Range values the kernels need, all derived on the host exactly as the
 // reference derives them (src/yuezu_fps.cpp:7-11, 136-161, 170-193).
@@ -55,6 +64,21 @@ struct LdsPlan {
   uint32_t sk, sp;        // staging: dcap x 64 keys (u64) / positions (float4)
   uint32_t dcap;          // staging slots (level-1 nodes per fast iteration)
   uint32_t total;         // bytes
+};
+
+// State of the speculative-run engine of one cloud, carried between the
+// kernels of a round and from one round to the next.
+struct RunState {
+  uint64_t kref0;     // every key is <= kref0 when the update pass runs
+  uint64_t bkey;      // list threshold chosen by the selection
+  uint32_t s0;        // bin shift of the fine histogram of the update pass
+  uint32_t s0_next;   // bin shift proposed for the next round
+  uint32_t npicks;    // picks of the last run (applied by the next update pass)
+  uint32_t nlist;     // list entries gathered this round
+  uint32_t hc[3];     // cube half-width per axis at the latest pick
+  uint32_t rounds;    // rounds that ran (statistics)
+  uint32_t err;       // set if a list overflowed (internal error)
+  uint32_t pad;
 };
 
 // Everything one cloud's kernels touch.  Device pointers; passed by value to
@@ -90,6 +114,15 @@ struct CloudDev {
   uint32_t *counter;          // arrival counter of the grid-wide step
   int32_t *out;               // m entries
   uint64_t *prof;             // loop phase clocks / counters, or null
+  // speculative-run engine
+  RunState *rs;
+  uint32_t *hist;             // kHists x kHistBins
+  float4 *pick_p;             // kListCap: x, y, z, D of each pick of a run
+  uint2 *pick_c;              // kListCap: cube lo / hi cells (10 bits per axis)
+  float4 *list_p;             // kListCap: x, y, z, min distance
+  uint2 *list_r;              // kListCap: logical rank, input row
+  uint32_t *list_c;           // kListCap: cell (10 bits per axis)
+  const float *cube_t;        // 3 x kCubeTab: smallest D giving half-width k
 };
 
 // Argmax key: larger min-distance wins, equal distances go to the smaller

@@ -328,26 +328,6 @@ __device__ __forceinline__ Lds carve(unsigned char *base, const LdsPlan &pl) {
   return s;
 }
 
-// Block-wide exclusive scan of one value per thread with a single barrier:
-// every wave reads all wave totals.  Consecutive calls must alternate wsum
-// buffers (kLW entries each).
-template <uint32_t kLW>
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum, uint32_t *total) {
-  const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
-  const uint32_t x = wave_incl_scan(v);
-  if (lane == 63) wsum[wave] = x;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-#pragma unroll
-  for (uint32_t w = 0; w < kLW; ++w) {
-    uint32_t t = wsum[w];
-    before += w < wave ? t : 0u;
-    all += t;
-  }
-  *total = all;
-  return x - v + before;
-}
-
 // First marker of level-1 node g appends it to the dirty list and gives it a
 // staging slot (when one is left).
 __device__ __forceinline__ void mark_dirty(const Lds &s, uint32_t *count, uint32_t dcap,
@@ -544,9 +524,10 @@ __global__ __launch_bounds__(NT) void k_late_loop(const CloudDev *__restrict__ c
       uint32_t cnt = 0;
       if (t < ncell) {
         const uint32_t ix = t % ex, iy = (t / ex) % ey, iz = t / (ex * ey);
-        const uint32_t b = bucket_of(c.r, s.lut, (uint32_t)cb.lo[0] + ix,
-                                     (uint32_t)cb.lo[1] + iy, (uint32_t)cb.lo[2] + iz);
-        cl = cell_leaves(c, s, b);
+        const uint32_t code = cell_code(c.r, s.lut, (uint32_t)cb.lo[0] + ix,
+                                        (uint32_t)cb.lo[1] + iy, (uint32_t)cb.lo[2] + iz);
+        const bool rep = c.r.bijective || bucket_first_in_cube(c.r, s.lut, code, cb);
+        if (rep) cl = cell_leaves(c, s, c.r.bijective ? code : code % c.r.T);
         for (uint32_t g = cl.la / kFan; cl.la < cl.lb && g <= (cl.lb - 1) / kFan; ++g) {
           if (node_pruned(s, g, q.x, q.y, q.z)) continue;
           cnt += min(cl.lb, (g + 1) * kFan) - max(cl.la, g * kFan);

@@ -239,6 +239,8 @@ py::dict last_stats_py() {
   d["n_leaves"] = s.n_leaves;
   d["wide_iters"] = s.wide_iters;
   d["samples"] = s.samples;
+  d["rounds"] = s.rounds;
+  d["engine"] = s.engine ? "runs" : "tree";
   return d;
 }
 

@@ -123,13 +123,20 @@ def test_device_pointer_entry_point(lib):
     assert np.array_equal(got, case.expected)
 
 
+TREE = {"NSFPS_ENGINE": "tree"}
+
+
 @pytest.mark.parametrize("env", [
-    {"NSFPS_WIDE_ITERS": "0"}, {"NSFPS_WIDE_ITERS": "1"}, {"NSFPS_WIDE_ITERS": "37"},
-    {"NSFPS_WIDE_ITERS": "100000"}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_PROFILE": "1"},
-])
+    {}, {"NSFPS_NO_PADDED": "1"},
+    {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
+    {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
+    {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
+    {**TREE, "NSFPS_LATE_THREADS": "1024"},
+], ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()) or "runs")
 def test_schedule_and_layout_do_not_change_results(yf, env, monkeypatch):
-    """Where the grid-wide phase hands over to the single-workgroup loop, the
-    padded or table layout and the profiling build are result-invariant."""
+    """The engine (speculative runs, or grid-wide steps + single-workgroup
+    tree loop), where the grid-wide phase hands over, the padded or table
+    layout and the profiling build are result-invariant."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for name in ["testpy_10k_1k", "lattice_ties_16", "granularity_64x64x64", "boundary_aligned"]:
@@ -168,3 +175,67 @@ def test_full_size_properties(yf):
     assert np.array_equal(a, b)
     assert a[0] == 0 and len(np.unique(a)) == len(a) == w["n_samples"]
     assert a.min() >= 0 and a.max() < len(w["clouds"][0])
+
+
+def test_engine_choice(yf, monkeypatch):
+    """Speculative runs on one-to-one bucket grids, the tree loop otherwise or
+    when asked for."""
+    by = {c.name: c for c in GOLDEN_CASES}
+    run_module(yf, by["granularity_32x32x32"])
+    st = yf.last_stats()
+    assert st["engine"] == "runs" and st["rounds"] >= 1
+    run_module(yf, by["general_10x10x10"])
+    assert yf.last_stats()["engine"] == "tree"
+    monkeypatch.setenv("NSFPS_ENGINE", "tree")
+    run_module(yf, by["granularity_32x32x32"])
+    assert yf.last_stats()["engine"] == "tree"
+
+
+@pytest.mark.parametrize("wname", ["quickstart", "lidar_scan"])
+def test_workload_on_tree_engine(yf, lib, wname, monkeypatch):
+    monkeypatch.setenv("NSFPS_ENGINE", "tree")
+    w, g, outs = run_workload(yf, lib, wname)
+    assert yf.last_stats()["engine"] == "tree"
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
+def lattice(k, lo=0.0, hi=1.0):
+    g = np.linspace(lo, hi, k, dtype=np.float32)
+    return np.stack(np.meshgrid(g, g, g, indexing="ij"), -1).reshape(-1, 3).astype(np.float32)
+
+
+@pytest.mark.parametrize("name,pts,m,rng", [
+    # thousands of exactly equal distances: the threshold selection refines
+    # down to logical ranks or falls back to the maximum key
+    ("lattice40", lattice(40), 3000, (-0.01, 1.01, -0.01, 1.01, -0.01, 1.01, 16, 16, 16)),
+    ("lattice32_fine", lattice(32), 5000, (-0.01, 1.01, -0.01, 1.01, -0.01, 1.01, 64, 64, 64)),
+    # 2,000 distinct points, each 30 times
+    ("dup30", np.repeat(np.random.RandomState(11).rand(2000, 3).astype(np.float32), 30, axis=0),
+     2500, (0.0, 1.0, 0.0, 1.0, 0.0, 1.0, 32, 32, 32)),
+    # two far clusters: the threshold window must move far between rounds
+    ("two_clusters", np.concatenate([np.random.RandomState(12).randn(30000, 3) * 0.01,
+                                     np.random.RandomState(13).randn(30000, 3) * 0.01 + 5.0]
+                                    ).astype(np.float32),
+     4000, (-1.0, 6.0, -1.0, 6.0, -1.0, 6.0, 32, 32, 32)),
+], ids=lambda v: v if isinstance(v, str) else "")
+def test_tie_heavy_clouds_match_oracle(yf, oracle, name, pts, m, rng):
+    got = yf.fps(pts, m, yf.make_range(*rng))
+    assert yf.last_stats()["engine"] == "runs"
+    want = oracle.fps(pts, m, rng)
+    assert len(got) == len(want)
+    assert np.array_equal(got, want), name
+
+
+def test_shared_buckets_visited_once(yf):
+    """Grids whose block counts are not powers of two map several cells to one
+    bucket; each bucket of a cube must be updated by one wave only (two waves
+    on one leaf could pair a new leaf key with an old winner).  Repeated after
+    a large call so that the workspace holds stale data."""
+    from ns_fps_amd.workloads import make_workload
+    w = make_workload("lidar_scan")
+    yf.fps(w["clouds"][0], w["n_samples"], yf.make_range(*w["range"]))
+    cases = [c for c in GOLDEN_CASES if c.name.startswith("general_")]
+    assert cases
+    for rep in range(3):
+        for case in cases:
+            assert np.array_equal(run_module(yf, case), case.expected), (case.name, rep)
