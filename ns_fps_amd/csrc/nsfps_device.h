@@ -158,6 +158,14 @@ __device__ __forceinline__ uint32_t dpp_or0(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
 }
 
+// Pure DPP move (old value undefined): lets the compiler fold it into the
+// consuming VALU op.  Only used with controls that read a valid lane for
+// every lane (quad permutes, row mirrors), so bound_ctrl never applies.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
 constexpr int kDppQuad1032 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int kDppQuad2301 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;
@@ -176,14 +184,49 @@ __device__ __forceinline__ uint32_t rdlane(uint32_t v, uint32_t l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
 }
 
+// Maximum of a u32 over each row of 16 lanes, in every lane of the row (all
+// lanes must be active).
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, dpp_mov<kDppQuad1032>(v));
+  v = max(v, dpp_mov<kDppQuad2301>(v));
+  v = max(v, dpp_mov<kDppHalfMirror>(v));
+  v = max(v, dpp_mov<kDppMirror>(v));
+  return v;
+}
+
 // Maximum of a u32 over the 64 lanes (all lanes must be active); the result
-// is wave-uniform.  Rows of 16 lanes by DPP, then the four row maxima.
+// is wave-uniform: the four row maxima.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, dpp<kDppQuad1032>(v));
-  v = max(v, dpp<kDppQuad2301>(v));
-  v = max(v, dpp<kDppHalfMirror>(v));
-  v = max(v, dpp<kDppMirror>(v));
+  v = row_max_u32(v);
   return max(max(rdlane(v, 0), rdlane(v, 16)), max(rdlane(v, 32), rdlane(v, 48)));
+}
+
+// Scalar max of two wave-uniform values, kept on the scalar unit (a vector
+// max here would put the result in a VGPR and every later test on it would
+// be a vector compare feeding a branch).
+__device__ __forceinline__ uint32_t smax_u32(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("s_max_u32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b) : "scc");
+  return r;
+}
+
+// wave_max_u32 with the result in a scalar register.
+__device__ __forceinline__ uint32_t wave_max_u32_s(uint32_t v) {
+  v = row_max_u32(v);
+  return smax_u32(smax_u32(rdlane(v, 0), rdlane(v, 16)), smax_u32(rdlane(v, 32), rdlane(v, 48)));
+}
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+// Minimum of a u32 over the 64 lanes (all lanes must be active); wave-uniform.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp_mov<kDppQuad1032>(v));
+  v = min(v, dpp_mov<kDppQuad2301>(v));
+  v = min(v, dpp_mov<kDppHalfMirror>(v));
+  v = min(v, dpp_mov<kDppMirror>(v));
+  return min(min(rdlane(v, 0), rdlane(v, 16)), min(rdlane(v, 32), rdlane(v, 48)));
 }
 
 // Lane holding the largest key (hi << 32 | lo) among active lanes, or 64 when

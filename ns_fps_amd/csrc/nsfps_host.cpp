@@ -482,7 +482,7 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
 // batches the host reads each cloud's done flag, sample count and list
 // overflow flag.
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds, hipStream_t st,
-                        uint64_t *rounds_out) {
+                        bool profile, uint64_t *rounds_out) {
   uint32_t max_nl1 = 1;
   for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
   const uint32_t nc = (uint32_t)plans.size();
@@ -495,7 +495,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0;
   while (true) {
-    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, st));
+    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, profile, st));
     enqueued += batch;
     for (uint32_t i = 0; i < nc; ++i) {
       const CloudDev &c = plans[i].dev;
@@ -572,9 +572,9 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
     HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                            hipMemcpyHostToDevice, st));
     HIP_TRY(hipEventRecord(a.ev[4], st));
-    rc = run_rounds(plans, d_clouds, st, &rounds);
+    if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
+    rc = run_rounds(plans, d_clouds, st, profile, &rounds);
     if (rc) return rc;
-    memset(g_prof, 0, sizeof(g_prof));
   } else {
     if (plans.size() == 1) {
       uint32_t e = wide_iters_for(plans[0]);
@@ -605,7 +605,7 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
       HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
                              hipMemcpyDeviceToHost, st));
   }
-  if (profile && !runs)
+  if (profile)
     HIP_TRY(hipMemcpyAsync(g_prof, plans[0].dev.prof, sizeof(g_prof), hipMemcpyDeviceToHost, st));
   else
     memset(g_prof, 0, sizeof(g_prof));

@@ -408,101 +408,421 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 
 // ---------------------------------------------------------------- the run
 
-// One workgroup per cloud, list entry tid in thread tid.  Per sample: every
-// wave finds its maximum key, the winners meet in LDS (one barrier), every
-// wave reads all of them and agrees on the block maximum.
-__global__ __launch_bounds__(kListCap) void k_run(const CloudDev *__restrict__ clouds) {
+// One workgroup per cloud, four waves.  Waves 1-3 own the list (kOwnSlots
+// entries per lane), sorted into 64 coarse spatial groups so that the 64
+// entries of one (wave, slot) span a small box of cells.  Wave 0 samples.
+//
+// The threshold argument is applied once more inside the list: a hot
+// threshold H leaves at most kHot entries at or above it; wave 0 takes a copy
+// of them, one per lane, and samples from them alone -- no barrier, no LDS
+// exchange per sample -- while their maximum key stays >= max(H, B).  Every
+// sample is published in LDS as it is taken, and waves 1-3 apply it to their
+// entries meanwhile (a per-(wave, slot) cell box test skips most of them; the
+// originals of the hot copies get the same updates, min() being idempotent),
+// so when the hot run ends every entry is exact and the next hot set can be
+// chosen.  The run ends when no entry is >= B.
+constexpr uint32_t kRunThreads = 256;
+constexpr uint32_t kRunWaves = kRunThreads / 64;
+constexpr uint32_t kOwnSlots = 6;
+constexpr uint32_t kHot = 64;
+constexpr uint32_t kSelBins = 256;
+constexpr uint32_t kPubDone = 0x10000u;  // flag in the published sample count
+constexpr uint32_t kLoadSlots = kListCap / kRunThreads;
+static_assert(3 * 64 * kOwnSlots >= kListCap, "owner lanes hold the list");
+
+// Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
+// rounds into the cloud's profile words) when PROF is set.
+enum : uint32_t {
+  kRpLoad = 0, kRpSelect, kRpGather, kRpHot, kRpDrain, kRpTail,
+  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpSelPasses, kRpWords = 16
+};
+
+__device__ __forceinline__ uint32_t spatial_group(uint32_t cell, uint32_t b0, uint32_t b1,
+                                                  uint32_t b2) {
+  // 4 x 4 x 4 boxes of cells, Morton-ordered
+  const uint32_t gx = ((cell & 1023u) * 4u) / b0, gy = (((cell >> 10) & 1023u) * 4u) / b1,
+                 gz = ((cell >> 20) * 4u) / b2;
+  return (gx & 1u) | ((gy & 1u) << 1) | ((gz & 1u) << 2) | ((gx & 2u) << 2) | ((gy & 2u) << 3) |
+         ((gz & 2u) << 4);
+}
+
+// |cell - qc| <= h on every axis, as (cell - qc + h) <= 2h in unsigned
+// arithmetic; o = h - qc per axis.
+__device__ __forceinline__ bool in_cube_rel(uint32_t cell, uint32_t ox, uint32_t oy, uint32_t oz,
+                                            uint32_t wx, uint32_t wy, uint32_t wz) {
+  return (cell & 1023u) + ox <= wx && ((cell >> 10) & 1023u) + oy <= wy &&
+         (cell >> 20) + oz <= wz;
+}
+
+// Cube corners of a sample: cell qc, half-widths h (10 bits per axis),
+// clipped to the grid.
+__device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b0, uint32_t b1,
+                                             uint32_t b2, uint32_t &lo_c, uint32_t &hi_c) {
+  const uint32_t qcx = qc & 1023u, qcy = (qc >> 10) & 1023u, qcz = qc >> 20;
+  const uint32_t g0 = h & 1023u, g1 = (h >> 10) & 1023u, g2 = h >> 20;
+  lo_c = pack_cell(qcx > g0 ? qcx - g0 : 0u, qcy > g1 ? qcy - g1 : 0u, qcz > g2 ? qcz - g2 : 0u);
+  hi_c = pack_cell(min(qcx + g0, b0 - 1), min(qcy + g1, b1 - 1), min(qcz + g2, b2 - 1));
+}
+
+template <bool PROF>
+__global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
   __shared__ float s_t[3][kCubeTab];
-  __shared__ uint4 s_rec[2][kListCap / 64][2];
+  __shared__ uint4 s_ent[kListCap][2];  // sorted list: {x, y, z, d}, {~rank, row, cell, -}
+  __shared__ uint4 s_hot[kHot][2];      // hot copies, same layout
+  __shared__ uint4 s_pk[kHot][2];       // samples of a hot run: {qx, qy, qz, row}, {cell, h, D, -}
+  __shared__ uint32_t s_cnt[64], s_off[64];
+  __shared__ uint32_t s_hist[kSelBins];
+  __shared__ uint64_t s_wk[kRunWaves];
+  __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
+  __shared__ uint32_t s_misc[8];
+  __shared__ uint32_t s_pub;
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   if (*gptr(c.done)) return;
+  uint64_t pf[kRpWords] = {}, tl = 0;
+  if (PROF) tl = __builtin_amdgcn_s_memtime();
+#define NSFPS_RMARK(ph)                                  \
+  do {                                                   \
+    if (PROF) {                                          \
+      const uint64_t t_ = __builtin_amdgcn_s_memtime();  \
+      pf[ph] += t_ - tl;                                 \
+      tl = t_;                                           \
+    }                                                    \
+  } while (0)
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
+  const uint32_t b0 = c.r.blocks[0], b1 = c.r.blocks[1], b2 = c.r.blocks[2];
 #pragma unroll
   for (int a = 0; a < 3; ++a)
-    for (uint32_t k = tid; k <= c.r.blocks[a]; k += kListCap) s_t[a][k] = gptr(c.cube_t)[a * kCubeTab + k];
+    for (uint32_t k = tid; k <= c.r.blocks[a]; k += kRunThreads)
+      s_t[a][k] = gptr(c.cube_t)[a * kCubeTab + k];
+  if (tid < 64) s_cnt[tid] = 0;
   const uint32_t nlist = min(rs.nlist, kListCap);
   const uint64_t bkey = rs.bkey;
-  const bool act = tid < nlist;
-  float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
-  uint2 er = make_uint2(0u, 0u);
-  uint32_t ec = 0;
-  if (act) {
-    e = gptr(c.list_p)[tid];
-    er = gptr(c.list_r)[tid];
-    ec = gptr(c.list_c)[tid];
-  }
-  const uint32_t ex = ec & 1023u, ey = (ec >> 10) & 1023u, ez = ec >> 20;
-  const uint32_t lo = ~er.x;
-  uint32_t h0 = rs.hc[0], h1 = rs.hc[1], h2 = rs.hc[2];
-  const uint32_t b0 = c.r.blocks[0], b1 = c.r.blocks[1], b2 = c.r.blocks[2];
-  uint32_t it = *gptr(c.iter);
-  const uint32_t m = c.m;
   __syncthreads();
-  float t0 = h0 ? s_t[0][h0] : 0.f, t1 = h1 ? s_t[1][h1] : 0.f, t2 = h2 ? s_t[2][h2] : 0.f;
-  float d = e.w;
-  uint32_t np = 0, par = 0;
-  bool done = false, capped = false;
-  while (true) {
-    if (np == kListCap) {  // cannot happen (every pick is a distinct list entry); stay exact anyway
-      capped = true;
-      break;
-    }
-    const uint32_t hi = act ? __float_as_uint(d) : 0u;
-    uint32_t mh;
-    const uint32_t wl = key_winner(hi, lo, act, mh);
-    if (lane == wl) {
-      s_rec[par][wave][0] = make_uint4(hi, lo, __float_as_uint(e.x), __float_as_uint(e.y));
-      s_rec[par][wave][1] = make_uint4(__float_as_uint(e.z), er.y, ec, 0u);
-    } else if (wl == 64 && lane == 0) {
-      s_rec[par][wave][0] = make_uint4(0u, 0u, 0u, 0u);
-      s_rec[par][wave][1] = make_uint4(0u, 0u, 0u, 0u);
+
+  // ---- list -> LDS in spatial-group order (counting sort)
+  {
+    float4 P[kLoadSlots];
+    uint2 R[kLoadSlots];
+    uint32_t C[kLoadSlots], G[kLoadSlots], K[kLoadSlots];
+#pragma unroll
+    for (uint32_t s = 0; s < kLoadSlots; ++s) {
+      const uint32_t i = s * kRunThreads + tid;
+      if (i < nlist) {
+        P[s] = gptr(c.list_p)[i];
+        R[s] = gptr(c.list_r)[i];
+        C[s] = gptr(c.list_c)[i];
+        G[s] = spatial_group(C[s], b0, b1, b2);
+        K[s] = atomicAdd(&s_cnt[G[s]], 1u);
+      }
     }
     __syncthreads();
-    uint4 r0 = make_uint4(0u, 0u, 0u, 0u), r1 = r0;
-    if (lane < kListCap / 64) {
-      r0 = s_rec[par][lane][0];
-      r1 = s_rec[par][lane][1];
+    if (wave == 0) {
+      const uint32_t v = s_cnt[lane];
+      s_off[lane] = wave_incl_scan(v) - v;
     }
-    uint32_t bh;
-    const uint32_t wv = key_winner(r0.x, r0.y, lane < kListCap / 64, bh);
-    const uint32_t wlo = rdlane(r0.y, wv);
-    const uint64_t wkey = ((uint64_t)bh << 32) | wlo;
-    if (wkey < bkey || wkey == 0) break;  // not provably the global maximum
-    if (bh == 0) {                        // maximum distance 0: src/yuezu_fps.cpp:705-706
+    __syncthreads();
+#pragma unroll
+    for (uint32_t s = 0; s < kLoadSlots; ++s) {
+      const uint32_t i = s * kRunThreads + tid;
+      if (i < nlist) {
+        const uint32_t pos = s_off[G[s]] + K[s];
+        s_ent[pos][0] = make_uint4(__float_as_uint(P[s].x), __float_as_uint(P[s].y),
+                                   __float_as_uint(P[s].z), __float_as_uint(P[s].w));
+        s_ent[pos][1] = make_uint4(~R[s].x, R[s].y, C[s], 0u);
+      }
+    }
+    __syncthreads();
+  }
+  // owned entries: sorted entry g * 64 + lane with group g = 3 * slot + wave - 1;
+  // an empty slot has distance 0 and key 0 and is never live
+  float x[kOwnSlots], y[kOwnSlots], z[kOwnSlots], d[kOwnSlots];
+  uint32_t lo[kOwnSlots], row[kOwnSlots], cc[kOwnSlots];
+  uint32_t blo[kOwnSlots], bhi[kOwnSlots];  // cell box of each (wave, slot), packed corners
+#pragma unroll
+  for (uint32_t s = 0; s < kOwnSlots; ++s) {
+    const uint32_t i = (3 * s + wave - 1) * 64 + lane;
+    const bool v = wave > 0 && i < nlist;
+    uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;
+    if (v) {
+      e0 = s_ent[i][0];
+      e1 = s_ent[i][1];
+    }
+    x[s] = __uint_as_float(e0.x);
+    y[s] = __uint_as_float(e0.y);
+    z[s] = __uint_as_float(e0.z);
+    d[s] = __uint_as_float(e0.w);
+    lo[s] = e1.x;
+    row[s] = e1.y;
+    cc[s] = e1.z;
+    const uint32_t cx = e1.z & 1023u, cy = (e1.z >> 10) & 1023u, cz = e1.z >> 20;
+    blo[s] = pack_cell(wave_min_u32(v ? cx : 1023u), wave_min_u32(v ? cy : 1023u),
+                       wave_min_u32(v ? cz : 1023u));
+    bhi[s] = pack_cell(wave_max_u32(v ? cx : 0u), wave_max_u32(v ? cy : 0u),
+                       wave_max_u32(v ? cz : 0u));
+  }
+  uint32_t h0 = rs.hc[0], h1 = rs.hc[1], h2 = rs.hc[2];
+  uint32_t it = *gptr(c.iter);
+  const uint32_t m = c.m;
+  NSFPS_GLOBAL int32_t *const out = gptr(c.out);
+  NSFPS_GLOBAL float4 *const pick_p = gptr(c.pick_p);
+  NSFPS_GLOBAL uint2 *const pick_c = gptr(c.pick_c);
+  uint32_t np = 0;
+  bool done = false;
+  NSFPS_RMARK(kRpLoad);
+  while (true) {
+    // ---- hot threshold: live entries (key >= B); their maximum and count
+    uint64_t key[kOwnSlots];
+    bool live[kOwnSlots];
+    uint64_t kmx = 0;
+    uint32_t nl = 0;
+#pragma unroll
+    for (uint32_t s = 0; s < kOwnSlots; ++s) {
+      key[s] = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
+      live[s] = lo[s] != 0u && key[s] >= bkey;
+      kmx = live[s] && key[s] > kmx ? key[s] : kmx;
+      nl += (uint32_t)__popcll(__ballot(live[s]));
+    }
+    kmx = wave_max_u64(kmx);
+    if (lane == 0) {
+      s_wk[wave] = kmx;
+      s_wn[wave] = nl;
+    }
+    __syncthreads();
+    uint64_t kmax = 0;
+    uint32_t nlive = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kRunWaves; ++w) {
+      kmax = s_wk[w] > kmax ? s_wk[w] : kmax;
+      nlive += s_wn[w];
+    }
+    __syncthreads();
+    if (nlive == 0) break;  // every key is below B: the run ends
+    uint64_t hth = bkey;
+    if (nlive > kHot) {
+      uint64_t kref = kmax;
+      uint32_t cap = kHot;
+      uint32_t S = bit_length(kmax - bkey);
+      S = S > 8u ? S - 8u : 0u;
+      while (true) {
+        s_hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t s = 0; s < kOwnSlots; ++s) {
+          if (live[s] && key[s] <= kref) {
+            const uint64_t bb = (kref - key[s]) >> S;
+            if (bb < kSelBins) atomicAdd(&s_hist[(uint32_t)bb], 1u);
+          }
+        }
+        __syncthreads();
+        if (wave == 0) {
+          const uint4 hv = reinterpret_cast<const uint4 *>(s_hist)[lane];
+          const uint32_t tot = hv.x + hv.y + hv.z + hv.w;
+          const uint32_t incl = wave_incl_scan(tot);
+          uint32_t cum = incl - tot;
+          const uint32_t bins[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j) {
+            if (cum <= cap && cum + bins[j] > cap) {
+              s_misc[0] = 4 * lane + j;
+              s_misc[1] = cum;
+            }
+            cum += bins[j];
+          }
+          if (lane == 63 && incl <= cap) s_misc[0] = kNone;
+        }
+        __syncthreads();
+        const uint32_t bs = s_misc[0], before = s_misc[1];
+        if (PROF) pf[kRpSelPasses] += 1;
+        __syncthreads();
+        if (bs == kNone) {  // cannot happen (every window holds more than cap keys):
+          hth = kmax;       // then take the maximum alone
+          break;
+        }
+        if (before >= cap / 2 || S == 0) {
+          hth = kref - ((uint64_t)bs << S) + 1;
+          break;
+        }
+        kref -= (uint64_t)bs << S;
+        cap -= before;
+        S = S >= 8u ? S - 8u : 0u;
+      }
+      hth = hth > bkey ? hth : bkey;
+    }
+    NSFPS_RMARK(kRpSelect);
+    // ---- hot copies -> LDS -> wave 0
+    {
+      uint64_t bal[kOwnSlots];
+#pragma unroll
+      for (uint32_t s = 0; s < kOwnSlots; ++s) {
+        bal[s] = __ballot(live[s] && key[s] >= hth);
+        if (lane == 0) s_wn[wave * kOwnSlots + s] = (uint32_t)__popcll(bal[s]);
+      }
+      if (tid == 0) s_pub = 0;
+      __syncthreads();
+      uint32_t base = 0, nhot = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < kRunWaves * kOwnSlots; ++j) {
+        const uint32_t v = s_wn[j];
+        base += j < wave * kOwnSlots ? v : 0u;
+        nhot += v;
+      }
+#pragma unroll
+      for (uint32_t s = 0; s < kOwnSlots; ++s) {
+        if ((bal[s] >> lane) & 1) {
+          const uint32_t hi = base + lanes_below(bal[s]);
+          if (hi < kHot) {
+            s_hot[hi][0] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
+                                      __float_as_uint(z[s]), __float_as_uint(d[s]));
+            s_hot[hi][1] = make_uint4(lo[s], row[s], cc[s], 0u);
+          } else {  // cannot happen (at most kHot keys are >= the hot threshold)
+            rs.err = 2;
+          }
+        }
+        base += (uint32_t)__popcll(bal[s]);
+      }
+      if (tid == 0) s_misc[2] = nhot < kHot ? nhot : kHot;
+      __syncthreads();
+    }
+    NSFPS_RMARK(kRpGather);
+    if (wave == 0) {
+      // ---- hot run.  Uniform values stay in scalar registers so that the
+      // tests on them are scalar compares.
+      const uint32_t nhot = s_misc[2];
+      uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;  // an idle lane: distance 0, key 0
+      if (lane < nhot) {
+        e0 = s_hot[lane][0];
+        e1 = s_hot[lane][1];
+      }
+      const float hx = __uint_as_float(e0.x), hy = __uint_as_float(e0.y), hz = __uint_as_float(e0.z);
+      float hd = __uint_as_float(e0.w);
+      const uint32_t hlo = e1.x, hrow = e1.y, hcell = e1.z;
+      const uint32_t hcx = hcell & 1023u, hcy = (hcell >> 10) & 1023u, hcz = hcell >> 20;
+      const uint32_t hth_hi = uniform((uint32_t)(hth >> 32)), hth_lo = uniform((uint32_t)hth);
+      // thresholds as bits: non-negative floats order like their bit patterns
+      uint32_t tb0 = h0 ? uniform(__float_as_uint(s_t[0][h0])) : 0u;
+      uint32_t tb1 = h1 ? uniform(__float_as_uint(s_t[1][h1])) : 0u;
+      uint32_t tb2 = h2 ? uniform(__float_as_uint(s_t[2][h2])) : 0u;
+      const uint32_t room = m - it;  // samples left (>= 1)
+      uint32_t npk = 0, stop = 0;
+      while (true) {
+        // publish the previous sample (its LDS writes were issued one step ago)
+        if (lane == 0)
+          __hip_atomic_store(&s_pub, npk, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint32_t hi = __float_as_uint(hd);
+        const uint32_t M = wave_max_u32_s(hi);
+        uint64_t tw = __ballot(hi == M);
+        if (__popcll(tw) > 1) {
+          const uint32_t L = wave_max_u32_s(hi == M ? hlo : 0u);
+          tw = __ballot(hi == M && hlo == L);
+        }
+        const uint32_t wl = (uint32_t)__ffsll((long long)tw) - 1;
+        const uint32_t wlo = rdlane(hlo, wl);
+        if (M < hth_hi || (M == hth_hi && wlo < hth_lo)) {  // below the hot threshold
+          stop = 1;
+          break;
+        }
+        if (M == 0) {  // maximum distance 0: src/yuezu_fps.cpp:705-706
+          stop = 2;
+          break;
+        }
+        const uint32_t qxb = rdlane(__float_as_uint(hx), wl), qyb = rdlane(__float_as_uint(hy), wl);
+        const uint32_t qzb = rdlane(__float_as_uint(hz), wl), qc = rdlane(hcell, wl);
+        const uint32_t qrow = rdlane(hrow, wl);
+        // half-widths never grow: step down through the threshold table
+        if (M < tb0 || M < tb1 || M < tb2) {
+          while (h0 && M < tb0) tb0 = --h0 ? uniform(__float_as_uint(s_t[0][h0])) : 0u;
+          while (h1 && M < tb1) tb1 = --h1 ? uniform(__float_as_uint(s_t[1][h1])) : 0u;
+          while (h2 && M < tb2) tb2 = --h2 ? uniform(__float_as_uint(s_t[2][h2])) : 0u;
+        }
+        if (lane == 0) {
+          s_pk[npk][0] = make_uint4(qxb, qyb, qzb, qrow);
+          s_pk[npk][1] = make_uint4(qc, h0 | (h1 << 10) | (h2 << 20), M, 0u);
+        }
+        if (++npk >= room) {  // the last sample needs no update
+          stop = 2;
+          break;
+        }
+        const uint32_t qcx = qc & 1023u, qcy = (qc >> 10) & 1023u, qcz = qc >> 20;
+        const bool inc = hcx - qcx + h0 <= 2 * h0 && hcy - qcy + h1 <= 2 * h1 &&
+                         hcz - qcz + h2 <= 2 * h2;
+        const float dd = sqdist(hx, hy, hz, __uint_as_float(qxb), __uint_as_float(qyb),
+                                __uint_as_float(qzb));
+        hd = inc && dd < hd ? dd : hd;
+      }
+      if (lane == 0) {
+        s_misc[3] = npk;
+        s_misc[4] = stop;
+        s_misc[7] = h0 | (h1 << 10) | (h2 << 20);
+        __hip_atomic_store(&s_pub, npk | kPubDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      NSFPS_RMARK(kRpHot);
+    } else {
+      // ---- waves 1-3: the published samples to the owned entries, in batches
+      // (lane l holds sample j + l); a slot meets only the samples whose cube
+      // overlaps its cell box.  Wave 0 always publishes the done flag when
+      // its run ends, so this wait ends.
+      uint32_t j = 0;
+      while (true) {
+        const uint32_t pub =
+            uniform(__hip_atomic_load(&s_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        const uint32_t n = pub & (kPubDone - 1);
+        if (n > j) {
+          const bool have = lane < n - j;
+          uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0;
+          uint32_t lo_c = 0, hi_c = 0;
+          if (have) {
+            a0 = s_pk[j + lane][0];
+            a1 = s_pk[j + lane][1];
+            cube_corners(a1.x, a1.y, b0, b1, b2, lo_c, hi_c);
+          }
+#pragma unroll
+          for (uint32_t s = 0; s < kOwnSlots; ++s) {
+            uint64_t msk = __ballot(have && cube_overlaps(make_uint2(lo_c, hi_c), blo[s], bhi[s]));
+            while (msk) {
+              const uint32_t t = (uint32_t)__ffsll((long long)msk) - 1;
+              msk &= msk - 1;
+              const uint32_t qc = rdlane(a1.x, t), hh = rdlane(a1.y, t);
+              const uint32_t g0 = hh & 1023u, g1 = (hh >> 10) & 1023u, g2 = hh >> 20;
+              if (in_cube_rel(cc[s], g0 - (qc & 1023u), g1 - ((qc >> 10) & 1023u),
+                              g2 - (qc >> 20), 2 * g0, 2 * g1, 2 * g2)) {
+                const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(rdlane(a0.x, t)),
+                                        __uint_as_float(rdlane(a0.y, t)),
+                                        __uint_as_float(rdlane(a0.z, t)));
+                d[s] = dd < d[s] ? dd : d[s];
+              }
+            }
+          }
+          j = n;
+        }
+        if (pub & kPubDone) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+    NSFPS_RMARK(kRpDrain);
+    const uint32_t npk = s_misc[3], stop = s_misc[4];
+    h0 = s_misc[7] & 1023u;
+    h1 = (s_misc[7] >> 10) & 1023u;
+    h2 = s_misc[7] >> 20;
+    // the run's samples to global memory: rows, positions and cubes
+    if (wave == 0 && lane < npk) {
+      const uint4 a0 = s_pk[lane][0], a1 = s_pk[lane][1];
+      uint32_t lo_c, hi_c;
+      cube_corners(a1.x, a1.y, b0, b1, b2, lo_c, hi_c);
+      out[it + lane] = (int32_t)a0.w;
+      pick_p[np + lane] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
+                                      __uint_as_float(a0.z), __uint_as_float(a1.z));
+      pick_c[np + lane] = make_uint2(lo_c, hi_c);
+    }
+    it += npk;
+    np += npk;
+    if (PROF) pf[kRpHotRounds] += 1;
+    if (stop == 2) {
       done = true;
       break;
     }
-    if (tid == 0) gptr(c.out)[it] = (int32_t)rdlane(r1.y, wv);
-    if (++it >= m) {
-      done = true;
-      break;
-    }
-    const float qx = __uint_as_float(rdlane(r0.z, wv)), qy = __uint_as_float(rdlane(r0.w, wv));
-    const float qz = __uint_as_float(rdlane(r1.x, wv));
-    const uint32_t qc = rdlane(r1.z, wv);
-    const float D = __uint_as_float(bh);
-    // half-widths never grow: step down through the threshold table
-    while (h0 && D < t0) t0 = --h0 ? s_t[0][h0] : 0.f;
-    while (h1 && D < t1) t1 = --h1 ? s_t[1][h1] : 0.f;
-    while (h2 && D < t2) t2 = --h2 ? s_t[2][h2] : 0.f;
-    const uint32_t qx_c = qc & 1023u, qy_c = (qc >> 10) & 1023u, qz_c = qc >> 20;
-    if (tid == 0) {
-      const uint32_t lo_c = pack_cell(qx_c > h0 ? qx_c - h0 : 0u, qy_c > h1 ? qy_c - h1 : 0u,
-                                      qz_c > h2 ? qz_c - h2 : 0u);
-      const uint32_t hi_c = pack_cell(min(qx_c + h0, b0 - 1), min(qy_c + h1, b1 - 1),
-                                      min(qz_c + h2, b2 - 1));
-      gptr(c.pick_p)[np] = make_float4(qx, qy, qz, D);
-      gptr(c.pick_c)[np] = make_uint2(lo_c, hi_c);
-    }
-    ++np;
-    const uint32_t ax = max(ex, qx_c) - min(ex, qx_c), ay = max(ey, qy_c) - min(ey, qy_c),
-                   az = max(ez, qz_c) - min(ez, qz_c);
-    if (act && ax <= h0 && ay <= h1 && az <= h2) {
-      const float dd = sqdist(e.x, e.y, e.z, qx, qy, qz);
-      d = dd < d ? dd : d;
-    }
-    par ^= 1u;
+    if (hth == bkey && stop == 1) break;  // every live entry was hot: all below B now
   }
   if (tid == 0) {
     *gptr(c.iter) = it;
@@ -510,13 +830,21 @@ __global__ __launch_bounds__(kListCap) void k_run(const CloudDev *__restrict__ c
     rs.hc[0] = h0;
     rs.hc[1] = h1;
     rs.hc[2] = h2;
-    rs.kref0 = capped ? ~0ull : bkey - 1;  // every key is below the threshold now
-    rs.s0 = capped ? kMaxShift : rs.s0_next;
+    rs.kref0 = bkey - 1;  // every key is below the threshold now
+    rs.s0 = rs.s0_next;
     rs.nlist = 0;
     rs.rounds += 1;
     if (done) *gptr(c.done) = 1;
   }
-  for (uint32_t j = tid; j < kHists * kHistBins; j += kListCap) gptr(c.hist)[j] = 0;
+  for (uint32_t j = tid; j < kHists * kHistBins; j += kRunThreads) gptr(c.hist)[j] = 0;
+  if (PROF && tid == 0) {
+    NSFPS_RMARK(kRpTail);
+    pf[kRpPicks] = np;
+    pf[kRpRounds] = 1;
+    NSFPS_GLOBAL uint64_t *pw = gptr(c.prof);
+    for (uint32_t i = 0; i < kRpWords; ++i) pw[i] += pf[i];
+  }
+#undef NSFPS_RMARK
 }
 
 // ------------------------------------------------------------------ setup
@@ -558,13 +886,16 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 }
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, hipStream_t st) {
+                         uint32_t rounds, bool profile, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   for (uint32_t r = 0; r < rounds; ++r) {
     k_update<<<grid, kPassThreads, 0, st>>>(d_clouds);
     for (uint32_t p = 1; p <= kRefinePasses; ++p) k_refine<<<grid, kPassThreads, 0, st>>>(d_clouds, p);
     k_gather<<<grid, kPassThreads, 0, st>>>(d_clouds);
-    k_run<<<nclouds, kListCap, 0, st>>>(d_clouds);
+    if (profile)
+      k_run<true><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    else
+      k_run<false><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
   }
   return hipGetLastError();
 }
