@@ -62,7 +62,6 @@ struct HostRange {
   nsfps_range prim;
   nsfps_range_info info;
   std::vector<uint32_t> lut[3];
-  std::vector<float> cube_t;  // 3 x kCubeTab half-width thresholds
   RangeDev dev;
 };
 
@@ -78,38 +77,6 @@ nsfps_status check_range(const nsfps_range &r) {
     if (v > 1024) return fail(NSFPS_EUNSUPPORTED, "block counts above 1024 per axis are not supported");
   }
   return NSFPS_OK;
-}
-
-// Cube half-width of get_morton_codes_in_range (src/yuezu_fps.cpp:564-570)
-// for one axis, evaluated like the device's cube_half: IEEE sqrtf and
-// division, ceil, clamped to the grid.
-uint32_t cube_half_host(float D, float bs, uint32_t blocks) {
-  volatile float rad = std::sqrt(D < 0.0f ? 0.0f : D);
-  volatile float q = rad / bs;
-  float f = std::ceil(q);
-  if (!(f < (float)blocks)) return blocks;
-  return (uint32_t)f;
-}
-
-// t[a * kCubeTab + k] = smallest D >= 0 whose half-width on axis a is >= k
-// (k = 1..blocks; +inf if none).  The half-width is monotone in D, so a
-// non-increasing sequence of D walks down this table.
-void cube_thresholds(const RangeDev &d, std::vector<float> &t) {
-  t.assign(3 * kCubeTab, INFINITY);
-  for (int a = 0; a < 3; ++a) {
-    t[a * kCubeTab] = 0.0f;
-    for (uint32_t k = 1; k <= d.blocks[a]; ++k) {
-      uint32_t lo = 0, hi = 0x7f800000u;  // [0, +inf]
-      auto val = [](uint32_t u) { float f; memcpy(&f, &u, 4); return f; };
-      if (cube_half_host(val(hi), d.bsize[a], d.blocks[a]) < k) continue;
-      while (lo < hi) {
-        uint32_t mid = lo + (hi - lo) / 2;
-        if (cube_half_host(val(mid), d.bsize[a], d.blocks[a]) >= k) hi = mid;
-        else lo = mid + 1;
-      }
-      t[a * kCubeTab + k] = val(lo);
-    }
-  }
 }
 
 // make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
@@ -164,7 +131,6 @@ void derive(const nsfps_range &r, HostRange &h) {
   d.lut_total = off;
   d.T = (uint32_t)h.info.total_blocks;
   d.bijective = bij ? 1u : 0u;
-  cube_thresholds(d, h.cube_t);
 }
 
 void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) {
@@ -260,7 +226,6 @@ struct CloudPlan {
   // build-time buffers
   float *d_xyz_stage = nullptr;
   uint32_t *d_lut = nullptr, *d_counts = nullptr, *d_lc = nullptr;
-  float *d_cube_t = nullptr;
   uint32_t *d_small = nullptr;  // [0] non-finite flag, [1] max occupancy, [2] phys0
   uint2 *d_cell_info = nullptr;
 };
@@ -322,8 +287,6 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.list_p = bp.take<float4>(kListCap);
   c.list_r = bp.take<uint2>(kListCap);
   c.list_c = bp.take<uint32_t>(kListCap);
-  p.d_cube_t = bp.take<float>(3 * kCubeTab);
-  c.cube_t = p.d_cube_t;
   c.lut = p.d_lut;
   c.n = n;
   c.m = p.m;
@@ -392,8 +355,6 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   std::vector<uint32_t> lut;
   for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
   HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
-  HIP_TRY(hipMemcpyAsync(p.d_cube_t, p.rng.cube_t.data(), p.rng.cube_t.size() * 4,
-                         hipMemcpyHostToDevice, st));
   const float *xyz = p.d_xyz_in;
   if (p.h_xyz) {
     HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)n * 12, hipMemcpyHostToDevice, st));

@@ -31,8 +31,6 @@ constexpr uint32_t kListCap = 1024;
 constexpr uint32_t kHistBins = 4096;
 constexpr uint32_t kHists = 4;
 constexpr uint32_t kRefinePasses = 2;
-// Entries per axis of the cube half-width threshold table (blocks <= 1024).
-constexpr uint32_t kCubeTab = 1025;
 
 // Range values the kernels need, all derived on the host exactly as the
 // reference derives them (src/yuezu_fps.cpp:7-11, 136-161, 170-193).
@@ -75,10 +73,8 @@ struct RunState {
   uint32_t s0_next;   // bin shift proposed for the next round
   uint32_t npicks;    // picks of the last run (applied by the next update pass)
   uint32_t nlist;     // list entries gathered this round
-  uint32_t hc[3];     // cube half-width per axis at the latest pick
   uint32_t rounds;    // rounds that ran (statistics)
   uint32_t err;       // set if a list overflowed (internal error)
-  uint32_t pad;
 };
 
 // Everything one cloud's kernels touch.  Device pointers; passed by value to
@@ -122,7 +118,6 @@ struct CloudDev {
   float4 *list_p;             // kListCap: x, y, z, min distance
   uint2 *list_r;              // kListCap: logical rank, input row
   uint32_t *list_c;           // kListCap: cell (10 bits per axis)
-  const float *cube_t;        // 3 x kCubeTab: smallest D giving half-width k
 };
 
 // Argmax key: larger min-distance wins, equal distances go to the smaller

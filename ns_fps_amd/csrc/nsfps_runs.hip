@@ -426,7 +426,12 @@ constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = 6;
 constexpr uint32_t kHot = 64;
 constexpr uint32_t kSelBins = 256;
+constexpr uint32_t kBatch = 4;           // samples per hot step at most
 constexpr uint32_t kPubDone = 0x10000u;  // flag in the published sample count
+#ifndef NSFPS_POLL_SLEEP
+#define NSFPS_POLL_SLEEP 4
+#endif
+constexpr int kPollSleep = NSFPS_POLL_SLEEP;  // s_sleep units (64 clocks) between polls
 constexpr uint32_t kLoadSlots = kListCap / kRunThreads;
 static_assert(3 * 64 * kOwnSlots >= kListCap, "owner lanes hold the list");
 
@@ -434,8 +439,9 @@ static_assert(3 * 64 * kOwnSlots >= kListCap, "owner lanes hold the list");
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
   kRpLoad = 0, kRpSelect, kRpGather, kRpHot, kRpDrain, kRpTail,
-  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpSelPasses, kRpWords = 16
+  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpWords = 16
 };
+
 
 __device__ __forceinline__ uint32_t spatial_group(uint32_t cell, uint32_t b0, uint32_t b1,
                                                   uint32_t b2) {
@@ -466,10 +472,11 @@ __device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b
 
 template <bool PROF>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  __shared__ float s_t[3][kCubeTab];
   __shared__ uint4 s_ent[kListCap][2];  // sorted list: {x, y, z, d}, {~rank, row, cell, -}
   __shared__ uint4 s_hot[kHot][2];      // hot copies, same layout
-  __shared__ uint4 s_pk[kHot][2];       // samples of a hot run: {qx, qy, qz, row}, {cell, h, D, -}
+  __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy index, half-widths
+  __shared__ uint64_t s_hk[kHot];       // hot keys (ranking)
+  __shared__ uint32_t s_ord[kHot];      // copy index by rank
   __shared__ uint32_t s_cnt[64], s_off[64];
   __shared__ uint32_t s_hist[kSelBins];
   __shared__ uint64_t s_wk[kRunWaves];
@@ -491,10 +498,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   } while (0)
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   const uint32_t b0 = c.r.blocks[0], b1 = c.r.blocks[1], b2 = c.r.blocks[2];
-#pragma unroll
-  for (int a = 0; a < 3; ++a)
-    for (uint32_t k = tid; k <= c.r.blocks[a]; k += kRunThreads)
-      s_t[a][k] = gptr(c.cube_t)[a * kCubeTab + k];
   if (tid < 64) s_cnt[tid] = 0;
   const uint32_t nlist = min(rs.nlist, kListCap);
   const uint64_t bkey = rs.bkey;
@@ -561,7 +564,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     bhi[s] = pack_cell(wave_max_u32(v ? cx : 0u), wave_max_u32(v ? cy : 0u),
                        wave_max_u32(v ? cz : 0u));
   }
-  uint32_t h0 = rs.hc[0], h1 = rs.hc[1], h2 = rs.hc[2];
   uint32_t it = *gptr(c.iter);
   const uint32_t m = c.m;
   NSFPS_GLOBAL int32_t *const out = gptr(c.out);
@@ -633,7 +635,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         }
         __syncthreads();
         const uint32_t bs = s_misc[0], before = s_misc[1];
-        if (PROF) pf[kRpSelPasses] += 1;
         __syncthreads();
         if (bs == kNone) {  // cannot happen (every window holds more than cap keys):
           hth = kmax;       // then take the maximum alone
@@ -686,74 +687,216 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     NSFPS_RMARK(kRpGather);
     if (wave == 0) {
-      // ---- hot run.  Uniform values stay in scalar registers so that the
-      // tests on them are scalar compares.
+      // ---- hot run.  The hot copies are ranked by key once; samples are then
+      // taken down that order.  A copy no cube has touched keeps its key, so
+      // the next sample is the first untouched copy in rank order, or the
+      // largest touched ("dirty") copy when its key is larger.  Ranked, the
+      // copies at or above the hot threshold and those with a distance > 0
+      // are prefixes, and every copy's cube half-widths are computed once up
+      // front; a step then needs no key reads while nothing is dirty.
       const uint32_t nhot = s_misc[2];
-      uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;  // an idle lane: distance 0, key 0
-      if (lane < nhot) {
-        e0 = s_hot[lane][0];
-        e1 = s_hot[lane][1];
+      uint64_t mykey = 0;  // an idle lane: key 0, ranked after every copy
+      if (lane < nhot)
+        mykey = ((uint64_t)s_hot[lane][0].w << 32) | s_hot[lane][1].x;
+      s_hk[lane] = mykey;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      uint32_t rank = 0;
+#pragma unroll 8
+      for (uint32_t i = 0; i < kHot; ++i) {
+        const uint64_t k = s_hk[i];
+        rank += (k > mykey || (k == mykey && i < lane)) ? 1u : 0u;
+      }
+      s_ord[rank] = lane;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const uint32_t src = s_ord[lane];  // lane = rank, src = index of the copy in s_hot
+      const bool real = lane < nhot;
+      uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;
+      if (real) {
+        e0 = s_hot[src][0];
+        e1 = s_hot[src][1];
       }
       const float hx = __uint_as_float(e0.x), hy = __uint_as_float(e0.y), hz = __uint_as_float(e0.z);
       float hd = __uint_as_float(e0.w);
-      const uint32_t hlo = e1.x, hrow = e1.y, hcell = e1.z;
+      const uint32_t hlo = e1.x, hcell = e1.z;
       const uint32_t hcx = hcell & 1023u, hcy = (hcell >> 10) & 1023u, hcz = hcell >> 20;
-      const uint32_t hth_hi = uniform((uint32_t)(hth >> 32)), hth_lo = uniform((uint32_t)hth);
-      // thresholds as bits: non-negative floats order like their bit patterns
-      uint32_t tb0 = h0 ? uniform(__float_as_uint(s_t[0][h0])) : 0u;
-      uint32_t tb1 = h1 ? uniform(__float_as_uint(s_t[1][h1])) : 0u;
-      uint32_t tb2 = h2 ? uniform(__float_as_uint(s_t[2][h2])) : 0u;
-      const uint32_t room = m - it;  // samples left (>= 1)
-      uint32_t npk = 0, stop = 0;
+      // cube half-widths of this copy as a sample (src/yuezu_fps.cpp:564-570);
+      // at or beyond the grid they select the same cells as blocks - 1
+      auto halves = [&](float D) {
+        return min((uint32_t)cube_half(D, c.r.bsize[0], b0), b0 - 1) |
+               (min((uint32_t)cube_half(D, c.r.bsize[1], b1), b1 - 1) << 10) |
+               (min((uint32_t)cube_half(D, c.r.bsize[2], b2), b2 - 1) << 20);
+      };
+      uint32_t hpk = halves(hd);
+      const uint64_t hkey = ((uint64_t)__float_as_uint(hd) << 32) | hlo;
+      const uint32_t cut = (uint32_t)__popcll(__ballot(real && hkey >= hth));  // >= hot threshold
+      const uint32_t nz = (uint32_t)__popcll(__ballot(real && hd > 0.0f));     // distance > 0
+      const uint32_t th_hi = uniform((uint32_t)(hth >> 32)), th_lo = uniform((uint32_t)hth);
+      const uint32_t room = uniform(m - it);  // samples left (>= 1)
+      uint64_t avail = nhot >= 64 ? ~0ull : ((1ull << nhot) - 1);  // untouched, not taken
+      uint64_t dirty = 0;
+      uint32_t dl = 64;  // lane of the dirty maximum (64: none)
+      uint32_t dk_hi = 0, dk_lo = 0;
+      uint32_t npk = 0, npub = 0, stop = 0;
+      uint32_t rec_x = 0, rec_y = 0;  // lane j: record of sample j
+      uint32_t kb = kBatch;           // batch width: kBatch, 1 after a conflict, doubling back
       while (true) {
-        // publish the previous sample (its LDS writes were issued one step ago)
-        if (lane == 0)
-          __hip_atomic_store(&s_pub, npk, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const uint32_t hi = __float_as_uint(hd);
-        const uint32_t M = wave_max_u32_s(hi);
-        uint64_t tw = __ballot(hi == M);
-        if (__popcll(tw) > 1) {
-          const uint32_t L = wave_max_u32_s(hi == M ? hlo : 0u);
-          tw = __ballot(hi == M && hlo == L);
+        uint64_t taken = 0, touched = 0;
+        uint32_t n = 0, nmax = 0;
+        float nd = hd;
+        if (!dirty) {
+          // ---- batch: the next untouched copies in rank order.  Every copy
+          // ranked above candidate k is taken, and a copy lowered by an earlier
+          // candidate's cube started below it, so candidate k is the maximum
+          // unless an earlier candidate's cube lowered it: the batch is the
+          // prefix of candidates no earlier cube lowered.
+          uint32_t ac[kBatch];
+          uint64_t rest = avail;
+#pragma unroll
+          for (uint32_t k = 0; k < kBatch; ++k) {
+            ac[k] = rest ? (uint32_t)__builtin_ctzll(rest) : 64u;
+            rest &= rest - 1;
+          }
+          if (ac[0] >= cut) {  // hot set exhausted, or below the hot threshold
+            stop = 1;
+            break;
+          }
+          if (ac[0] >= nz) {  // maximum distance 0: src/yuezu_fps.cpp:705-706
+            stop = 2;
+            break;
+          }
+          nmax = 1;
+#pragma unroll
+          for (uint32_t k = 1; k < kBatch; ++k)
+            if (nmax == k && k < kb && ac[k] < cut && ac[k] < nz && npk + k < room) nmax = k + 1;
+          uint32_t qh[kBatch], qsrc[kBatch];
+          uint64_t tk[kBatch];
+          bool dk[kBatch];
+          float ddk[kBatch];
+#pragma unroll
+          for (uint32_t k = 0; k < kBatch; ++k) {
+            tk[k] = 0;
+            dk[k] = false;
+            ddk[k] = 0.f;
+            qh[k] = qsrc[k] = 0;
+            if (k < nmax) {
+              const uint32_t w = ac[k];
+              const float qx = __uint_as_float(rdlane(__float_as_uint(hx), w));
+              const float qy = __uint_as_float(rdlane(__float_as_uint(hy), w));
+              const float qz = __uint_as_float(rdlane(__float_as_uint(hz), w));
+              const uint32_t qc = rdlane(hcell, w);
+              qh[k] = rdlane(hpk, w);
+              qsrc[k] = rdlane(src, w);
+              const uint32_t c0 = qh[k] & 1023u, c1 = (qh[k] >> 10) & 1023u, c2 = qh[k] >> 20;
+              const bool inc = (hcx - (qc & 1023u) + c0 <= 2 * c0) &
+                               (hcy - ((qc >> 10) & 1023u) + c1 <= 2 * c1) &
+                               (hcz - (qc >> 20) + c2 <= 2 * c2);
+              ddk[k] = sqdist(hx, hy, hz, qx, qy, qz);
+              dk[k] = (bool)((avail >> lane) & 1) & inc & (ddk[k] < hd);
+              tk[k] = __ballot(dk[k]);
+            }
+          }
+          n = 1;
+          uint64_t tacc = tk[0];
+#pragma unroll
+          for (uint32_t k = 1; k < kBatch; ++k) {
+            if (n == k && k < nmax && !((tacc >> ac[k]) & 1)) {
+              n = k + 1;
+              tacc |= tk[k];
+            }
+          }
+#pragma unroll
+          for (uint32_t k = 0; k < kBatch; ++k) {
+            if (k < n) {
+              if (lane == npk + k) {
+                rec_x = qsrc[k] | ((qh[k] & 0xfffffu) << 8);
+                rec_y = qh[k] >> 20;
+              }
+              taken |= 1ull << ac[k];
+              touched |= tk[k];
+              nd = dk[k] && ddk[k] < nd ? ddk[k] : nd;
+            }
+          }
+          kb = n < nmax ? 1u : (n == kb ? min(2 * kb, kBatch) : kb);
+        } else {
+          // ---- one sample: the first untouched copy or the dirty maximum
+          const uint32_t al = avail ? (uint32_t)__builtin_ctzll(avail) : 64u;
+          uint32_t ak_hi = 0, ak_lo = 0;
+          if (al < 64) {
+            ak_hi = rdlane(__float_as_uint(hd), al);
+            ak_lo = rdlane(hlo, al);
+          }
+          const bool useb = dl < 64 && (dk_hi > ak_hi || (dk_hi == ak_hi && dk_lo > ak_lo));
+          const uint32_t wl = useb ? dl : al;
+          const uint32_t M = useb ? dk_hi : ak_hi, wlo = useb ? dk_lo : ak_lo;
+          if (wl >= 64 || M < th_hi || (M == th_hi && wlo < th_lo)) {
+            stop = 1;
+            break;
+          }
+          if (M == 0) {
+            stop = 2;
+            break;
+          }
+          const float qx = __uint_as_float(rdlane(__float_as_uint(hx), wl));
+          const float qy = __uint_as_float(rdlane(__float_as_uint(hy), wl));
+          const float qz = __uint_as_float(rdlane(__float_as_uint(hz), wl));
+          const uint32_t qc = rdlane(hcell, wl), qh = rdlane(hpk, wl), qs = rdlane(src, wl);
+          if (lane == npk) {
+            rec_x = qs | ((qh & 0xfffffu) << 8);
+            rec_y = qh >> 20;
+          }
+          n = 1;
+          taken = 1ull << wl;
+          const uint32_t c0 = qh & 1023u, c1 = (qh >> 10) & 1023u, c2 = qh >> 20;
+          const bool inc = (hcx - (qc & 1023u) + c0 <= 2 * c0) &
+                           (hcy - ((qc >> 10) & 1023u) + c1 <= 2 * c1) &
+                           (hcz - (qc >> 20) + c2 <= 2 * c2);
+          const float dd = sqdist(hx, hy, hz, qx, qy, qz);
+          const bool dec = (bool)(((avail | dirty) >> lane) & 1) & inc & (dd < hd);
+          touched = __ballot(dec);
+          nd = dec ? dd : hd;
+          if (useb || ((dirty & ~taken) == 0 && !(touched & ~taken))) kb = kBatch;
         }
-        const uint32_t wl = (uint32_t)__ffsll((long long)tw) - 1;
-        const uint32_t wlo = rdlane(hlo, wl);
-        if (M < hth_hi || (M == hth_hi && wlo < hth_lo)) {  // below the hot threshold
-          stop = 1;
-          break;
+        npk += n;
+        if (npk - npub >= 8) {  // publish
+          if (lane >= npub && lane < npk) s_rec[lane] = make_uint2(rec_x, rec_y);
+          if (lane == 0)
+            __hip_atomic_store(&s_pub, npk, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+          npub = npk;
         }
-        if (M == 0) {  // maximum distance 0: src/yuezu_fps.cpp:705-706
+        if (npk >= room) {  // the last sample needs no update
           stop = 2;
           break;
         }
-        const uint32_t qxb = rdlane(__float_as_uint(hx), wl), qyb = rdlane(__float_as_uint(hy), wl);
-        const uint32_t qzb = rdlane(__float_as_uint(hz), wl), qc = rdlane(hcell, wl);
-        const uint32_t qrow = rdlane(hrow, wl);
-        // half-widths never grow: step down through the threshold table
-        if (M < tb0 || M < tb1 || M < tb2) {
-          while (h0 && M < tb0) tb0 = --h0 ? uniform(__float_as_uint(s_t[0][h0])) : 0u;
-          while (h1 && M < tb1) tb1 = --h1 ? uniform(__float_as_uint(s_t[1][h1])) : 0u;
-          while (h2 && M < tb2) tb2 = --h2 ? uniform(__float_as_uint(s_t[2][h2])) : 0u;
+        touched &= ~taken;
+        avail &= ~taken;
+        dirty &= ~taken;
+        const bool redo = touched || ((taken & (dl < 64 ? 1ull << dl : 0ull)) && dirty);
+        if (touched) {
+          if ((touched >> lane) & 1) {
+            hd = nd;
+            hpk = halves(hd);
+          }
+          dirty |= touched;
+          avail &= ~touched;
         }
-        if (lane == 0) {
-          s_pk[npk][0] = make_uint4(qxb, qyb, qzb, qrow);
-          s_pk[npk][1] = make_uint4(qc, h0 | (h1 << 10) | (h2 << 20), M, 0u);
+        if (redo) {  // the dirty maximum
+          const bool dv = (dirty >> lane) & 1;
+          const uint32_t hi = dv ? __float_as_uint(hd) : 0u;
+          const uint32_t Md = wave_max_u32_s(hi);
+          uint64_t tw = __ballot(dv && hi == Md);
+          if (__popcll(tw) > 1) {
+            const uint32_t L = wave_max_u32_s(dv && hi == Md ? hlo : 0u);
+            tw = __ballot(dv && hi == Md && hlo == L);
+          }
+          dl = tw ? (uint32_t)__ffsll((long long)tw) - 1 : 64u;
+          dk_hi = Md;
+          dk_lo = tw ? rdlane(hlo, dl) : 0u;
         }
-        if (++npk >= room) {  // the last sample needs no update
-          stop = 2;
-          break;
-        }
-        const uint32_t qcx = qc & 1023u, qcy = (qc >> 10) & 1023u, qcz = qc >> 20;
-        const bool inc = hcx - qcx + h0 <= 2 * h0 && hcy - qcy + h1 <= 2 * h1 &&
-                         hcz - qcz + h2 <= 2 * h2;
-        const float dd = sqdist(hx, hy, hz, __uint_as_float(qxb), __uint_as_float(qyb),
-                                __uint_as_float(qzb));
-        hd = inc && dd < hd ? dd : hd;
       }
+      if (lane >= npub && lane < npk) s_rec[lane] = make_uint2(rec_x, rec_y);
       if (lane == 0) {
         s_misc[3] = npk;
         s_misc[4] = stop;
-        s_misc[7] = h0 | (h1 << 10) | (h2 << 20);
         __hip_atomic_store(&s_pub, npk | kPubDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
       NSFPS_RMARK(kRpHot);
@@ -769,12 +912,14 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         const uint32_t n = pub & (kPubDone - 1);
         if (n > j) {
           const bool have = lane < n - j;
-          uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0;
-          uint32_t lo_c = 0, hi_c = 0;
+          uint4 a0 = make_uint4(0u, 0u, 0u, 0u);
+          uint32_t qc = 0, hh = 0, lo_c = 0, hi_c = 0;
           if (have) {
-            a0 = s_pk[j + lane][0];
-            a1 = s_pk[j + lane][1];
-            cube_corners(a1.x, a1.y, b0, b1, b2, lo_c, hi_c);
+            const uint2 r = s_rec[j + lane];
+            a0 = s_hot[r.x & 255u][0];
+            qc = s_hot[r.x & 255u][1].z;
+            hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+            cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
           }
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
@@ -782,10 +927,10 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
             while (msk) {
               const uint32_t t = (uint32_t)__ffsll((long long)msk) - 1;
               msk &= msk - 1;
-              const uint32_t qc = rdlane(a1.x, t), hh = rdlane(a1.y, t);
-              const uint32_t g0 = hh & 1023u, g1 = (hh >> 10) & 1023u, g2 = hh >> 20;
-              if (in_cube_rel(cc[s], g0 - (qc & 1023u), g1 - ((qc >> 10) & 1023u),
-                              g2 - (qc >> 20), 2 * g0, 2 * g1, 2 * g2)) {
+              const uint32_t tc = rdlane(qc, t), th = rdlane(hh, t);
+              const uint32_t g0 = th & 1023u, g1 = (th >> 10) & 1023u, g2 = th >> 20;
+              if (in_cube_rel(cc[s], g0 - (tc & 1023u), g1 - ((tc >> 10) & 1023u),
+                              g2 - (tc >> 20), 2 * g0, 2 * g1, 2 * g2)) {
                 const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(rdlane(a0.x, t)),
                                         __uint_as_float(rdlane(a0.y, t)),
                                         __uint_as_float(rdlane(a0.z, t)));
@@ -796,23 +941,22 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
           j = n;
         }
         if (pub & kPubDone) break;
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(kPollSleep);
       }
     }
     __syncthreads();
     NSFPS_RMARK(kRpDrain);
     const uint32_t npk = s_misc[3], stop = s_misc[4];
-    h0 = s_misc[7] & 1023u;
-    h1 = (s_misc[7] >> 10) & 1023u;
-    h2 = s_misc[7] >> 20;
     // the run's samples to global memory: rows, positions and cubes
     if (wave == 0 && lane < npk) {
-      const uint4 a0 = s_pk[lane][0], a1 = s_pk[lane][1];
+      const uint2 r = s_rec[lane];
+      const uint4 a0 = s_hot[r.x & 255u][0], a1 = s_hot[r.x & 255u][1];
+      const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
       uint32_t lo_c, hi_c;
-      cube_corners(a1.x, a1.y, b0, b1, b2, lo_c, hi_c);
-      out[it + lane] = (int32_t)a0.w;
+      cube_corners(a1.z, hh, b0, b1, b2, lo_c, hi_c);
+      out[it + lane] = (int32_t)a1.y;
       pick_p[np + lane] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
-                                      __uint_as_float(a0.z), __uint_as_float(a1.z));
+                                      __uint_as_float(a0.z), 0.f);
       pick_c[np + lane] = make_uint2(lo_c, hi_c);
     }
     it += npk;
@@ -827,9 +971,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   if (tid == 0) {
     *gptr(c.iter) = it;
     rs.npicks = np;
-    rs.hc[0] = h0;
-    rs.hc[1] = h1;
-    rs.hc[2] = h2;
     rs.kref0 = bkey - 1;  // every key is below the threshold now
     rs.s0 = rs.s0_next;
     rs.nlist = 0;
@@ -862,9 +1003,6 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
     rs.s0_next = kMaxShift;
     rs.npicks = 1;
     rs.nlist = 0;
-    rs.hc[0] = c.r.blocks[0];
-    rs.hc[1] = c.r.blocks[1];
-    rs.hc[2] = c.r.blocks[2];
     rs.rounds = 0;
     rs.err = 0;
     const float4 p0 = *gptr(c.root_pos);

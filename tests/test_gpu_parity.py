@@ -212,6 +212,9 @@ def lattice(k, lo=0.0, hi=1.0):
     # 2,000 distinct points, each 30 times
     ("dup30", np.repeat(np.random.RandomState(11).rand(2000, 3).astype(np.float32), 30, axis=0),
      2500, (0.0, 1.0, 0.0, 1.0, 0.0, 1.0, 32, 32, 32)),
+    # 1024 blocks on one axis: early cubes span the whole axis (half-width 1024)
+    ("blocks1024", np.random.RandomState(14).rand(30000, 3).astype(np.float32), 3000,
+     (0.0, 1.0, 0.0, 1.0, 0.0, 1.0, 1024, 4, 4)),
     # two far clusters: the threshold window must move far between rounds
     ("two_clusters", np.concatenate([np.random.RandomState(12).randn(30000, 3) * 0.01,
                                      np.random.RandomState(13).randn(30000, 3) * 0.01 + 5.0]
