@@ -408,40 +408,36 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 
 // ---------------------------------------------------------------- the run
 
-// One workgroup per cloud, four waves.  Waves 1-3 own the list (kOwnSlots
-// entries per lane), sorted into 64 coarse spatial groups so that the 64
-// entries of one (wave, slot) span a small box of cells.  Wave 0 samples.
+// One workgroup per cloud, four waves; every thread holds kOwnSlots list
+// entries, sorted into 64 coarse spatial groups so that the 64 entries of one
+// (wave, slot) span a small box of cells.
 //
 // The threshold argument is applied once more inside the list: a hot
-// threshold H leaves at most kHot entries at or above it; wave 0 takes a copy
-// of them, one per lane, and samples from them alone -- no barrier, no LDS
-// exchange per sample -- while their maximum key stays >= max(H, B).  Every
-// sample is published in LDS as it is taken, and waves 1-3 apply it to their
-// entries meanwhile (a per-(wave, slot) cell box test skips most of them; the
-// originals of the hot copies get the same updates, min() being idempotent),
-// so when the hot run ends every entry is exact and the next hot set can be
-// chosen.  The run ends when no entry is >= B.
+// threshold H leaves at most kHot entries at or above it, and those are
+// resolved in parallel phases.  Rank the remaining hot copies by key; copy j
+// is "lowered" when the cube of a higher-ranked copy contains it and brings
+// its distance down.  Every copy ranked above the first lowered one is a
+// sample, in rank order: all copies ranked above it are samples too, a copy
+// lowered by one of them started below it, and the rest of the list is below
+// H.  So a phase takes that whole prefix at once, applies its cubes to the
+// remaining copies, and ranks again, until no copy is >= max(H, B).  Then the
+// hot run's samples are applied to every list entry (a per-(wave, slot) cell
+// box test skips most pairs) and the next hot set is chosen.  The run ends
+// when no entry is >= B.
 constexpr uint32_t kRunThreads = 256;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
-constexpr uint32_t kOwnSlots = 6;
+constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
 constexpr uint32_t kHot = 64;
+constexpr uint32_t kQuarter = kRunThreads / kHot;  // threads per hot copy
 constexpr uint32_t kSelBins = 256;
-constexpr uint32_t kBatch = 4;           // samples per hot step at most
-constexpr uint32_t kPubDone = 0x10000u;  // flag in the published sample count
-#ifndef NSFPS_POLL_SLEEP
-#define NSFPS_POLL_SLEEP 4
-#endif
-constexpr int kPollSleep = NSFPS_POLL_SLEEP;  // s_sleep units (64 clocks) between polls
-constexpr uint32_t kLoadSlots = kListCap / kRunThreads;
-static_assert(3 * 64 * kOwnSlots >= kListCap, "owner lanes hold the list");
+static_assert(kOwnSlots == 4 && kQuarter == 4, "the run kernel layout");
 
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
-  kRpLoad = 0, kRpSelect, kRpGather, kRpHot, kRpDrain, kRpTail,
-  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpWords = 16
+  kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail,
+  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWords = 16
 };
-
 
 __device__ __forceinline__ uint32_t spatial_group(uint32_t cell, uint32_t b0, uint32_t b1,
                                                   uint32_t b2) {
@@ -452,16 +448,17 @@ __device__ __forceinline__ uint32_t spatial_group(uint32_t cell, uint32_t b0, ui
          ((gz & 2u) << 4);
 }
 
-// |cell - qc| <= h on every axis, as (cell - qc + h) <= 2h in unsigned
-// arithmetic; o = h - qc per axis.
-__device__ __forceinline__ bool in_cube_rel(uint32_t cell, uint32_t ox, uint32_t oy, uint32_t oz,
-                                            uint32_t wx, uint32_t wy, uint32_t wz) {
-  return (cell & 1023u) + ox <= wx && ((cell >> 10) & 1023u) + oy <= wy &&
-         (cell >> 20) + oz <= wz;
+// Cell inside the cube of a sample at cell qc with packed half-widths h
+// (10 bits per axis): |cell - qc| <= h per axis, as (cell - qc + h) <= 2h in
+// unsigned arithmetic (bitwise, no branches).
+__device__ __forceinline__ bool in_cube_h(uint32_t cell, uint32_t qc, uint32_t h) {
+  const uint32_t h0 = h & 1023u, h1 = (h >> 10) & 1023u, h2 = h >> 20;
+  return ((cell & 1023u) - (qc & 1023u) + h0 <= 2 * h0) &
+         (((cell >> 10) & 1023u) - ((qc >> 10) & 1023u) + h1 <= 2 * h1) &
+         ((cell >> 20) - (qc >> 20) + h2 <= 2 * h2);
 }
 
-// Cube corners of a sample: cell qc, half-widths h (10 bits per axis),
-// clipped to the grid.
+// Cube corners of a sample: cell qc, half-widths h, clipped to the grid.
 __device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b0, uint32_t b1,
                                              uint32_t b2, uint32_t &lo_c, uint32_t &hi_c) {
   const uint32_t qcx = qc & 1023u, qcy = (qc >> 10) & 1023u, qcz = qc >> 20;
@@ -470,19 +467,38 @@ __device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b
   hi_c = pack_cell(min(qcx + g0, b0 - 1), min(qcy + g1, b1 - 1), min(qcz + g2, b2 - 1));
 }
 
+// Cube half-widths of a sample with distance D (src/yuezu_fps.cpp:564-570),
+// packed 10 bits per axis; at or beyond the grid they select the same cells
+// as blocks - 1.
+__device__ __forceinline__ uint32_t packed_halves(const RangeDev &r, float D) {
+  return min((uint32_t)cube_half(D, r.bsize[0], r.blocks[0]), r.blocks[0] - 1) |
+         (min((uint32_t)cube_half(D, r.bsize[1], r.blocks[1]), r.blocks[1] - 1) << 10) |
+         (min((uint32_t)cube_half(D, r.bsize[2], r.blocks[2]), r.blocks[2] - 1) << 20);
+}
+
+// Sum / OR over the four lanes of a quad.
+__device__ __forceinline__ uint32_t quad_sum(uint32_t v) {
+  v += dpp_mov<kDppQuad1032>(v);
+  return v + dpp_mov<kDppQuad2301>(v);
+}
+__device__ __forceinline__ uint32_t quad_min(uint32_t v) {
+  v = min(v, dpp_mov<kDppQuad1032>(v));
+  return min(v, dpp_mov<kDppQuad2301>(v));
+}
+
 template <bool PROF>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
   __shared__ uint4 s_ent[kListCap][2];  // sorted list: {x, y, z, d}, {~rank, row, cell, -}
-  __shared__ uint4 s_hot[kHot][2];      // hot copies, same layout
-  __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy index, half-widths
-  __shared__ uint64_t s_hk[kHot];       // hot keys (ranking)
-  __shared__ uint32_t s_ord[kHot];      // copy index by rank
+  __shared__ uint4 s_hq[kHot];          // hot copies: {cell, half-widths, distance bits, ~rank}
+  __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
+  __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy, half-widths
   __shared__ uint32_t s_cnt[64], s_off[64];
   __shared__ uint32_t s_hist[kSelBins];
   __shared__ uint64_t s_wk[kRunWaves];
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
-  __shared__ uint32_t s_misc[8];
-  __shared__ uint32_t s_pub;
+  __shared__ uint64_t s_wm[kRunWaves];  // per-wave masks (phase accept)
+  __shared__ uint32_t s_wr[kRunWaves][4];
+  __shared__ uint32_t s_misc[4];
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   if (*gptr(c.done)) return;
@@ -505,11 +521,11 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
 
   // ---- list -> LDS in spatial-group order (counting sort)
   {
-    float4 P[kLoadSlots];
-    uint2 R[kLoadSlots];
-    uint32_t C[kLoadSlots], G[kLoadSlots], K[kLoadSlots];
+    float4 P[kOwnSlots];
+    uint2 R[kOwnSlots];
+    uint32_t C[kOwnSlots], G[kOwnSlots], K[kOwnSlots];
 #pragma unroll
-    for (uint32_t s = 0; s < kLoadSlots; ++s) {
+    for (uint32_t s = 0; s < kOwnSlots; ++s) {
       const uint32_t i = s * kRunThreads + tid;
       if (i < nlist) {
         P[s] = gptr(c.list_p)[i];
@@ -526,7 +542,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t s = 0; s < kLoadSlots; ++s) {
+    for (uint32_t s = 0; s < kOwnSlots; ++s) {
       const uint32_t i = s * kRunThreads + tid;
       if (i < nlist) {
         const uint32_t pos = s_off[G[s]] + K[s];
@@ -537,15 +553,15 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     __syncthreads();
   }
-  // owned entries: sorted entry g * 64 + lane with group g = 3 * slot + wave - 1;
+  // owned entries: sorted entry g * 64 + lane with group g = kRunWaves * slot + wave;
   // an empty slot has distance 0 and key 0 and is never live
   float x[kOwnSlots], y[kOwnSlots], z[kOwnSlots], d[kOwnSlots];
   uint32_t lo[kOwnSlots], row[kOwnSlots], cc[kOwnSlots];
   uint32_t blo[kOwnSlots], bhi[kOwnSlots];  // cell box of each (wave, slot), packed corners
 #pragma unroll
   for (uint32_t s = 0; s < kOwnSlots; ++s) {
-    const uint32_t i = (3 * s + wave - 1) * 64 + lane;
-    const bool v = wave > 0 && i < nlist;
+    const uint32_t i = (kRunWaves * s + wave) * 64 + lane;
+    const bool v = i < nlist;
     uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;
     if (v) {
       e0 = s_ent[i][0];
@@ -651,7 +667,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       hth = hth > bkey ? hth : bkey;
     }
     NSFPS_RMARK(kRpSelect);
-    // ---- hot copies -> LDS -> wave 0
+    // ---- hot copies -> LDS
+    uint32_t nhot = 0;
     {
       uint64_t bal[kOwnSlots];
 #pragma unroll
@@ -659,9 +676,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         bal[s] = __ballot(live[s] && key[s] >= hth);
         if (lane == 0) s_wn[wave * kOwnSlots + s] = (uint32_t)__popcll(bal[s]);
       }
-      if (tid == 0) s_pub = 0;
       __syncthreads();
-      uint32_t base = 0, nhot = 0;
+      uint32_t base = 0;
 #pragma unroll
       for (uint32_t j = 0; j < kRunWaves * kOwnSlots; ++j) {
         const uint32_t v = s_wn[j];
@@ -673,294 +689,180 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         if ((bal[s] >> lane) & 1) {
           const uint32_t hi = base + lanes_below(bal[s]);
           if (hi < kHot) {
-            s_hot[hi][0] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
-                                      __float_as_uint(z[s]), __float_as_uint(d[s]));
-            s_hot[hi][1] = make_uint4(lo[s], row[s], cc[s], 0u);
+            s_hq[hi] = make_uint4(cc[s], packed_halves(c.r, d[s]), __float_as_uint(d[s]), lo[s]);
+            s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
+                                  __float_as_uint(z[s]), row[s]);
           } else {  // cannot happen (at most kHot keys are >= the hot threshold)
             rs.err = 2;
           }
         }
         base += (uint32_t)__popcll(bal[s]);
       }
-      if (tid == 0) s_misc[2] = nhot < kHot ? nhot : kHot;
+      nhot = nhot < kHot ? nhot : kHot;
       __syncthreads();
     }
     NSFPS_RMARK(kRpGather);
-    if (wave == 0) {
-      // ---- hot run.  The hot copies are ranked by key once; samples are then
-      // taken down that order.  A copy no cube has touched keeps its key, so
-      // the next sample is the first untouched copy in rank order, or the
-      // largest touched ("dirty") copy when its key is larger.  Ranked, the
-      // copies at or above the hot threshold and those with a distance > 0
-      // are prefixes, and every copy's cube half-widths are computed once up
-      // front; a step then needs no key reads while nothing is dirty.
-      const uint32_t nhot = s_misc[2];
-      uint64_t mykey = 0;  // an idle lane: key 0, ranked after every copy
-      if (lane < nhot)
-        mykey = ((uint64_t)s_hot[lane][0].w << 32) | s_hot[lane][1].x;
-      s_hk[lane] = mykey;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      uint32_t rank = 0;
-#pragma unroll 8
-      for (uint32_t i = 0; i < kHot; ++i) {
-        const uint64_t k = s_hk[i];
-        rank += (k > mykey || (k == mykey && i < lane)) ? 1u : 0u;
+    // ---- phases: thread (j, q) works for hot copy j against copies 16q..16q+15
+    const uint32_t hj = tid / kQuarter, hq = tid % kQuarter;
+    const uint32_t room = m - it;  // samples left (>= 1)
+    const uint32_t th_hi = (uint32_t)(hth >> 32), th_lo = (uint32_t)hth;
+    uint64_t taken = 0;  // hot copies already sampled (uniform)
+    uint32_t npk = 0, stop = 0;
+    while (true) {
+      const uint4 me = s_hq[hj];
+      const uint64_t remm = (nhot >= 64 ? ~0ull : ((1ull << nhot) - 1)) & ~taken;
+      const bool remj = (remm >> hj) & 1;
+      // bit u of cand: copy 16q + u is remaining, ranked above j, and its cube holds j
+      uint32_t cnt = 0, cand = 0;
+#pragma unroll
+      for (uint32_t u = 0; u < kHot / kQuarter; ++u) {
+        const uint32_t i = hq * (kHot / kQuarter) + u;
+        const uint4 o = s_hq[i];
+        const uint32_t gt = (uint32_t)((remm >> i) & 1) &
+                            ((uint32_t)(o.z > me.z) | ((uint32_t)(o.z == me.z) & (uint32_t)(o.w > me.w)));
+        cnt += gt;
+        cand |= (gt & (uint32_t)in_cube_h(me.x, o.x, o.y)) << u;
       }
-      s_ord[rank] = lane;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      const uint32_t src = s_ord[lane];  // lane = rank, src = index of the copy in s_hot
-      const bool real = lane < nhot;
-      uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;
-      if (real) {
-        e0 = s_hot[src][0];
-        e1 = s_hot[src][1];
-      }
-      const float hx = __uint_as_float(e0.x), hy = __uint_as_float(e0.y), hz = __uint_as_float(e0.z);
-      float hd = __uint_as_float(e0.w);
-      const uint32_t hlo = e1.x, hcell = e1.z;
-      const uint32_t hcx = hcell & 1023u, hcy = (hcell >> 10) & 1023u, hcz = hcell >> 20;
-      // cube half-widths of this copy as a sample (src/yuezu_fps.cpp:564-570);
-      // at or beyond the grid they select the same cells as blocks - 1
-      auto halves = [&](float D) {
-        return min((uint32_t)cube_half(D, c.r.bsize[0], b0), b0 - 1) |
-               (min((uint32_t)cube_half(D, c.r.bsize[1], b1), b1 - 1) << 10) |
-               (min((uint32_t)cube_half(D, c.r.bsize[2], b2), b2 - 1) << 20);
-      };
-      uint32_t hpk = halves(hd);
-      const uint64_t hkey = ((uint64_t)__float_as_uint(hd) << 32) | hlo;
-      const uint32_t cut = (uint32_t)__popcll(__ballot(real && hkey >= hth));  // >= hot threshold
-      const uint32_t nz = (uint32_t)__popcll(__ballot(real && hd > 0.0f));     // distance > 0
-      const uint32_t th_hi = uniform((uint32_t)(hth >> 32)), th_lo = uniform((uint32_t)hth);
-      const uint32_t room = uniform(m - it);  // samples left (>= 1)
-      uint64_t avail = nhot >= 64 ? ~0ull : ((1ull << nhot) - 1);  // untouched, not taken
-      uint64_t dirty = 0;
-      uint32_t dl = 64;  // lane of the dirty maximum (64: none)
-      uint32_t dk_hi = 0, dk_lo = 0;
-      uint32_t npk = 0, npub = 0, stop = 0;
-      uint32_t rec_x = 0, rec_y = 0;  // lane j: record of sample j
-      uint32_t kb = kBatch;           // batch width: kBatch, 1 after a conflict, doubling back
-      while (true) {
-        uint64_t taken = 0, touched = 0;
-        uint32_t n = 0, nmax = 0;
-        float nd = hd;
-        if (!dirty) {
-          // ---- batch: the next untouched copies in rank order.  Every copy
-          // ranked above candidate k is taken, and a copy lowered by an earlier
-          // candidate's cube started below it, so candidate k is the maximum
-          // unless an earlier candidate's cube lowered it: the batch is the
-          // prefix of candidates no earlier cube lowered.
-          uint32_t ac[kBatch];
-          uint64_t rest = avail;
-#pragma unroll
-          for (uint32_t k = 0; k < kBatch; ++k) {
-            ac[k] = rest ? (uint32_t)__builtin_ctzll(rest) : 64u;
-            rest &= rest - 1;
-          }
-          if (ac[0] >= cut) {  // hot set exhausted, or below the hot threshold
-            stop = 1;
-            break;
-          }
-          if (ac[0] >= nz) {  // maximum distance 0: src/yuezu_fps.cpp:705-706
-            stop = 2;
-            break;
-          }
-          nmax = 1;
-#pragma unroll
-          for (uint32_t k = 1; k < kBatch; ++k)
-            if (nmax == k && k < kb && ac[k] < cut && ac[k] < nz && npk + k < room) nmax = k + 1;
-          uint32_t qh[kBatch], qsrc[kBatch];
-          uint64_t tk[kBatch];
-          bool dk[kBatch];
-          float ddk[kBatch];
-#pragma unroll
-          for (uint32_t k = 0; k < kBatch; ++k) {
-            tk[k] = 0;
-            dk[k] = false;
-            ddk[k] = 0.f;
-            qh[k] = qsrc[k] = 0;
-            if (k < nmax) {
-              const uint32_t w = ac[k];
-              const float qx = __uint_as_float(rdlane(__float_as_uint(hx), w));
-              const float qy = __uint_as_float(rdlane(__float_as_uint(hy), w));
-              const float qz = __uint_as_float(rdlane(__float_as_uint(hz), w));
-              const uint32_t qc = rdlane(hcell, w);
-              qh[k] = rdlane(hpk, w);
-              qsrc[k] = rdlane(src, w);
-              const uint32_t c0 = qh[k] & 1023u, c1 = (qh[k] >> 10) & 1023u, c2 = qh[k] >> 20;
-              const bool inc = (hcx - (qc & 1023u) + c0 <= 2 * c0) &
-                               (hcy - ((qc >> 10) & 1023u) + c1 <= 2 * c1) &
-                               (hcz - (qc >> 20) + c2 <= 2 * c2);
-              ddk[k] = sqdist(hx, hy, hz, qx, qy, qz);
-              dk[k] = (bool)((avail >> lane) & 1) & inc & (ddk[k] < hd);
-              tk[k] = __ballot(dk[k]);
-            }
-          }
-          n = 1;
-          uint64_t tacc = tk[0];
-#pragma unroll
-          for (uint32_t k = 1; k < kBatch; ++k) {
-            if (n == k && k < nmax && !((tacc >> ac[k]) & 1)) {
-              n = k + 1;
-              tacc |= tk[k];
-            }
-          }
-#pragma unroll
-          for (uint32_t k = 0; k < kBatch; ++k) {
-            if (k < n) {
-              if (lane == npk + k) {
-                rec_x = qsrc[k] | ((qh[k] & 0xfffffu) << 8);
-                rec_y = qh[k] >> 20;
-              }
-              taken |= 1ull << ac[k];
-              touched |= tk[k];
-              nd = dk[k] && ddk[k] < nd ? ddk[k] : nd;
-            }
-          }
-          kb = n < nmax ? 1u : (n == kb ? min(2 * kb, kBatch) : kb);
-        } else {
-          // ---- one sample: the first untouched copy or the dirty maximum
-          const uint32_t al = avail ? (uint32_t)__builtin_ctzll(avail) : 64u;
-          uint32_t ak_hi = 0, ak_lo = 0;
-          if (al < 64) {
-            ak_hi = rdlane(__float_as_uint(hd), al);
-            ak_lo = rdlane(hlo, al);
-          }
-          const bool useb = dl < 64 && (dk_hi > ak_hi || (dk_hi == ak_hi && dk_lo > ak_lo));
-          const uint32_t wl = useb ? dl : al;
-          const uint32_t M = useb ? dk_hi : ak_hi, wlo = useb ? dk_lo : ak_lo;
-          if (wl >= 64 || M < th_hi || (M == th_hi && wlo < th_lo)) {
-            stop = 1;
-            break;
-          }
-          if (M == 0) {
-            stop = 2;
-            break;
-          }
-          const float qx = __uint_as_float(rdlane(__float_as_uint(hx), wl));
-          const float qy = __uint_as_float(rdlane(__float_as_uint(hy), wl));
-          const float qz = __uint_as_float(rdlane(__float_as_uint(hz), wl));
-          const uint32_t qc = rdlane(hcell, wl), qh = rdlane(hpk, wl), qs = rdlane(src, wl);
-          if (lane == npk) {
-            rec_x = qs | ((qh & 0xfffffu) << 8);
-            rec_y = qh >> 20;
-          }
-          n = 1;
-          taken = 1ull << wl;
-          const uint32_t c0 = qh & 1023u, c1 = (qh >> 10) & 1023u, c2 = qh >> 20;
-          const bool inc = (hcx - (qc & 1023u) + c0 <= 2 * c0) &
-                           (hcy - ((qc >> 10) & 1023u) + c1 <= 2 * c1) &
-                           (hcz - (qc >> 20) + c2 <= 2 * c2);
-          const float dd = sqdist(hx, hy, hz, qx, qy, qz);
-          const bool dec = (bool)(((avail | dirty) >> lane) & 1) & inc & (dd < hd);
-          touched = __ballot(dec);
-          nd = dec ? dd : hd;
-          if (useb || ((dirty & ~taken) == 0 && !(touched & ~taken))) kb = kBatch;
-        }
-        npk += n;
-        if (npk - npub >= 8) {  // publish
-          if (lane >= npub && lane < npk) s_rec[lane] = make_uint2(rec_x, rec_y);
-          if (lane == 0)
-            __hip_atomic_store(&s_pub, npk, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-          npub = npk;
-        }
-        if (npk >= room) {  // the last sample needs no update
-          stop = 2;
-          break;
-        }
-        touched &= ~taken;
-        avail &= ~taken;
-        dirty &= ~taken;
-        const bool redo = touched || ((taken & (dl < 64 ? 1ull << dl : 0ull)) && dirty);
-        if (touched) {
-          if ((touched >> lane) & 1) {
-            hd = nd;
-            hpk = halves(hd);
-          }
-          dirty |= touched;
-          avail &= ~touched;
-        }
-        if (redo) {  // the dirty maximum
-          const bool dv = (dirty >> lane) & 1;
-          const uint32_t hi = dv ? __float_as_uint(hd) : 0u;
-          const uint32_t Md = wave_max_u32_s(hi);
-          uint64_t tw = __ballot(dv && hi == Md);
-          if (__popcll(tw) > 1) {
-            const uint32_t L = wave_max_u32_s(dv && hi == Md ? hlo : 0u);
-            tw = __ballot(dv && hi == Md && hlo == L);
-          }
-          dl = tw ? (uint32_t)__ffsll((long long)tw) - 1 : 64u;
-          dk_hi = Md;
-          dk_lo = tw ? rdlane(hlo, dl) : 0u;
+      uint32_t low = 0;
+      if (cand) {  // rare: the exact distance decides
+        const uint4 pj = s_hp[hj];
+        while (cand) {
+          const uint32_t u = (uint32_t)__builtin_ctz(cand);
+          cand &= cand - 1;
+          const uint4 pi = s_hp[hq * (kHot / kQuarter) + u];
+          const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
+                                  __uint_as_float(pj.z), __uint_as_float(pi.x),
+                                  __uint_as_float(pi.y), __uint_as_float(pi.z));
+          low |= dd < __uint_as_float(me.z) ? 1u : 0u;
         }
       }
-      if (lane >= npub && lane < npk) s_rec[lane] = make_uint2(rec_x, rec_y);
+      const uint32_t rank = quad_sum(cnt);
+      const bool lowered = quad_sum(low) != 0;
+      // prefix length: first lowered rank, copies >= the hot threshold, copies
+      // with distance > 0, samples left
+      const bool rep = remj && hq == 0;
+      const bool ge = me.z > th_hi || (me.z == th_hi && me.w >= th_lo);
+      const uint32_t lr = rep && lowered ? rank : 0xffffffffu;
+      const uint32_t wmin = wave_min_u32(lr);
+      const uint32_t wge = (uint32_t)__popcll(__ballot(rep && ge));
+      const uint32_t wnz = (uint32_t)__popcll(__ballot(rep && ge && me.z != 0u));
       if (lane == 0) {
-        s_misc[3] = npk;
-        s_misc[4] = stop;
-        __hip_atomic_store(&s_pub, npk | kPubDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        s_wr[wave][0] = wmin;
+        s_wr[wave][1] = wge;
+        s_wr[wave][2] = wnz;
       }
-      NSFPS_RMARK(kRpHot);
-    } else {
-      // ---- waves 1-3: the published samples to the owned entries, in batches
-      // (lane l holds sample j + l); a slot meets only the samples whose cube
-      // overlaps its cell box.  Wave 0 always publishes the done flag when
-      // its run ends, so this wait ends.
-      uint32_t j = 0;
-      while (true) {
-        const uint32_t pub =
-            uniform(__hip_atomic_load(&s_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
-        const uint32_t n = pub & (kPubDone - 1);
-        if (n > j) {
-          const bool have = lane < n - j;
-          uint4 a0 = make_uint4(0u, 0u, 0u, 0u);
-          uint32_t qc = 0, hh = 0, lo_c = 0, hi_c = 0;
-          if (have) {
-            const uint2 r = s_rec[j + lane];
-            a0 = s_hot[r.x & 255u][0];
-            qc = s_hot[r.x & 255u][1].z;
-            hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
-            cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
-          }
+      __syncthreads();
+      uint32_t P = 0xffffffffu, nge = 0, nnz = 0;
 #pragma unroll
-          for (uint32_t s = 0; s < kOwnSlots; ++s) {
-            uint64_t msk = __ballot(have && cube_overlaps(make_uint2(lo_c, hi_c), blo[s], bhi[s]));
-            while (msk) {
-              const uint32_t t = (uint32_t)__ffsll((long long)msk) - 1;
-              msk &= msk - 1;
-              const uint32_t tc = rdlane(qc, t), th = rdlane(hh, t);
-              const uint32_t g0 = th & 1023u, g1 = (th >> 10) & 1023u, g2 = th >> 20;
-              if (in_cube_rel(cc[s], g0 - (tc & 1023u), g1 - ((tc >> 10) & 1023u),
-                              g2 - (tc >> 20), 2 * g0, 2 * g1, 2 * g2)) {
-                const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(rdlane(a0.x, t)),
-                                        __uint_as_float(rdlane(a0.y, t)),
-                                        __uint_as_float(rdlane(a0.z, t)));
-                d[s] = dd < d[s] ? dd : d[s];
-              }
-            }
-          }
-          j = n;
-        }
-        if (pub & kPubDone) break;
-        __builtin_amdgcn_s_sleep(kPollSleep);
+      for (uint32_t w = 0; w < kRunWaves; ++w) {
+        P = min(P, s_wr[w][0]);
+        nge += s_wr[w][1];
+        nnz += s_wr[w][2];
       }
+      // copies >= the hot threshold are a rank prefix, and so are those with
+      // distance > 0 among them
+      P = min(min(P, nnz), room - npk);
+      if (P == 0) {  // rank 0: below the hot threshold, or distance 0, or no room
+        stop = (nge == 0) ? 1u : 2u;
+        break;
+      }
+      // the prefix: samples npk .. npk + P - 1 in rank order
+      const bool acc = remj && rank < P;
+      if (acc && hq == 0) s_rec[npk + rank] = make_uint2(hj | ((me.y & 0xfffffu) << 8), me.y >> 20);
+      const uint64_t am = __ballot(acc && hq == 0);
+      // quad leaders are lanes 0, 4, ..., 60 of the wave: copy 16 * wave + lane / 4
+      uint64_t amc = 0;
+#pragma unroll
+      for (uint32_t k = 0; k < 16; ++k) amc |= ((am >> (4 * k)) & 1ull) << k;
+      if (lane == 0) s_wm[wave] = amc << (16 * wave);
+      __syncthreads();
+      uint64_t accm = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kRunWaves; ++w) accm |= s_wm[w];
+      taken |= accm;
+      npk += P;
+      if (npk >= room) {  // the last sample needs no update
+        stop = 2;
+        break;
+      }
+      if (P >= nnz && nnz < nge) {  // the next copy has distance 0: src/yuezu_fps.cpp:705-706
+        stop = 2;
+        break;
+      }
+      // the accepted cubes on the remaining copies
+      const bool remj2 = hj < nhot && !((taken >> hj) & 1);
+      uint32_t mnb = 0xffffffffu;
+      {
+        const uint32_t am2 = (uint32_t)(accm >> (hq * (kHot / kQuarter))) & 0xffffu;
+        uint32_t cand2 = 0;
+        if (remj2) {
+#pragma unroll
+          for (uint32_t u = 0; u < kHot / kQuarter; ++u) {
+            const uint4 o = s_hq[hq * (kHot / kQuarter) + u];
+            cand2 |= (((am2 >> u) & 1u) & (uint32_t)in_cube_h(me.x, o.x, o.y)) << u;
+          }
+        }
+        if (cand2) {  // rare: the exact distances
+          const uint4 pj = s_hp[hj];
+          while (cand2) {
+            const uint32_t u = (uint32_t)__builtin_ctz(cand2);
+            cand2 &= cand2 - 1;
+            const uint4 pi = s_hp[hq * (kHot / kQuarter) + u];
+            const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
+                                    __uint_as_float(pj.z), __uint_as_float(pi.x),
+                                    __uint_as_float(pi.y), __uint_as_float(pi.z));
+            mnb = min(mnb, __float_as_uint(dd));  // non-negative floats order like their bits
+          }
+        }
+      }
+      mnb = quad_min(mnb);
+      __syncthreads();  // every thread has read s_hq
+      if (remj2 && hq == 0 && mnb < me.z) {
+        s_hq[hj] = make_uint4(me.x, packed_halves(c.r, __uint_as_float(mnb)), mnb, me.w);
+      }
+      __syncthreads();
+      if (PROF) pf[kRpPhaseCount] += 1;
     }
-    __syncthreads();
-    NSFPS_RMARK(kRpDrain);
-    const uint32_t npk = s_misc[3], stop = s_misc[4];
-    // the run's samples to global memory: rows, positions and cubes
-    if (wave == 0 && lane < npk) {
-      const uint2 r = s_rec[lane];
-      const uint4 a0 = s_hot[r.x & 255u][0], a1 = s_hot[r.x & 255u][1];
-      const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
-      uint32_t lo_c, hi_c;
-      cube_corners(a1.z, hh, b0, b1, b2, lo_c, hi_c);
-      out[it + lane] = (int32_t)a1.y;
-      pick_p[np + lane] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
-                                      __uint_as_float(a0.z), 0.f);
-      pick_c[np + lane] = make_uint2(lo_c, hi_c);
+    NSFPS_RMARK(kRpPhases);
+    // ---- the hot run's samples to every owned entry (pairs whose cube meets
+    // the (wave, slot) cell box), and to global memory
+    {
+      const bool have = lane < npk;
+      uint4 a0 = make_uint4(0u, 0u, 0u, 0u);
+      uint32_t qc = 0, hh = 0, lo_c = 0, hi_c = 0;
+      if (have) {
+        const uint2 r = s_rec[lane];
+        const uint32_t cp = r.x & 255u;
+        a0 = s_hp[cp];
+        qc = s_hq[cp].x;
+        hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+        cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
+        if (wave == 0) {
+          out[it + lane] = (int32_t)a0.w;
+          pick_p[np + lane] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
+                                          __uint_as_float(a0.z), 0.f);
+          pick_c[np + lane] = make_uint2(lo_c, hi_c);
+        }
+      }
+#pragma unroll
+      for (uint32_t s = 0; s < kOwnSlots; ++s) {
+        uint64_t msk = __ballot(have && cube_overlaps(make_uint2(lo_c, hi_c), blo[s], bhi[s]));
+        while (msk) {
+          const uint32_t t = (uint32_t)__builtin_ctzll(msk);
+          msk &= msk - 1;
+          if (in_cube_h(cc[s], rdlane(qc, t), rdlane(hh, t))) {
+            const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(rdlane(a0.x, t)),
+                                    __uint_as_float(rdlane(a0.y, t)),
+                                    __uint_as_float(rdlane(a0.z, t)));
+            d[s] = dd < d[s] ? dd : d[s];
+          }
+        }
+      }
     }
     it += npk;
     np += npk;
+    __syncthreads();  // s_hq / s_hp / s_rec are rewritten by the next hot set
+    NSFPS_RMARK(kRpApply);
     if (PROF) pf[kRpHotRounds] += 1;
     if (stop == 2) {
       done = true;
