@@ -3,10 +3,16 @@
 
 Metric: FPS ms per call and samples/s at 1,048,576 points -> 65,536 samples
 (uniform cube in [-1,1]^3, 32^3 blocks, start index 0), plus the fraction of
-the HBM roofline reached by the dominant kernel (the single-workgroup sampling
-loop).  A "step" is one complete FPS call on device-resident input: structure
-build (cell keys, radix sorts, leaves) + the whole sampling loop + the int32
-indices written to device memory.
+the HBM roofline reached by the sampling pass.  A "step" is one complete FPS
+call on device-resident input: structure build (cell keys, radix sorts,
+leaves) + the whole sampling pass + the int32 indices written to device
+memory.
+
+Roofline: the sampling pass (speculative-run rounds: k_update, k_refine,
+k_gather, k_run) moves the reference's algorithmic bytes -- 16 B per
+candidate point and 8 B per candidate 16-point leaf of every iteration, the
+per-iteration census in tests/golden/census.npz -- in the hipEvent-timed
+sample_ms of the call.
 
 Prints ONE JSON line (rank 0).  With --all it first prints one extra line per
 workload (informational), the contract line always comes last.
@@ -64,10 +70,10 @@ def golden_hashes(wname):
         return json.load(f).get(wname)
 
 
-def profile_traffic(kernel="k_late_loop", wname="uniform_cube"):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    PMC summary (FETCH_SIZE and WRITE_SIZE in KiB, calibrated by a copy kernel
-    of known size); None when no summary was committed."""
+def profile_traffic(kernel="sampling", wname="uniform_cube"):
+    """HBM bytes per call of the sampling pass from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE in KiB, calibrated by a copy kernel of
+    known size); None when no summary was committed."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_{wname}_pmc.txt")
     if not os.path.exists(path):
         return None
@@ -161,6 +167,9 @@ def main():
     ap.add_argument("--workload", default="uniform_cube")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also print a line per workload")
+    ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device (a copy kernel of known size for "
+                         "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this FPS path runs on exactly one GPU: a single cloud's "
@@ -177,6 +186,13 @@ def main():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
     hip = Hip()
+    if args.calibrate:
+        nbytes = args.calibrate << 20
+        src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+        hip.memcpy_d2d(dst, src, nbytes)
+        hip.synchronize()
+        hip.free(src)
+        hip.free(dst)
 
     if args.all:
         for wname in ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]:
@@ -212,21 +228,20 @@ def main():
     m = int(w["n_samples"])
     g = golden_hashes(args.workload)
     exact = g is not None and digest == g["output_sha256"][0] and len(out) == g["lengths"][0]
-    late = [s["late_ms"] for s in stats]
-    late_ms = statistics.mean(late)
-    wide_iters = int(stats[-1]["wide_iters"])
+    sample_ms = statistics.mean(s["sample_ms"] for s in stats)
     census = load_census(args.workload)
     roofline = None
-    if census is not None and census["cum"] is not None and wide_iters < len(census["cum"]):
-        # bytes of the iterations the loop kernel performs: all of them after
-        # the grid-wide ones (entry 0 of the census is the first full pass)
-        alg = census["total"] - int(census["cum"][wide_iters])
-        achieved = alg / (late_ms * 1e6)  # GB/s
+    engine = "runs" if stats[-1].get("engine", 0) else "tree"
+    if census is not None:
+        alg = census["total"]  # every iteration, first pass included
+        achieved = alg / (sample_ms * 1e6)  # GB/s
         roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
-                    "traffic": profile_traffic("k_late_loop", args.workload),
-                    "kernel": "k_late_loop", "alg_bytes_per_launch": alg,
-                    "kernel_ms": round(late_ms, 3)}
+                    "traffic": profile_traffic("sampling", args.workload),
+                    "kernel": "sampling pass (k_update+k_refine+k_gather+k_run rounds)"
+                    if engine == "runs" else "k_wide_update+k_late_loop",
+                    "alg_bytes_per_launch": alg, "kernel_ms": round(sample_ms, 3)}
+    wide_iters = int(stats[-1]["wide_iters"])
     line = {
         "metric": "FPS ms/call & samples/s at 1M pts -> 65,536 samples; % of HBM roofline",
         "value": round(len(out) / (ms / 1e3), 2),
@@ -240,7 +255,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded uniform cube, NumPy RandomState(2))",
-        "config": workload_config(w, {"wide_iters": wide_iters,
+        "config": workload_config(w, {"engine": engine, "rounds": int(stats[-1].get("rounds", 0)),
+                                      "wide_iters": wide_iters,
                                       "device_ms": round(statistics.mean(s["device_ms"] for s in stats), 3),
                                       "build_ms": round(statistics.mean(s["build_ms"] for s in stats), 3),
                                       "bit_exact_vs_reference": exact}),

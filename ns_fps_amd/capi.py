@@ -155,5 +155,9 @@ class Hip:
                                        self.D2H), "hipMemcpy")
         return out
 
+    def memcpy_d2d(self, dst, src, nbytes):
+        self._ck(self.rt.hipMemcpy(_vp(dst), _vp(src), ctypes.c_size_t(nbytes), self.D2D),
+                 "hipMemcpy")
+
     def synchronize(self):
         self._ck(self.rt.hipDeviceSynchronize(), "hipDeviceSynchronize")
