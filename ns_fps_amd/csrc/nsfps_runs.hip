@@ -409,8 +409,10 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // ---------------------------------------------------------------- the run
 
 // One workgroup per cloud, four waves; every thread holds kOwnSlots list
-// entries, sorted into 64 coarse spatial groups so that the 64 entries of one
-// (wave, slot) span a small box of cells.
+// entries.  The list sits in LDS sorted by coarse cell (x >> sx, y >> sy,
+// z >> sz; at most kCells of them) with the first entry of every coarse cell,
+// so the entries inside a cube are found by walking, for each coarse (y, z)
+// row the cube spans, the entries of its x range.
 //
 // The threshold argument is applied once more inside the list: a hot
 // threshold H leaves at most kHot entries at or above it, and those are
@@ -421,32 +423,28 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // lowered by one of them started below it, and the rest of the list is below
 // H.  So a phase takes that whole prefix at once, applies its cubes to the
 // remaining copies, and ranks again, until no copy is >= max(H, B).  Then the
-// hot run's samples are applied to every list entry (a per-(wave, slot) cell
-// box test skips most pairs) and the next hot set is chosen.  The run ends
-// when no entry is >= B.
+// hot run's samples are applied to every list entry (a
+// sample with a small cube is applied by one quad walking its rows of the
+// cell index, one with a large cube by every thread to its own entries) and
+// the next hot set is chosen.  The run ends when no entry is >= B.
 constexpr uint32_t kRunThreads = 256;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
 constexpr uint32_t kHot = 64;
 constexpr uint32_t kQuarter = kRunThreads / kHot;  // threads per hot copy
 constexpr uint32_t kSelBins = 256;
+constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
+constexpr uint32_t kQuadRows = 64;     // cubes over more coarse rows, or over more
+constexpr uint32_t kQuadEntries = 32;  // list entries, are applied by every thread
 static_assert(kOwnSlots == 4 && kQuarter == 4, "the run kernel layout");
+static_assert(kCells == 16 * kRunThreads, "the cell scan takes 16 cells per thread");
 
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
-  kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail,
+  kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail, kRpBig,
   kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWords = 16
 };
-
-__device__ __forceinline__ uint32_t spatial_group(uint32_t cell, uint32_t b0, uint32_t b1,
-                                                  uint32_t b2) {
-  // 4 x 4 x 4 boxes of cells, Morton-ordered
-  const uint32_t gx = ((cell & 1023u) * 4u) / b0, gy = (((cell >> 10) & 1023u) * 4u) / b1,
-                 gz = ((cell >> 20) * 4u) / b2;
-  return (gx & 1u) | ((gy & 1u) << 1) | ((gz & 1u) << 2) | ((gx & 2u) << 2) | ((gy & 2u) << 3) |
-         ((gz & 2u) << 4);
-}
 
 // Cell inside the cube of a sample at cell qc with packed half-widths h
 // (10 bits per axis): |cell - qc| <= h per axis, as (cell - qc + h) <= 2h in
@@ -488,17 +486,21 @@ __device__ __forceinline__ uint32_t quad_min(uint32_t v) {
 
 template <bool PROF>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  __shared__ uint4 s_ent[kListCap][2];  // sorted list: {x, y, z, d}, {~rank, row, cell, -}
+  __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, fine cell}
+  __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
+  __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
   __shared__ uint4 s_hq[kHot];          // hot copies: {cell, half-widths, distance bits, ~rank}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
   __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy, half-widths
-  __shared__ uint32_t s_cnt[64], s_off[64];
+  __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
+  __shared__ uint32_t s_big[2];                         // samples with large cubes
   __shared__ uint32_t s_hist[kSelBins];
   __shared__ uint64_t s_wk[kRunWaves];
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
   __shared__ uint64_t s_wm[kRunWaves];  // per-wave masks (phase accept)
   __shared__ uint32_t s_wr[kRunWaves][4];
   __shared__ uint32_t s_misc[4];
+  __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   if (*gptr(c.done)) return;
@@ -514,12 +516,28 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   } while (0)
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   const uint32_t b0 = c.r.blocks[0], b1 = c.r.blocks[1], b2 = c.r.blocks[2];
-  if (tid < 64) s_cnt[tid] = 0;
+  // coarse cells (x >> sx, y >> sy, z >> sz), at most kCells of them: the
+  // longest coarse axis is halved until they fit
+  uint32_t sx = 0, sy = 0, sz = 0;
+  while (true) {
+    const uint32_t ex = ((b0 - 1) >> sx) + 1, ey = ((b1 - 1) >> sy) + 1, ez = ((b2 - 1) >> sz) + 1;
+    if (ex * ey * ez <= kCells) break;
+    if (ex >= ey && ex >= ez) ++sx;
+    else if (ey >= ez) ++sy;
+    else ++sz;
+  }
+  const uint32_t ncx = ((b0 - 1) >> sx) + 1, ncy = ((b1 - 1) >> sy) + 1;
+  for (uint32_t j = tid; j < kCells + 4; j += kRunThreads) s_cell[j] = 0;
+  if (tid == 0) {
+    s_geo[0] = sx | (sy << 8) | (sz << 16);
+    s_geo[1] = ncx;
+    s_geo[2] = ncy;
+  }
   const uint32_t nlist = min(rs.nlist, kListCap);
   const uint64_t bkey = rs.bkey;
   __syncthreads();
 
-  // ---- list -> LDS in spatial-group order (counting sort)
+  // ---- list -> LDS in coarse-cell order (counting sort)
   {
     float4 P[kOwnSlots];
     uint2 R[kOwnSlots];
@@ -531,54 +549,67 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         P[s] = gptr(c.list_p)[i];
         R[s] = gptr(c.list_r)[i];
         C[s] = gptr(c.list_c)[i];
-        G[s] = spatial_group(C[s], b0, b1, b2);
-        K[s] = atomicAdd(&s_cnt[G[s]], 1u);
+        G[s] = (((C[s] >> 20) >> sz) * ncy + (((C[s] >> 10) & 1023u) >> sy)) * ncx +
+               ((C[s] & 1023u) >> sx);
+        K[s] = atomicAdd(&s_cell[G[s]], 1u);
       }
     }
     __syncthreads();
-    if (wave == 0) {
-      const uint32_t v = s_cnt[lane];
-      s_off[lane] = wave_incl_scan(v) - v;
+    {  // exclusive scan of the cell counts, cells 16 tid .. 16 tid + 15 per thread
+      uint4 v[4];
+      uint32_t sum = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        v[j] = reinterpret_cast<const uint4 *>(s_cell)[4 * tid + j];
+        sum += v[j].x + v[j].y + v[j].z + v[j].w;
+      }
+      uint32_t tot;
+      uint32_t pre = block_excl_scan<kRunWaves>(sum, s_wn, &tot);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint4 o = make_uint4(pre, pre + v[j].x, pre + v[j].x + v[j].y,
+                                   pre + v[j].x + v[j].y + v[j].z);
+        pre += v[j].x + v[j].y + v[j].z + v[j].w;
+        reinterpret_cast<uint4 *>(s_cell)[4 * tid + j] = o;
+      }
+      if (tid == 0) s_cell[kCells] = tot;
     }
     __syncthreads();
 #pragma unroll
     for (uint32_t s = 0; s < kOwnSlots; ++s) {
       const uint32_t i = s * kRunThreads + tid;
       if (i < nlist) {
-        const uint32_t pos = s_off[G[s]] + K[s];
-        s_ent[pos][0] = make_uint4(__float_as_uint(P[s].x), __float_as_uint(P[s].y),
-                                   __float_as_uint(P[s].z), __float_as_uint(P[s].w));
-        s_ent[pos][1] = make_uint4(~R[s].x, R[s].y, C[s], 0u);
+        const uint32_t pos = s_cell[G[s]] + K[s];
+        s_pc[pos] = make_uint4(__float_as_uint(P[s].x), __float_as_uint(P[s].y),
+                               __float_as_uint(P[s].z), C[s]);
+        s_dd[pos] = __float_as_uint(P[s].w);
+        s_rk[pos] = make_uint2(~R[s].x, R[s].y);
       }
     }
     __syncthreads();
   }
-  // owned entries: sorted entry g * 64 + lane with group g = kRunWaves * slot + wave;
-  // an empty slot has distance 0 and key 0 and is never live
+  // owned entries: sorted entry s * kRunThreads + tid; an empty slot has
+  // distance 0 and key 0 and is never live
   float x[kOwnSlots], y[kOwnSlots], z[kOwnSlots], d[kOwnSlots];
   uint32_t lo[kOwnSlots], row[kOwnSlots], cc[kOwnSlots];
-  uint32_t blo[kOwnSlots], bhi[kOwnSlots];  // cell box of each (wave, slot), packed corners
 #pragma unroll
   for (uint32_t s = 0; s < kOwnSlots; ++s) {
-    const uint32_t i = (kRunWaves * s + wave) * 64 + lane;
-    const bool v = i < nlist;
-    uint4 e0 = make_uint4(0u, 0u, 0u, 0u), e1 = e0;
-    if (v) {
-      e0 = s_ent[i][0];
-      e1 = s_ent[i][1];
+    const uint32_t i = s * kRunThreads + tid;
+    uint4 e0 = make_uint4(0u, 0u, 0u, 0u);
+    uint2 e1 = make_uint2(0u, 0u);
+    uint32_t e2 = 0;
+    if (i < nlist) {
+      e0 = s_pc[i];
+      e1 = s_rk[i];
+      e2 = s_dd[i];
     }
     x[s] = __uint_as_float(e0.x);
     y[s] = __uint_as_float(e0.y);
     z[s] = __uint_as_float(e0.z);
-    d[s] = __uint_as_float(e0.w);
+    cc[s] = e0.w;
+    d[s] = __uint_as_float(e2);
     lo[s] = e1.x;
     row[s] = e1.y;
-    cc[s] = e1.z;
-    const uint32_t cx = e1.z & 1023u, cy = (e1.z >> 10) & 1023u, cz = e1.z >> 20;
-    blo[s] = pack_cell(wave_min_u32(v ? cx : 1023u), wave_min_u32(v ? cy : 1023u),
-                       wave_min_u32(v ? cz : 1023u));
-    bhi[s] = pack_cell(wave_max_u32(v ? cx : 0u), wave_max_u32(v ? cy : 0u),
-                       wave_max_u32(v ? cz : 0u));
   }
   uint32_t it = *gptr(c.iter);
   const uint32_t m = c.m;
@@ -699,6 +730,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         base += (uint32_t)__popcll(bal[s]);
       }
       nhot = nhot < kHot ? nhot : kHot;
+      if (tid < 2) s_big[tid] = 0;
       __syncthreads();
     }
     NSFPS_RMARK(kRpGather);
@@ -824,40 +856,108 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       if (PROF) pf[kRpPhaseCount] += 1;
     }
     NSFPS_RMARK(kRpPhases);
-    // ---- the hot run's samples to every owned entry (pairs whose cube meets
-    // the (wave, slot) cell box), and to global memory
+    // ---- the hot run's samples -> global memory and every list entry.
+    // Quad k takes sample k: a cube whose coarse cells span at most kQuadRows
+    // rows and hold at most kQuadEntries list entries is applied by walking
+    // those rows of the cell index (distances min-ed into LDS); a larger one
+    // is flagged and applied below by every thread to its own entries.
     {
-      const bool have = lane < npk;
-      uint4 a0 = make_uint4(0u, 0u, 0u, 0u);
-      uint32_t qc = 0, hh = 0, lo_c = 0, hi_c = 0;
-      if (have) {
-        const uint2 r = s_rec[lane];
+      const uint32_t k = tid / kQuarter, q = tid % kQuarter;
+      if (k < npk) {
+        // kept in vector registers: the scalar file is full here
+        const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
+        const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
+        const uint2 r = s_rec[k];
         const uint32_t cp = r.x & 255u;
-        a0 = s_hp[cp];
-        qc = s_hq[cp].x;
-        hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+        const uint4 a0 = s_hp[cp];
+        const uint32_t qc = s_hq[cp].x;
+        const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+        uint32_t lo_c, hi_c;
         cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
-        if (wave == 0) {
-          out[it + lane] = (int32_t)a0.w;
-          pick_p[np + lane] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
-                                          __uint_as_float(a0.z), 0.f);
-          pick_c[np + lane] = make_uint2(lo_c, hi_c);
+        if (q == 0) {
+          out[it + k] = (int32_t)a0.w;
+          pick_p[np + k] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
+                                       __uint_as_float(a0.z), 0.f);
+          pick_c[np + k] = make_uint2(lo_c, hi_c);
         }
-      }
-#pragma unroll
-      for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        uint64_t msk = __ballot(have && cube_overlaps(make_uint2(lo_c, hi_c), blo[s], bhi[s]));
-        while (msk) {
-          const uint32_t t = (uint32_t)__builtin_ctzll(msk);
-          msk &= msk - 1;
-          if (in_cube_h(cc[s], rdlane(qc, t), rdlane(hh, t))) {
-            const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(rdlane(a0.x, t)),
-                                    __uint_as_float(rdlane(a0.y, t)),
-                                    __uint_as_float(rdlane(a0.z, t)));
-            d[s] = dd < d[s] ? dd : d[s];
+        const uint32_t x0 = (lo_c & 1023u) >> gsx, x1 = (hi_c & 1023u) >> gsx;
+        const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
+        const uint32_t z0 = (lo_c >> 20) >> gsz, z1 = (hi_c >> 20) >> gsz;
+        const uint32_t ny = y1 - y0 + 1, nrows = ny * (z1 - z0 + 1);
+        uint32_t ry0 = q, rz0 = 0;  // first row of this lane
+        while (ry0 >= ny) {
+          ry0 -= ny;
+          ++rz0;
+        }
+        uint32_t cnt = 0;  // list entries in the coarse cells of the cube
+        if (nrows <= kQuadRows) {
+          uint32_t ry = ry0, rz = rz0;
+          for (uint32_t rr = q; rr < nrows; rr += kQuarter) {
+            const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
+            cnt += s_cell[rw + x1 + 1] - s_cell[rw + x0];
+            ry += kQuarter;
+            while (ry >= ny) {
+              ry -= ny;
+              ++rz;
+            }
+          }
+        }
+        cnt = quad_sum(cnt);
+        if (nrows > kQuadRows || cnt > kQuadEntries) {
+          if (q == 0) atomicOr(&s_big[k >> 5], 1u << (k & 31u));
+        } else if (cnt) {
+          const float px = __uint_as_float(a0.x), py = __uint_as_float(a0.y),
+                      pz = __uint_as_float(a0.z);
+          uint32_t ry = ry0, rz = rz0;
+          for (uint32_t rr = q; rr < nrows; rr += kQuarter) {
+            const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
+            const uint32_t e1 = s_cell[rw + x1 + 1];
+            for (uint32_t e = s_cell[rw + x0]; e < e1; ++e) {
+              const uint4 p = s_pc[e];
+              if (in_cube_h(p.w, qc, hh)) {
+                const uint32_t dd =
+                    __float_as_uint(sqdist(__uint_as_float(p.x), __uint_as_float(p.y),
+                                           __uint_as_float(p.z), px, py, pz));
+                atomicMin(&s_dd[e], dd);  // non-negative floats order like their bits
+              }
+            }
+            ry += kQuarter;
+            while (ry >= ny) {
+              ry -= ny;
+              ++rz;
+            }
           }
         }
       }
+      __syncthreads();  // the quads' updates are in LDS
+#pragma unroll
+      for (uint32_t s = 0; s < kOwnSlots; ++s)
+        if (s * kRunThreads + tid < nlist) d[s] = __uint_as_float(s_dd[s * kRunThreads + tid]);
+      NSFPS_RMARK(kRpApply);
+      uint64_t bigm = ((uint64_t)uniform(s_big[1]) << 32) | uniform(s_big[0]);
+      if (bigm) {
+        while (bigm) {
+          const uint32_t kb = (uint32_t)__builtin_ctzll(bigm);
+          bigm &= bigm - 1;
+          const uint2 r = s_rec[kb];
+          const uint32_t cp = r.x & 255u;
+          const uint4 a0 = s_hp[cp];
+          const uint32_t qc = s_hq[cp].x;
+          const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+#pragma unroll
+          for (uint32_t s = 0; s < kOwnSlots; ++s) {
+            if (in_cube_h(cc[s], qc, hh)) {
+              const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
+                                      __uint_as_float(a0.y), __uint_as_float(a0.z));
+              d[s] = dd < d[s] ? dd : d[s];
+            }
+          }
+        }
+#pragma unroll
+        for (uint32_t s = 0; s < kOwnSlots; ++s)
+          if (s * kRunThreads + tid < nlist) s_dd[s * kRunThreads + tid] = __float_as_uint(d[s]);
+      }
+      NSFPS_RMARK(kRpBig);
     }
     it += npk;
     np += npk;
