@@ -442,7 +442,7 @@ static_assert(kCells == 16 * kRunThreads, "the cell scan takes 16 cells per thre
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
-  kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail, kRpBig,
+  kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail, kRpBig, kRpRank,
   kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWords = 16
 };
 
@@ -454,6 +454,25 @@ __device__ __forceinline__ bool in_cube_h(uint32_t cell, uint32_t qc, uint32_t h
   return ((cell & 1023u) - (qc & 1023u) + h0 <= 2 * h0) &
          (((cell >> 10) & 1023u) - ((qc >> 10) & 1023u) + h1 <= 2 * h1) &
          ((cell >> 20) - (qc >> 20) + h2 <= 2 * h2);
+}
+
+// Cells packed 11 bits per axis (x | y << 11 | z << 22): bits 10 and 21 stay
+// clear and act as guards, so lo <= c <= hi on all three axes takes two
+// subtractions.  cg = pack11(c) | kGuards, c11 = pack11(c), hig = pack11(hi) |
+// kGuards.  Per axis, cg - lo keeps its guard bit (or, for z, does not borrow)
+// exactly when c >= lo, and hig - c11 likewise when c <= hi.
+constexpr uint32_t kGuards = (1u << 10) | (1u << 21);
+
+__device__ __forceinline__ uint32_t pack11(uint32_t c10) {
+  return (c10 & 1023u) | (((c10 >> 10) & 1023u) << 11) | ((c10 >> 20) << 22);
+}
+
+__device__ __forceinline__ uint32_t in_box11(uint32_t cg, uint32_t c11, uint32_t lo,
+                                             uint32_t hig) {
+  uint32_t t1, t2;
+  const bool b1 = __builtin_usub_overflow(cg, lo, &t1);
+  const bool b2 = __builtin_usub_overflow(hig, c11, &t2);
+  return (uint32_t)(((t1 & t2 & kGuards) == kGuards) & !b1 & !b2);
 }
 
 // Cube corners of a sample: cell qc, half-widths h, clipped to the grid.
@@ -474,6 +493,10 @@ __device__ __forceinline__ uint32_t packed_halves(const RangeDev &r, float D) {
          (min((uint32_t)cube_half(D, r.bsize[2], r.blocks[2]), r.blocks[2] - 1) << 20);
 }
 
+// LDS slot of hot copy i: the copies a quarter reads together (u, 16 + u,
+// 32 + u, 48 + u) sit side by side, so one read by a wave touches distinct banks.
+__device__ __forceinline__ uint32_t hot_slot(uint32_t i) { return ((i & 15u) << 2) | (i >> 4); }
+
 // Sum / OR over the four lanes of a quad.
 __device__ __forceinline__ uint32_t quad_sum(uint32_t v) {
   v += dpp_mov<kDppQuad1032>(v);
@@ -489,7 +512,13 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, fine cell}
   __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
   __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
-  __shared__ uint4 s_hq[kHot];          // hot copies: {cell, half-widths, distance bits, ~rank}
+  __shared__ uint4 s_hq[2][kHot];       // hot copies at hot_slot(i), one buffer per phase parity:
+                                        //   {pack11(cube lo), pack11(cube hi) | guards, ~rank,
+                                        //   distance bits}; key 0 once taken
+  __shared__ __align__(16) uint32_t s_rank[kHot];  // rank of each hot copy in the phase
+  __shared__ unsigned long long s_lowm[2];  // bit r: the copy ranked r is lowered
+  __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
+                                        //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
   __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy, half-widths
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
@@ -497,8 +526,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint32_t s_hist[kSelBins];
   __shared__ uint64_t s_wk[kRunWaves];
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
-  __shared__ uint64_t s_wm[kRunWaves];  // per-wave masks (phase accept)
-  __shared__ uint32_t s_wr[kRunWaves][4];
+  __shared__ uint32_t s_wr[2][kRunWaves][2];
   __shared__ uint32_t s_misc[4];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
   const CloudDev &c = clouds[blockIdx.x];
@@ -719,8 +747,9 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
         if ((bal[s] >> lane) & 1) {
           const uint32_t hi = base + lanes_below(bal[s]);
-          if (hi < kHot) {
-            s_hq[hi] = make_uint4(cc[s], packed_halves(c.r, d[s]), __float_as_uint(d[s]), lo[s]);
+          if (hi < kHot) {  // the cube corners follow below, one copy per thread
+            s_hq[0][hot_slot(hi)] = make_uint4(0u, 0u, lo[s], __float_as_uint(d[s]));
+            s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), 0u);
             s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
                                   __float_as_uint(z[s]), row[s]);
           } else {  // cannot happen (at most kHot keys are >= the hot threshold)
@@ -730,30 +759,45 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         base += (uint32_t)__popcll(bal[s]);
       }
       nhot = nhot < kHot ? nhot : kHot;
+      if (tid >= nhot && tid < kHot) s_hq[0][hot_slot(tid)] = make_uint4(0u, 0u, 0u, 0u);  // unused
       if (tid < 2) s_big[tid] = 0;
+      if (tid == 0) s_lowm[0] = 0;
+      __syncthreads();
+      if (tid < nhot) {
+        const uint4 hq0 = s_hq[0][hot_slot(tid)];
+        const uint32_t cl = s_hx[tid].x;
+        const uint32_t h = packed_halves(c.r, __uint_as_float(hq0.w));
+        uint32_t lo_c, hi_c;
+        cube_corners(cl, h, b0, b1, b2, lo_c, hi_c);
+        s_hq[0][hot_slot(tid)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hq0.z, hq0.w);
+        s_hx[tid].w = h;
+      }
       __syncthreads();
     }
     NSFPS_RMARK(kRpGather);
     // ---- phases: thread (j, q) works for hot copy j against copies 16q..16q+15
     const uint32_t hj = tid / kQuarter, hq = tid % kQuarter;
     const uint32_t room = m - it;  // samples left (>= 1)
-    const uint32_t th_hi = (uint32_t)(hth >> 32), th_lo = (uint32_t)hth;
-    uint64_t taken = 0;  // hot copies already sampled (uniform)
-    uint32_t npk = 0, stop = 0;
+    // Per phase, two barriers: after the ranks (the accepted prefix is known),
+    // and after the next buffer of hot copies is written.
+    uint32_t npk = 0, stop = 0, ph = 0;
     while (true) {
-      const uint4 me = s_hq[hj];
-      const uint64_t remm = (nhot >= 64 ? ~0ull : ((1ull << nhot) - 1)) & ~taken;
-      const bool remj = (remm >> hj) & 1;
+      const uint4 me = s_hq[ph][hot_slot(hj)];
+      const uint4 mx = s_hx[hj];
+      // the 16 copies of this quarter, all loads issued before any use
+      uint4 og[kHot / kQuarter];
+#pragma unroll
+      for (uint32_t u = 0; u < kHot / kQuarter; ++u) og[u] = s_hq[ph][4 * u + hq];  // copy 16 hq + u
+      __builtin_amdgcn_sched_barrier(0);
+      const uint64_t mkey = ((uint64_t)me.w << 32) | me.z;
+      const bool remj = mkey != 0;  // copies taken earlier, and unused slots, have key 0
       // bit u of cand: copy 16q + u is remaining, ranked above j, and its cube holds j
       uint32_t cnt = 0, cand = 0;
 #pragma unroll
       for (uint32_t u = 0; u < kHot / kQuarter; ++u) {
-        const uint32_t i = hq * (kHot / kQuarter) + u;
-        const uint4 o = s_hq[i];
-        const uint32_t gt = (uint32_t)((remm >> i) & 1) &
-                            ((uint32_t)(o.z > me.z) | ((uint32_t)(o.z == me.z) & (uint32_t)(o.w > me.w)));
+        const uint32_t gt = (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > mkey);
         cnt += gt;
-        cand |= (gt & (uint32_t)in_cube_h(me.x, o.x, o.y)) << u;
+        cand |= (gt & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
       }
       uint32_t low = 0;
       if (cand) {  // rare: the exact distance decides
@@ -765,53 +809,44 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
           const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
                                   __uint_as_float(pj.z), __uint_as_float(pi.x),
                                   __uint_as_float(pi.y), __uint_as_float(pi.z));
-          low |= dd < __uint_as_float(me.z) ? 1u : 0u;
+          low |= dd < __uint_as_float(me.w) ? 1u : 0u;
         }
       }
       const uint32_t rank = quad_sum(cnt);
       const bool lowered = quad_sum(low) != 0;
-      // prefix length: first lowered rank, copies >= the hot threshold, copies
-      // with distance > 0, samples left
       const bool rep = remj && hq == 0;
-      const bool ge = me.z > th_hi || (me.z == th_hi && me.w >= th_lo);
-      const uint32_t lr = rep && lowered ? rank : 0xffffffffu;
-      const uint32_t wmin = wave_min_u32(lr);
+      const bool ge = mkey >= hth;
+      if (rep) s_rank[hj] = rank;
+      if (hq == 0 && !remj) s_rank[hj] = kHot;  // never accepted
+      if (rep && lowered) atomicOr(&s_lowm[ph], 1ull << rank);
       const uint32_t wge = (uint32_t)__popcll(__ballot(rep && ge));
-      const uint32_t wnz = (uint32_t)__popcll(__ballot(rep && ge && me.z != 0u));
+      const uint32_t wnz = (uint32_t)__popcll(__ballot(rep && ge && me.w != 0u));
       if (lane == 0) {
-        s_wr[wave][0] = wmin;
-        s_wr[wave][1] = wge;
-        s_wr[wave][2] = wnz;
+        s_wr[ph][wave][0] = wge;
+        s_wr[ph][wave][1] = wnz;
       }
+      if (tid == 0) s_lowm[ph ^ 1] = 0;
       __syncthreads();
-      uint32_t P = 0xffffffffu, nge = 0, nnz = 0;
+      NSFPS_RMARK(kRpRank);
+      // prefix length: first lowered rank, copies >= the hot threshold with
+      // distance > 0 (a rank prefix), samples left
+      const unsigned long long lowm = s_lowm[ph];
+      uint32_t nge = 0, nnz = 0;
 #pragma unroll
       for (uint32_t w = 0; w < kRunWaves; ++w) {
-        P = min(P, s_wr[w][0]);
-        nge += s_wr[w][1];
-        nnz += s_wr[w][2];
+        nge += s_wr[ph][w][0];
+        nnz += s_wr[ph][w][1];
       }
-      // copies >= the hot threshold are a rank prefix, and so are those with
-      // distance > 0 among them
-      P = min(min(P, nnz), room - npk);
+      const uint32_t plow = lowm ? (uint32_t)__builtin_ctzll(lowm) : kHot;
+      const uint32_t P = min(min(plow, nnz), room - npk);
       if (P == 0) {  // rank 0: below the hot threshold, or distance 0, or no room
         stop = (nge == 0) ? 1u : 2u;
         break;
       }
       // the prefix: samples npk .. npk + P - 1 in rank order
       const bool acc = remj && rank < P;
-      if (acc && hq == 0) s_rec[npk + rank] = make_uint2(hj | ((me.y & 0xfffffu) << 8), me.y >> 20);
-      const uint64_t am = __ballot(acc && hq == 0);
-      // quad leaders are lanes 0, 4, ..., 60 of the wave: copy 16 * wave + lane / 4
-      uint64_t amc = 0;
-#pragma unroll
-      for (uint32_t k = 0; k < 16; ++k) amc |= ((am >> (4 * k)) & 1ull) << k;
-      if (lane == 0) s_wm[wave] = amc << (16 * wave);
-      __syncthreads();
-      uint64_t accm = 0;
-#pragma unroll
-      for (uint32_t w = 0; w < kRunWaves; ++w) accm |= s_wm[w];
-      taken |= accm;
+      if (acc && hq == 0)
+        s_rec[npk + rank] = make_uint2(hj | ((mx.w & 0xfffffu) << 8), mx.w >> 20);
       npk += P;
       if (npk >= room) {  // the last sample needs no update
         stop = 2;
@@ -822,18 +857,22 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         break;
       }
       // the accepted cubes on the remaining copies
-      const bool remj2 = hj < nhot && !((taken >> hj) & 1);
+      const bool remj2 = remj && !acc;
       uint32_t mnb = 0xffffffffu;
-      {
-        const uint32_t am2 = (uint32_t)(accm >> (hq * (kHot / kQuarter))) & 0xffffu;
-        uint32_t cand2 = 0;
-        if (remj2) {
+      if (remj2) {
+        uint32_t rk[kHot / kQuarter];
 #pragma unroll
-          for (uint32_t u = 0; u < kHot / kQuarter; ++u) {
-            const uint4 o = s_hq[hq * (kHot / kQuarter) + u];
-            cand2 |= (((am2 >> u) & 1u) & (uint32_t)in_cube_h(me.x, o.x, o.y)) << u;
-          }
+        for (uint32_t v = 0; v < kHot / kQuarter / 4; ++v) {
+          const uint4 r4 = reinterpret_cast<const uint4 *>(s_rank)[hq * (kHot / kQuarter / 4) + v];
+          rk[4 * v] = r4.x;
+          rk[4 * v + 1] = r4.y;
+          rk[4 * v + 2] = r4.z;
+          rk[4 * v + 3] = r4.w;
         }
+        uint32_t cand2 = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < kHot / kQuarter; ++u)
+          cand2 |= ((uint32_t)(rk[u] < P) & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
         if (cand2) {  // rare: the exact distances
           const uint4 pj = s_hp[hj];
           while (cand2) {
@@ -848,11 +887,24 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         }
       }
       mnb = quad_min(mnb);
-      __syncthreads();  // every thread has read s_hq
-      if (remj2 && hq == 0 && mnb < me.z) {
-        s_hq[hj] = make_uint4(me.x, packed_halves(c.r, __uint_as_float(mnb)), mnb, me.w);
+      // the next buffer: accepted copies get key 0, lowered ones new cubes
+      if (hq == 0) {
+        uint4 nv = me;
+        if (acc) {
+          nv.z = 0u;
+          nv.w = 0u;
+        } else if (remj && mnb < me.w) {
+          const uint32_t h = packed_halves(c.r, __uint_as_float(mnb));
+          uint32_t lo_c, hi_c;
+          cube_corners(mx.x, h, b0, b1, b2, lo_c, hi_c);
+          nv = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, me.z, mnb);
+          s_hx[hj].w = h;
+        }
+        s_hq[ph ^ 1][hot_slot(hj)] = nv;
       }
       __syncthreads();
+      ph ^= 1;
+      NSFPS_RMARK(kRpPhases);
       if (PROF) pf[kRpPhaseCount] += 1;
     }
     NSFPS_RMARK(kRpPhases);
@@ -870,7 +922,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         const uint2 r = s_rec[k];
         const uint32_t cp = r.x & 255u;
         const uint4 a0 = s_hp[cp];
-        const uint32_t qc = s_hq[cp].x;
+        const uint32_t qc = s_hx[cp].x;
         const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
         uint32_t lo_c, hi_c;
         cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
@@ -942,7 +994,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
           const uint2 r = s_rec[kb];
           const uint32_t cp = r.x & 255u;
           const uint4 a0 = s_hp[cp];
-          const uint32_t qc = s_hq[cp].x;
+          const uint32_t qc = s_hx[cp].x;
           const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
