@@ -35,6 +35,7 @@ constexpr uint32_t kPassThreads = 1024;  // grid-wide passes: one level-1 node p
 constexpr uint32_t kPassWaves = kPassThreads / 64;
 constexpr uint32_t kLeavesPerWave = kFan / kPassWaves;
 constexpr uint32_t kMaxShift = 52;  // kHistBins << 52 covers the whole u64 key range
+constexpr uint32_t kSparseGroups = 128;  // workgroups per cloud of the refinement and gather passes
 
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
   return x | (y << 10) | (z << 20);
@@ -298,33 +299,36 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
 
 // ------------------------------------------------------- refinement passes
 
-// Refinement pass `pass` (1 or 2): counts the keys of node blockIdx.x inside
-// the window the selection replayed from the earlier histograms asks for;
-// does nothing when the threshold is already resolved.
+// Refinement pass `pass` (1 or 2): counts the keys inside the window the
+// selection replayed from the earlier histograms asks for; does nothing when
+// the threshold is already resolved.  Few workgroups, each striding over the
+// level-1 nodes: the pass is usually skipped, and then costs little more than
+// its launch.
 __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restrict__ clouds,
                                                          uint32_t pass) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ uint32_t s_sc[kPassWaves + 2];
   const CloudDev &c = clouds[blockIdx.y];
-  const uint32_t g = blockIdx.x;
-  if (g >= c.nl1 || *gptr(c.done)) return;
+  if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const Sel s = sel_replay(c, pass, s_sc);
   if (s.state != 0 || s.pass != pass) return;
   const uint64_t wlo = window_lo(s.kref, s.S);
-  if (gptr(c.l1_key)[g] < wlo) return;
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   __syncthreads();
-  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-    const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
-    if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < wlo) continue;
-    const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-    const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
-    if (lane < cnt) {
-      const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
-      const uint32_t rank = gptr(c.RO)[st + lane].x;
-      const uint32_t b = key_bin(((uint64_t)__float_as_uint(d) << 32) | ~rank, s.kref, s.S);
-      if (b != kNone) atomicAdd(&s_hist[b], 1u);
+  for (uint32_t g = blockIdx.x; g < c.nl1; g += gridDim.x) {
+    if (gptr(c.l1_key)[g] < wlo) continue;
+    for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+      const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
+      if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < wlo) continue;
+      const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
+      const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
+      if (lane < cnt) {
+        const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
+        const uint32_t rank = gptr(c.RO)[st + lane].x;
+        const uint32_t b = key_bin(((uint64_t)__float_as_uint(d) << 32) | ~rank, s.kref, s.S);
+        if (b != kNone) atomicAdd(&s_hist[b], 1u);
+      }
     }
   }
   __syncthreads();
@@ -339,16 +343,16 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
 
 __device__ __forceinline__ uint32_t bit_length(uint64_t v) { return v ? 64u - __clzll(v) : 0u; }
 
-// Resolves the threshold from the histograms and appends every point of node
-// blockIdx.x whose key is >= it to the list.  When no threshold below the
-// maximum fits the list (more than kListCap keys inside the finest bin), the
-// threshold is the maximum key itself: a run of one sample.
+// Resolves the threshold from the histograms and appends every point whose key
+// is >= it to the list.  When no threshold below the maximum fits the list
+// (more than kListCap keys inside the finest bin), the threshold is the
+// maximum key itself: a run of one sample.  Few workgroups, each striding over
+// the level-1 nodes; most nodes hold no key above the threshold.
 __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_sc[kPassWaves + 2];
   __shared__ uint64_t s_wk[kPassWaves];
   const CloudDev &c = clouds[blockIdx.y];
-  const uint32_t g = blockIdx.x;
-  if (g >= c.nl1 || *gptr(c.done)) return;
+  if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   const Sel s = sel_replay(c, kRefinePasses + 1, s_sc);
@@ -366,41 +370,43 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     for (uint32_t w = 0; w < kPassWaves; ++w) best = s_wk[w] > best ? s_wk[w] : best;
     bkey = best;
   }
-  if (g == 0 && tid == 0) {
+  if (blockIdx.x == 0 && tid == 0) {
     rs.bkey = bkey;
     // next round: fine bins of about 1/2048 of this round's key span
     uint32_t nx = bit_length(rs.kref0 - bkey + 1);
     nx = nx > 11u ? nx - 11u : 0u;
     rs.s0_next = nx < kMaxShift ? nx : kMaxShift;
   }
-  if (gptr(c.l1_key)[g] < bkey) return;
-  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-    const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
-    if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < bkey) continue;
-    const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-    const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
-    const uint32_t cell = gptr(c.leaf_cell)[leaf];
-    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
-    uint2 ro = make_uint2(0u, 0u);
-    if (lane < cnt) {
-      p = gptr(c.P4)[st + lane];
-      ro = gptr(c.RO)[st + lane];
-    }
-    const bool take =
-        lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
-    const uint64_t m = __ballot(take);
-    if (!m) continue;
-    uint32_t base = 0;
-    if (lane == 0) base = atomicAdd(&rs.nlist, (uint32_t)__popcll(m));
-    base = rdlane(base, 0);
-    if (take) {
-      const uint32_t i = base + lanes_below(m);
-      if (i < kListCap) {
-        gptr(c.list_p)[i] = p;
-        gptr(c.list_r)[i] = ro;
-        gptr(c.list_c)[i] = cell;
-      } else {
-        rs.err = 1;
+  for (uint32_t g = blockIdx.x; g < c.nl1; g += gridDim.x) {
+    if (gptr(c.l1_key)[g] < bkey) continue;
+    for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+      const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
+      if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < bkey) continue;
+      const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
+      const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
+      const uint32_t cell = gptr(c.leaf_cell)[leaf];
+      float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+      uint2 ro = make_uint2(0u, 0u);
+      if (lane < cnt) {
+        p = gptr(c.P4)[st + lane];
+        ro = gptr(c.RO)[st + lane];
+      }
+      const bool take =
+          lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
+      const uint64_t m = __ballot(take);
+      if (!m) continue;
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&rs.nlist, (uint32_t)__popcll(m));
+      base = rdlane(base, 0);
+      if (take) {
+        const uint32_t i = base + lanes_below(m);
+        if (i < kListCap) {
+          gptr(c.list_p)[i] = p;
+          gptr(c.list_r)[i] = ro;
+          gptr(c.list_c)[i] = cell;
+        } else {
+          rs.err = 1;
+        }
       }
     }
   }
@@ -1080,10 +1086,12 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, bool profile, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
+  const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
   for (uint32_t r = 0; r < rounds; ++r) {
     k_update<<<grid, kPassThreads, 0, st>>>(d_clouds);
-    for (uint32_t p = 1; p <= kRefinePasses; ++p) k_refine<<<grid, kPassThreads, 0, st>>>(d_clouds, p);
-    k_gather<<<grid, kPassThreads, 0, st>>>(d_clouds);
+    for (uint32_t p = 1; p <= kRefinePasses; ++p)
+      k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p);
+    k_gather<<<sparse, kPassThreads, 0, st>>>(d_clouds);
     if (profile)
       k_run<true><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
     else
