@@ -437,13 +437,15 @@ constexpr uint32_t kRunThreads = 256;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
 constexpr uint32_t kHot = 64;
-constexpr uint32_t kQuarter = kRunThreads / kHot;  // threads per hot copy
+constexpr uint32_t kCopyLanes = kRunThreads / kHot;  // threads per hot copy (and per sample)
+constexpr uint32_t kCmp = kHot / kCopyLanes;         // copies each of them compares against
 constexpr uint32_t kSelBins = 256;
 constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
-constexpr uint32_t kQuadRows = 64;     // cubes over more coarse rows, or over more
-constexpr uint32_t kQuadEntries = 32;  // list entries, are applied by every thread
-static_assert(kOwnSlots == 4 && kQuarter == 4, "the run kernel layout");
-static_assert(kCells == 16 * kRunThreads, "the cell scan takes 16 cells per thread");
+constexpr uint32_t kWalkRows = 64;     // cubes over more coarse rows, or over more
+constexpr uint32_t kWalkEntries = 32;  // list entries, are applied by every thread
+constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
+static_assert((kCopyLanes == 4 || kCopyLanes == 8) && kHot == 64, "the run kernel layout");
+static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
 // rounds into the cloud's profile words) when PROF is set.
@@ -499,18 +501,25 @@ __device__ __forceinline__ uint32_t packed_halves(const RangeDev &r, float D) {
          (min((uint32_t)cube_half(D, r.bsize[2], r.blocks[2]), r.blocks[2] - 1) << 20);
 }
 
-// LDS slot of hot copy i: the copies a quarter reads together (u, 16 + u,
-// 32 + u, 48 + u) sit side by side, so one read by a wave touches distinct banks.
-__device__ __forceinline__ uint32_t hot_slot(uint32_t i) { return ((i & 15u) << 2) | (i >> 4); }
-
-// Sum / OR over the four lanes of a quad.
-__device__ __forceinline__ uint32_t quad_sum(uint32_t v) {
-  v += dpp_mov<kDppQuad1032>(v);
-  return v + dpp_mov<kDppQuad2301>(v);
+// LDS slot of hot copy i.  Lane q of a copy's group compares against copies
+// q * kCmp + u; the kCopyLanes copies read together for one u sit side by
+// side, so one read by a wave touches distinct banks.
+__device__ __forceinline__ uint32_t hot_slot(uint32_t i) {
+  return (i % kCmp) * kCopyLanes + i / kCmp;
 }
-__device__ __forceinline__ uint32_t quad_min(uint32_t v) {
+
+// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes).
+__device__ __forceinline__ uint32_t group_sum(uint32_t v) {
+  v += dpp_mov<kDppQuad1032>(v);
+  v += dpp_mov<kDppQuad2301>(v);
+  if (kCopyLanes == 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
+  return v;
+}
+__device__ __forceinline__ uint32_t group_min(uint32_t v) {
   v = min(v, dpp_mov<kDppQuad1032>(v));
-  return min(v, dpp_mov<kDppQuad2301>(v));
+  v = min(v, dpp_mov<kDppQuad2301>(v));
+  if (kCopyLanes == 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
+  return v;
 }
 
 template <bool PROF>
@@ -589,22 +598,23 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       }
     }
     __syncthreads();
-    {  // exclusive scan of the cell counts, cells 16 tid .. 16 tid + 15 per thread
-      uint4 v[4];
+    {  // exclusive scan of the cell counts, kCellsPerThread consecutive cells per thread
+      constexpr uint32_t kV = kCellsPerThread / 4;
+      uint4 v[kV];
       uint32_t sum = 0;
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        v[j] = reinterpret_cast<const uint4 *>(s_cell)[4 * tid + j];
+      for (uint32_t j = 0; j < kV; ++j) {
+        v[j] = reinterpret_cast<const uint4 *>(s_cell)[kV * tid + j];
         sum += v[j].x + v[j].y + v[j].z + v[j].w;
       }
       uint32_t tot;
       uint32_t pre = block_excl_scan<kRunWaves>(sum, s_wn, &tot);
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
+      for (uint32_t j = 0; j < kV; ++j) {
         const uint4 o = make_uint4(pre, pre + v[j].x, pre + v[j].x + v[j].y,
                                    pre + v[j].x + v[j].y + v[j].z);
         pre += v[j].x + v[j].y + v[j].z + v[j].w;
-        reinterpret_cast<uint4 *>(s_cell)[4 * tid + j] = o;
+        reinterpret_cast<uint4 *>(s_cell)[kV * tid + j] = o;
       }
       if (tid == 0) s_cell[kCells] = tot;
     }
@@ -688,7 +698,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       uint32_t S = bit_length(kmax - bkey);
       S = S > 8u ? S - 8u : 0u;
       while (true) {
-        s_hist[tid] = 0;
+        if (tid < kSelBins) s_hist[tid] = 0;
         __syncthreads();
 #pragma unroll
         for (uint32_t s = 0; s < kOwnSlots; ++s) {
@@ -781,8 +791,9 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       __syncthreads();
     }
     NSFPS_RMARK(kRpGather);
-    // ---- phases: thread (j, q) works for hot copy j against copies 16q..16q+15
-    const uint32_t hj = tid / kQuarter, hq = tid % kQuarter;
+    // ---- phases: thread (j, q) works for hot copy j against copies
+    // kCmp q .. kCmp q + kCmp - 1
+    const uint32_t hj = tid / kCopyLanes, hq = tid % kCopyLanes;
     const uint32_t room = m - it;  // samples left (>= 1)
     // Per phase, two barriers: after the ranks (the accepted prefix is known),
     // and after the next buffer of hot copies is written.
@@ -790,17 +801,17 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     while (true) {
       const uint4 me = s_hq[ph][hot_slot(hj)];
       const uint4 mx = s_hx[hj];
-      // the 16 copies of this quarter, all loads issued before any use
-      uint4 og[kHot / kQuarter];
+      // the kCmp copies of this lane, all loads issued before any use
+      uint4 og[kCmp];
 #pragma unroll
-      for (uint32_t u = 0; u < kHot / kQuarter; ++u) og[u] = s_hq[ph][4 * u + hq];  // copy 16 hq + u
+      for (uint32_t u = 0; u < kCmp; ++u) og[u] = s_hq[ph][kCopyLanes * u + hq];  // copy kCmp hq + u
       __builtin_amdgcn_sched_barrier(0);
       const uint64_t mkey = ((uint64_t)me.w << 32) | me.z;
       const bool remj = mkey != 0;  // copies taken earlier, and unused slots, have key 0
-      // bit u of cand: copy 16q + u is remaining, ranked above j, and its cube holds j
+      // bit u of cand: copy kCmp q + u is remaining, ranked above j, and its cube holds j
       uint32_t cnt = 0, cand = 0;
 #pragma unroll
-      for (uint32_t u = 0; u < kHot / kQuarter; ++u) {
+      for (uint32_t u = 0; u < kCmp; ++u) {
         const uint32_t gt = (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > mkey);
         cnt += gt;
         cand |= (gt & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
@@ -811,15 +822,15 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         while (cand) {
           const uint32_t u = (uint32_t)__builtin_ctz(cand);
           cand &= cand - 1;
-          const uint4 pi = s_hp[hq * (kHot / kQuarter) + u];
+          const uint4 pi = s_hp[hq * kCmp + u];
           const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
                                   __uint_as_float(pj.z), __uint_as_float(pi.x),
                                   __uint_as_float(pi.y), __uint_as_float(pi.z));
           low |= dd < __uint_as_float(me.w) ? 1u : 0u;
         }
       }
-      const uint32_t rank = quad_sum(cnt);
-      const bool lowered = quad_sum(low) != 0;
+      const uint32_t rank = group_sum(cnt);
+      const bool lowered = group_sum(low) != 0;
       const bool rep = remj && hq == 0;
       const bool ge = mkey >= hth;
       if (rep) s_rank[hj] = rank;
@@ -866,10 +877,10 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       const bool remj2 = remj && !acc;
       uint32_t mnb = 0xffffffffu;
       if (remj2) {
-        uint32_t rk[kHot / kQuarter];
+        uint32_t rk[kCmp];
 #pragma unroll
-        for (uint32_t v = 0; v < kHot / kQuarter / 4; ++v) {
-          const uint4 r4 = reinterpret_cast<const uint4 *>(s_rank)[hq * (kHot / kQuarter / 4) + v];
+        for (uint32_t v = 0; v < kCmp / 4; ++v) {
+          const uint4 r4 = reinterpret_cast<const uint4 *>(s_rank)[hq * (kCmp / 4) + v];
           rk[4 * v] = r4.x;
           rk[4 * v + 1] = r4.y;
           rk[4 * v + 2] = r4.z;
@@ -877,14 +888,14 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         }
         uint32_t cand2 = 0;
 #pragma unroll
-        for (uint32_t u = 0; u < kHot / kQuarter; ++u)
+        for (uint32_t u = 0; u < kCmp; ++u)
           cand2 |= ((uint32_t)(rk[u] < P) & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
         if (cand2) {  // rare: the exact distances
           const uint4 pj = s_hp[hj];
           while (cand2) {
             const uint32_t u = (uint32_t)__builtin_ctz(cand2);
             cand2 &= cand2 - 1;
-            const uint4 pi = s_hp[hq * (kHot / kQuarter) + u];
+            const uint4 pi = s_hp[hq * kCmp + u];
             const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
                                     __uint_as_float(pj.z), __uint_as_float(pi.x),
                                     __uint_as_float(pi.y), __uint_as_float(pi.z));
@@ -892,7 +903,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
           }
         }
       }
-      mnb = quad_min(mnb);
+      mnb = group_min(mnb);
       // the next buffer: accepted copies get key 0, lowered ones new cubes
       if (hq == 0) {
         uint4 nv = me;
@@ -915,12 +926,13 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     NSFPS_RMARK(kRpPhases);
     // ---- the hot run's samples -> global memory and every list entry.
-    // Quad k takes sample k: a cube whose coarse cells span at most kQuadRows
-    // rows and hold at most kQuadEntries list entries is applied by walking
-    // those rows of the cell index (distances min-ed into LDS); a larger one
-    // is flagged and applied below by every thread to its own entries.
+    // Lane group k takes sample k: a cube whose coarse cells span at most
+    // kWalkRows rows and hold at most kWalkEntries list entries is applied by
+    // walking those rows of the cell index (distances min-ed into LDS); a
+    // larger one is flagged and applied below by every thread to its own
+    // entries.
     {
-      const uint32_t k = tid / kQuarter, q = tid % kQuarter;
+      const uint32_t k = tid / kCopyLanes, q = tid % kCopyLanes;
       if (k < npk) {
         // kept in vector registers: the scalar file is full here
         const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
@@ -948,26 +960,26 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
           ++rz0;
         }
         uint32_t cnt = 0;  // list entries in the coarse cells of the cube
-        if (nrows <= kQuadRows) {
+        if (nrows <= kWalkRows) {
           uint32_t ry = ry0, rz = rz0;
-          for (uint32_t rr = q; rr < nrows; rr += kQuarter) {
+          for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
             const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
             cnt += s_cell[rw + x1 + 1] - s_cell[rw + x0];
-            ry += kQuarter;
+            ry += kCopyLanes;
             while (ry >= ny) {
               ry -= ny;
               ++rz;
             }
           }
         }
-        cnt = quad_sum(cnt);
-        if (nrows > kQuadRows || cnt > kQuadEntries) {
+        cnt = group_sum(cnt);
+        if (nrows > kWalkRows || cnt > kWalkEntries) {
           if (q == 0) atomicOr(&s_big[k >> 5], 1u << (k & 31u));
         } else if (cnt) {
           const float px = __uint_as_float(a0.x), py = __uint_as_float(a0.y),
                       pz = __uint_as_float(a0.z);
           uint32_t ry = ry0, rz = rz0;
-          for (uint32_t rr = q; rr < nrows; rr += kQuarter) {
+          for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
             const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
             const uint32_t e1 = s_cell[rw + x1 + 1];
             for (uint32_t e = s_cell[rw + x0]; e < e1; ++e) {
@@ -979,7 +991,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
                 atomicMin(&s_dd[e], dd);  // non-negative floats order like their bits
               }
             }
-            ry += kQuarter;
+            ry += kCopyLanes;
             while (ry >= ny) {
               ry -= ny;
               ++rz;

@@ -242,3 +242,18 @@ def test_shared_buckets_visited_once(yf):
     for rep in range(3):
         for case in cases:
             assert np.array_equal(run_module(yf, case), case.expected), (case.name, rep)
+
+
+@pytest.mark.parametrize("name", ["manual_includes_all", "quickstart_full", "lattice_ties_16",
+                                  "shell_duplicates"])
+def test_repeated_calls_are_bit_identical(lib, name):
+    """The list and its cell order are built with atomics, so they differ from
+    call to call; the samples must not.  Thirty calls of one case, each against
+    the reference's golden vector."""
+    case = next(c for c in GOLDEN_CASES if c.name == name)
+    for i in range(30):
+        if case.range is None:
+            got = lib.fps_bbox(case.points, case.n_samples, case.blocks)
+        else:
+            got = lib.fps(case.points, case.n_samples, case.range)
+        assert np.array_equal(got, case.expected), (name, i)
