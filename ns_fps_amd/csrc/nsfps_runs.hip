@@ -414,8 +414,9 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 
 // ---------------------------------------------------------------- the run
 
-// One workgroup per cloud, four waves; every thread holds kOwnSlots list
-// entries.  The list sits in LDS sorted by coarse cell (x >> sx, y >> sy,
+// One workgroup per cloud, eight waves (two per SIMD: the kernel is bound by
+// instruction latency, which the second wave hides); every thread holds
+// kOwnSlots list entries.  The list sits in LDS sorted by coarse cell (x >> sx, y >> sy,
 // z >> sz; at most kCells of them) with the first entry of every coarse cell,
 // so the entries inside a cube are found by walking, for each coarse (y, z)
 // row the cube spans, the entries of its x range.
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // sample with a small cube is applied by one quad walking its rows of the
 // cell index, one with a large cube by every thread to its own entries) and
 // the next hot set is chosen.  The run ends when no entry is >= B.
-constexpr uint32_t kRunThreads = 256;
+constexpr uint32_t kRunThreads = 512;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
 constexpr uint32_t kHot = 64;
@@ -508,17 +509,20 @@ __device__ __forceinline__ uint32_t hot_slot(uint32_t i) {
   return (i % kCmp) * kCopyLanes + i / kCmp;
 }
 
-// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes).
+// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes): quad
+// permutes, then for groups of eight the other quad through a lane shuffle
+// (a row_half_mirror DPP step here gave wrong sums now and then with two
+// waves per SIMD; the shuffle has not).
 __device__ __forceinline__ uint32_t group_sum(uint32_t v) {
   v += dpp_mov<kDppQuad1032>(v);
   v += dpp_mov<kDppQuad2301>(v);
-  if (kCopyLanes == 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
+  if (kCopyLanes == 8) v += (uint32_t)__shfl_xor((int)v, 4, 64);
   return v;
 }
 __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   v = min(v, dpp_mov<kDppQuad1032>(v));
   v = min(v, dpp_mov<kDppQuad2301>(v));
-  if (kCopyLanes == 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
+  if (kCopyLanes == 8) v = min(v, (uint32_t)__shfl_xor((int)v, 4, 64));
   return v;
 }
 
