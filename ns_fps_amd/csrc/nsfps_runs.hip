@@ -526,6 +526,26 @@ __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   return v;
 }
 
+// Per-wave maximum and count of the live keys (>= bkey) among this thread's
+// entries, stored by lane 0 for the next hot set.
+__device__ __forceinline__ void publish_live(const float *d, const uint32_t *lo, uint64_t bkey,
+                                             uint64_t *s_wk, uint32_t *s_wn) {
+  uint64_t kmx = 0;
+  uint32_t nl = 0;
+#pragma unroll
+  for (uint32_t s = 0; s < kOwnSlots; ++s) {
+    const uint64_t key = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
+    const bool live = lo[s] != 0u && key >= bkey;
+    kmx = live && key > kmx ? key : kmx;
+    nl += (uint32_t)__popcll(__ballot(live));
+  }
+  kmx = wave_max_u64(kmx);
+  if (lane_id() == 0) {
+    s_wk[threadIdx.x >> 6] = kmx;
+    s_wn[threadIdx.x >> 6] = nl;
+  }
+}
+
 template <bool PROF>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
   __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, fine cell}
@@ -542,11 +562,11 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy, half-widths
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
   __shared__ uint32_t s_big[2];                         // samples with large cubes
-  __shared__ uint32_t s_hist[kSelBins];
+  __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
+  __shared__ uint32_t s_nhot;
   __shared__ uint64_t s_wk[kRunWaves];
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
   __shared__ uint32_t s_wr[2][kRunWaves][2];
-  __shared__ uint32_t s_misc[4];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -666,26 +686,14 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   NSFPS_GLOBAL uint2 *const pick_c = gptr(c.pick_c);
   uint32_t np = 0;
   bool done = false;
+  publish_live(d, lo, bkey, s_wk, s_wn);
+  if (tid < kSelBins) s_sel[0][tid] = 0;
+  if (tid == 0) s_nhot = 0;
+  __syncthreads();
   NSFPS_RMARK(kRpLoad);
   while (true) {
     // ---- hot threshold: live entries (key >= B); their maximum and count
-    uint64_t key[kOwnSlots];
-    bool live[kOwnSlots];
-    uint64_t kmx = 0;
-    uint32_t nl = 0;
-#pragma unroll
-    for (uint32_t s = 0; s < kOwnSlots; ++s) {
-      key[s] = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
-      live[s] = lo[s] != 0u && key[s] >= bkey;
-      kmx = live[s] && key[s] > kmx ? key[s] : kmx;
-      nl += (uint32_t)__popcll(__ballot(live[s]));
-    }
-    kmx = wave_max_u64(kmx);
-    if (lane == 0) {
-      s_wk[wave] = kmx;
-      s_wn[wave] = nl;
-    }
-    __syncthreads();
+    // were published at the end of the previous hot set (or after the load)
     uint64_t kmax = 0;
     uint32_t nlive = 0;
 #pragma unroll
@@ -693,48 +701,47 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       kmax = s_wk[w] > kmax ? s_wk[w] : kmax;
       nlive += s_wn[w];
     }
-    __syncthreads();
     if (nlive == 0) break;  // every key is below B: the run ends
+    uint64_t key[kOwnSlots];
+    bool live[kOwnSlots];
+#pragma unroll
+    for (uint32_t s = 0; s < kOwnSlots; ++s) {
+      key[s] = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
+      live[s] = lo[s] != 0u && key[s] >= bkey;
+    }
     uint64_t hth = bkey;
     if (nlive > kHot) {
+      // histogram windows of kSelBins bins below kref, refined 8 bits at a
+      // time; buffer i % 3 of step i was zeroed a step (or a hot set) before,
+      // and every wave scans it itself: one barrier per step
       uint64_t kref = kmax;
       uint32_t cap = kHot;
       uint32_t S = bit_length(kmax - bkey);
       S = S > 8u ? S - 8u : 0u;
-      while (true) {
-        if (tid < kSelBins) s_hist[tid] = 0;
-        __syncthreads();
+      for (uint32_t step = 0;; ++step) {
+        uint32_t *H = s_sel[step % 3];
 #pragma unroll
         for (uint32_t s = 0; s < kOwnSlots; ++s) {
           if (live[s] && key[s] <= kref) {
             const uint64_t bb = (kref - key[s]) >> S;
-            if (bb < kSelBins) atomicAdd(&s_hist[(uint32_t)bb], 1u);
+            if (bb < kSelBins) atomicAdd(&H[(uint32_t)bb], 1u);
           }
         }
+        if (tid < kSelBins) s_sel[(step + 1) % 3][tid] = 0;
         __syncthreads();
-        if (wave == 0) {
-          const uint4 hv = reinterpret_cast<const uint4 *>(s_hist)[lane];
-          const uint32_t tot = hv.x + hv.y + hv.z + hv.w;
-          const uint32_t incl = wave_incl_scan(tot);
-          uint32_t cum = incl - tot;
-          const uint32_t bins[4] = {hv.x, hv.y, hv.z, hv.w};
-#pragma unroll
-          for (uint32_t j = 0; j < 4; ++j) {
-            if (cum <= cap && cum + bins[j] > cap) {
-              s_misc[0] = 4 * lane + j;
-              s_misc[1] = cum;
-            }
-            cum += bins[j];
-          }
-          if (lane == 63 && incl <= cap) s_misc[0] = kNone;
-        }
-        __syncthreads();
-        const uint32_t bs = s_misc[0], before = s_misc[1];
-        __syncthreads();
-        if (bs == kNone) {  // cannot happen (every window holds more than cap keys):
-          hth = kmax;       // then take the maximum alone
+        const uint4 hv = reinterpret_cast<const uint4 *>(H)[lane];
+        const uint32_t tot = hv.x + hv.y + hv.z + hv.w;
+        const uint32_t incl = wave_incl_scan(tot);
+        const uint64_t over = __ballot(incl > cap);  // running totals only grow
+        if (!over) {  // cannot happen (every window holds more than cap keys):
+          hth = kmax;  // then take the maximum alone
           break;
         }
+        const uint32_t c0 = incl - tot, c1 = c0 + hv.x, c2 = c1 + hv.y, c3 = c2 + hv.z;
+        const uint32_t jj = c1 > cap ? 0u : c2 > cap ? 1u : c3 > cap ? 2u : 3u;
+        const uint32_t bf = c1 > cap ? c0 : c2 > cap ? c1 : c3 > cap ? c2 : c3;
+        const uint32_t L = (uint32_t)__builtin_ctzll(over);
+        const uint32_t bs = 4 * L + rdlane(jj, L), before = rdlane(bf, L);
         if (before >= cap / 2 || S == 0) {
           hth = kref - ((uint64_t)bs << S) + 1;
           break;
@@ -746,43 +753,35 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       hth = hth > bkey ? hth : bkey;
     }
     NSFPS_RMARK(kRpSelect);
-    // ---- hot copies -> LDS
-    uint32_t nhot = 0;
+    // ---- hot copies -> LDS, placed by an LDS counter; their cube corners
+    // follow, one copy per thread
+    uint32_t nhot;
     {
-      uint64_t bal[kOwnSlots];
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        bal[s] = __ballot(live[s] && key[s] >= hth);
-        if (lane == 0) s_wn[wave * kOwnSlots + s] = (uint32_t)__popcll(bal[s]);
-      }
-      __syncthreads();
-      uint32_t base = 0;
-#pragma unroll
-      for (uint32_t j = 0; j < kRunWaves * kOwnSlots; ++j) {
-        const uint32_t v = s_wn[j];
-        base += j < wave * kOwnSlots ? v : 0u;
-        nhot += v;
-      }
-#pragma unroll
-      for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        if ((bal[s] >> lane) & 1) {
-          const uint32_t hi = base + lanes_below(bal[s]);
-          if (hi < kHot) {  // the cube corners follow below, one copy per thread
-            s_hq[0][hot_slot(hi)] = make_uint4(0u, 0u, lo[s], __float_as_uint(d[s]));
-            s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), 0u);
-            s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
-                                  __float_as_uint(z[s]), row[s]);
-          } else {  // cannot happen (at most kHot keys are >= the hot threshold)
-            rs.err = 2;
+        const bool hot = live[s] && key[s] >= hth;
+        const uint64_t bal = __ballot(hot);
+        if (bal) {
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(&s_nhot, (uint32_t)__popcll(bal));
+          base = rdlane(base, 0);
+          if (hot) {
+            const uint32_t hi = base + lanes_below(bal);
+            if (hi < kHot) {
+              s_hq[0][hot_slot(hi)] = make_uint4(0u, 0u, lo[s], __float_as_uint(d[s]));
+              s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), 0u);
+              s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
+                                    __float_as_uint(z[s]), row[s]);
+            } else {  // cannot happen (at most kHot keys are >= the hot threshold)
+              rs.err = 2;
+            }
           }
         }
-        base += (uint32_t)__popcll(bal[s]);
       }
-      nhot = nhot < kHot ? nhot : kHot;
-      if (tid >= nhot && tid < kHot) s_hq[0][hot_slot(tid)] = make_uint4(0u, 0u, 0u, 0u);  // unused
       if (tid < 2) s_big[tid] = 0;
       if (tid == 0) s_lowm[0] = 0;
       __syncthreads();
+      nhot = min(s_nhot, kHot);
       if (tid < nhot) {
         const uint4 hq0 = s_hq[0][hot_slot(tid)];
         const uint32_t cl = s_hx[tid].x;
@@ -791,6 +790,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         cube_corners(cl, h, b0, b1, b2, lo_c, hi_c);
         s_hq[0][hot_slot(tid)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hq0.z, hq0.w);
         s_hx[tid].w = h;
+      } else if (tid < kHot) {
+        s_hq[0][hot_slot(tid)] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
       }
       __syncthreads();
     }
@@ -1035,6 +1036,11 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     it += npk;
     np += npk;
+    // the next hot set's live maximum and count, and its zeroed histogram and
+    // copy counter
+    publish_live(d, lo, bkey, s_wk, s_wn);
+    if (tid < kSelBins) s_sel[0][tid] = 0;
+    if (tid == 0) s_nhot = 0;
     __syncthreads();  // s_hq / s_hp / s_rec are rewritten by the next hot set
     NSFPS_RMARK(kRpApply);
     if (PROF) pf[kRpHotRounds] += 1;
