@@ -442,8 +442,9 @@ constexpr uint32_t kCopyLanes = kRunThreads / kHot;  // threads per hot copy (an
 constexpr uint32_t kCmp = kHot / kCopyLanes;         // copies each of them compares against
 constexpr uint32_t kSelBins = 256;
 constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
-constexpr uint32_t kWalkRows = 64;     // cubes over more coarse rows, or over more
-constexpr uint32_t kWalkEntries = 32;  // list entries, are applied by every thread
+constexpr uint32_t kWalkRows = 64;        // cubes over more coarse rows, or with more
+constexpr uint32_t kWalkLaneEntries = 16;  // list entries in one lane's rows, are
+                                          // applied by every thread
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
 static_assert((kCopyLanes == 4 || kCopyLanes == 8) && kHot == 64, "the run kernel layout");
 static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
@@ -452,7 +453,7 @@ static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
   kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail, kRpBig, kRpRank,
-  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWords = 16
+  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWalk, kRpPublish, kRpWords = 16
 };
 
 // Cell inside the cube of a sample at cell qc with packed half-widths h
@@ -509,20 +510,17 @@ __device__ __forceinline__ uint32_t hot_slot(uint32_t i) {
   return (i % kCmp) * kCopyLanes + i / kCmp;
 }
 
-// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes): quad
-// permutes, then for groups of eight the other quad through a lane shuffle
-// (a row_half_mirror DPP step here gave wrong sums now and then with two
-// waves per SIMD; the shuffle has not).
+// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes).
 __device__ __forceinline__ uint32_t group_sum(uint32_t v) {
   v += dpp_mov<kDppQuad1032>(v);
   v += dpp_mov<kDppQuad2301>(v);
-  if (kCopyLanes == 8) v += (uint32_t)__shfl_xor((int)v, 4, 64);
+  if (kCopyLanes == 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
   return v;
 }
 __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   v = min(v, dpp_mov<kDppQuad1032>(v));
   v = min(v, dpp_mov<kDppQuad2301>(v));
-  if (kCopyLanes == 8) v = min(v, (uint32_t)__shfl_xor((int)v, 4, 64));
+  if (kCopyLanes == 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
   return v;
 }
 
@@ -559,7 +557,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
                                         //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
-  __shared__ uint2 s_rec[kHot];         // samples of a hot run: copy, half-widths
+  __shared__ uint4 s_rp[kHot];          // samples of a hot run in order: {x, y, z, row}
+  __shared__ uint4 s_rc[kHot];          //   {cube lo, cube hi (clipped), cell, half-widths}
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
   __shared__ uint32_t s_big[2];                         // samples with large cubes
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
@@ -690,6 +689,9 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   if (tid < kSelBins) s_sel[0][tid] = 0;
   if (tid == 0) s_nhot = 0;
   __syncthreads();
+  // coarse grid, kept in vector registers (the scalar file is full in the walk)
+  const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
+  const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
   NSFPS_RMARK(kRpLoad);
   while (true) {
     // ---- hot threshold: live entries (key >= B); their maximum and count
@@ -867,8 +869,12 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       }
       // the prefix: samples npk .. npk + P - 1 in rank order
       const bool acc = remj && rank < P;
-      if (acc && hq == 0)
-        s_rec[npk + rank] = make_uint2(hj | ((mx.w & 0xfffffu) << 8), mx.w >> 20);
+      if (acc && hq == 0) {
+        uint32_t lo_c, hi_c;
+        cube_corners(mx.x, mx.w, b0, b1, b2, lo_c, hi_c);
+        s_rp[npk + rank] = s_hp[hj];
+        s_rc[npk + rank] = make_uint4(lo_c, hi_c, mx.x, mx.w);
+      }
       npk += P;
       if (npk >= room) {  // the last sample needs no update
         stop = 2;
@@ -929,65 +935,47 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       NSFPS_RMARK(kRpPhases);
       if (PROF) pf[kRpPhaseCount] += 1;
     }
+    __syncthreads();  // the loop can leave right after the last records were written
     NSFPS_RMARK(kRpPhases);
     // ---- the hot run's samples -> global memory and every list entry.
-    // Lane group k takes sample k: a cube whose coarse cells span at most
-    // kWalkRows rows and hold at most kWalkEntries list entries is applied by
-    // walking those rows of the cell index (distances min-ed into LDS); a
-    // larger one is flagged and applied below by every thread to its own
-    // entries.
+    // Lane group k takes sample k and walks the coarse rows its cube spans,
+    // min-ing distances into LDS.  A cube over more than kWalkRows rows, or a
+    // lane meeting more than kWalkLaneEntries entries in its rows, flags the
+    // sample instead; flagged samples are applied below by every thread to its
+    // own entries (applying a sample twice changes nothing).
     {
       const uint32_t k = tid / kCopyLanes, q = tid % kCopyLanes;
       if (k < npk) {
-        // kept in vector registers: the scalar file is full here
-        const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
-        const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
-        const uint2 r = s_rec[k];
-        const uint32_t cp = r.x & 255u;
-        const uint4 a0 = s_hp[cp];
-        const uint32_t qc = s_hx[cp].x;
-        const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
-        uint32_t lo_c, hi_c;
-        cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
+        const uint4 rp = s_rp[k], rc = s_rc[k];
+        const uint32_t lo_c = rc.x, hi_c = rc.y, qc = rc.z, hh = rc.w;
         if (q == 0) {
-          out[it + k] = (int32_t)a0.w;
-          pick_p[np + k] = make_float4(__uint_as_float(a0.x), __uint_as_float(a0.y),
-                                       __uint_as_float(a0.z), 0.f);
+          out[it + k] = (int32_t)rp.w;
+          pick_p[np + k] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
+                                       __uint_as_float(rp.z), 0.f);
           pick_c[np + k] = make_uint2(lo_c, hi_c);
         }
         const uint32_t x0 = (lo_c & 1023u) >> gsx, x1 = (hi_c & 1023u) >> gsx;
         const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
         const uint32_t z0 = (lo_c >> 20) >> gsz, z1 = (hi_c >> 20) >> gsz;
         const uint32_t ny = y1 - y0 + 1, nrows = ny * (z1 - z0 + 1);
-        uint32_t ry0 = q, rz0 = 0;  // first row of this lane
-        while (ry0 >= ny) {
-          ry0 -= ny;
-          ++rz0;
-        }
-        uint32_t cnt = 0;  // list entries in the coarse cells of the cube
-        if (nrows <= kWalkRows) {
-          uint32_t ry = ry0, rz = rz0;
+        bool big = nrows > kWalkRows;
+        if (!big) {
+          // row rr = rz * ny + ry; rz = floor((rr + 0.5) / ny) holds with an
+          // approximate reciprocal: rr < 64 leaves a margin of 0.5 / ny
+          const float rny = __builtin_amdgcn_rcpf((float)ny);
+          const float px = __uint_as_float(rp.x), py = __uint_as_float(rp.y),
+                      pz = __uint_as_float(rp.z);
+          uint32_t budget = kWalkLaneEntries;
           for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
+            const uint32_t rz = (uint32_t)(((float)rr + 0.5f) * rny), ry = rr - rz * ny;
             const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
-            cnt += s_cell[rw + x1 + 1] - s_cell[rw + x0];
-            ry += kCopyLanes;
-            while (ry >= ny) {
-              ry -= ny;
-              ++rz;
+            const uint32_t e0 = s_cell[rw + x0], e1 = s_cell[rw + x1 + 1];
+            if (e1 - e0 > budget) {
+              big = true;
+              break;
             }
-          }
-        }
-        cnt = group_sum(cnt);
-        if (nrows > kWalkRows || cnt > kWalkEntries) {
-          if (q == 0) atomicOr(&s_big[k >> 5], 1u << (k & 31u));
-        } else if (cnt) {
-          const float px = __uint_as_float(a0.x), py = __uint_as_float(a0.y),
-                      pz = __uint_as_float(a0.z);
-          uint32_t ry = ry0, rz = rz0;
-          for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
-            const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
-            const uint32_t e1 = s_cell[rw + x1 + 1];
-            for (uint32_t e = s_cell[rw + x0]; e < e1; ++e) {
+            budget -= e1 - e0;
+            for (uint32_t e = e0; e < e1; ++e) {
               const uint4 p = s_pc[e];
               if (in_cube_h(p.w, qc, hh)) {
                 const uint32_t dd =
@@ -996,15 +984,12 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
                 atomicMin(&s_dd[e], dd);  // non-negative floats order like their bits
               }
             }
-            ry += kCopyLanes;
-            while (ry >= ny) {
-              ry -= ny;
-              ++rz;
-            }
           }
         }
+        if (big) atomicOr(&s_big[k >> 5], 1u << (k & 31u));
       }
-      __syncthreads();  // the quads' updates are in LDS
+      NSFPS_RMARK(kRpWalk);
+      __syncthreads();  // the walks' updates are in LDS
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s)
         if (s * kRunThreads + tid < nlist) d[s] = __uint_as_float(s_dd[s * kRunThreads + tid]);
@@ -1014,11 +999,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         while (bigm) {
           const uint32_t kb = (uint32_t)__builtin_ctzll(bigm);
           bigm &= bigm - 1;
-          const uint2 r = s_rec[kb];
-          const uint32_t cp = r.x & 255u;
-          const uint4 a0 = s_hp[cp];
-          const uint32_t qc = s_hx[cp].x;
-          const uint32_t hh = ((r.x >> 8) & 1023u) | (((r.x >> 18) & 1023u) << 10) | (r.y << 20);
+          const uint4 a0 = s_rp[kb], rc = s_rc[kb];
+          const uint32_t qc = rc.z, hh = rc.w;
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
             if (in_cube_h(cc[s], qc, hh)) {
@@ -1038,11 +1020,12 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     np += npk;
     // the next hot set's live maximum and count, and its zeroed histogram and
     // copy counter
+    NSFPS_RMARK(kRpApply);
     publish_live(d, lo, bkey, s_wk, s_wn);
     if (tid < kSelBins) s_sel[0][tid] = 0;
     if (tid == 0) s_nhot = 0;
-    __syncthreads();  // s_hq / s_hp / s_rec are rewritten by the next hot set
-    NSFPS_RMARK(kRpApply);
+    __syncthreads();  // s_hq / s_hp / s_rp / s_rc are rewritten by the next hot set
+    NSFPS_RMARK(kRpPublish);
     if (PROF) pf[kRpHotRounds] += 1;
     if (stop == 2) {
       done = true;
