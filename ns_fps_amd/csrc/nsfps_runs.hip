@@ -442,6 +442,7 @@ constexpr uint32_t kCopyLanes = kRunThreads / kHot;  // threads per hot copy (an
 constexpr uint32_t kCmp = kHot / kCopyLanes;         // copies each of them compares against
 constexpr uint32_t kSelBins = 256;
 constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
+constexpr uint32_t kPhaseMin = 12;  // copies >= the hot threshold that justify another phase
 constexpr uint32_t kWalkRows = 64;        // cubes over more coarse rows, or with more
 constexpr uint32_t kWalkLaneEntries = 16;  // list entries in one lane's rows, are
                                           // applied by every thread
@@ -882,6 +883,10 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       }
       if (P >= nnz && nnz < nge) {  // the next copy has distance 0: src/yuezu_fps.cpp:705-706
         stop = 2;
+        break;
+      }
+      if (nge - P < kPhaseMin) {  // few copies left: they go back to the next selection
+        stop = P >= nge ? 1u : 0u;
         break;
       }
       // the accepted cubes on the remaining copies
