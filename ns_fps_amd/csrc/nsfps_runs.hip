@@ -981,13 +981,14 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
             }
             budget -= e1 - e0;
             for (uint32_t e = e0; e < e1; ++e) {
+              // one 16-byte read: the min is unconditional (a no-op outside the
+              // cube), so the cell is not read ahead of the coordinates
               const uint4 p = s_pc[e];
-              if (in_cube_h(p.w, qc, hh)) {
-                const uint32_t dd =
-                    __float_as_uint(sqdist(__uint_as_float(p.x), __uint_as_float(p.y),
-                                           __uint_as_float(p.z), px, py, pz));
-                atomicMin(&s_dd[e], dd);  // non-negative floats order like their bits
-              }
+              const uint32_t dd =
+                  __float_as_uint(sqdist(__uint_as_float(p.x), __uint_as_float(p.y),
+                                         __uint_as_float(p.z), px, py, pz));
+              // non-negative floats order like their bits
+              atomicMin(&s_dd[e], in_cube_h(p.w, qc, hh) ? dd : 0xffffffffu);
             }
           }
         }
