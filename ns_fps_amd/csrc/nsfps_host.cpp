@@ -441,7 +441,10 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
 // Speculative-run rounds until every cloud is done.  Rounds are enqueued in
 // growing batches; a round of a finished cloud returns at once.  Between
 // batches the host reads each cloud's done flag, sample count and list
-// overflow flag.
+// overflow flag.  Rounds run without refinement passes (the update pass's
+// windows nearly always resolve the threshold) until a round had to force it
+// and got a list under a quarter full; from the next batch on, every round
+// gets kRefinePasses passes.
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds, hipStream_t st,
                         bool profile, uint64_t *rounds_out) {
   uint32_t max_nl1 = 1;
@@ -454,9 +457,9 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   };
   std::vector<Probe> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
-  uint32_t batch = 4, stalled = 0;
+  uint32_t batch = 4, stalled = 0, passes = 0;
   while (true) {
-    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, profile, st));
+    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
     enqueued += batch;
     for (uint32_t i = 0; i < nc; ++i) {
       const CloudDev &c = plans[i].dev;
@@ -471,6 +474,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       if (q.rs.err) return fail(NSFPS_EDEVICE, "internal: speculative list overflow");
       all = all && q.done;
       samples += q.iter;
+      if (q.rs.forced) passes = kRefinePasses;
       rounds = std::max<uint64_t>(rounds, q.rs.rounds);
     }
     *rounds_out = rounds;

@@ -30,7 +30,7 @@ constexpr uint32_t kNone = 0xffffffffu;
 constexpr uint32_t kListCap = 1024;
 constexpr uint32_t kHistBins = 4096;
 constexpr uint32_t kHists = 4;
-constexpr uint32_t kRefinePasses = 2;
+constexpr uint32_t kRefinePasses = 2;  // refinement passes when they are launched
 
 // Range values the kernels need, all derived on the host exactly as the
 // reference derives them (src/yuezu_fps.cpp:7-11, 136-161, 170-193).
@@ -75,6 +75,8 @@ struct RunState {
   uint32_t nlist;     // list entries gathered this round
   uint32_t rounds;    // rounds that ran (statistics)
   uint32_t err;       // set if a list overflowed (internal error)
+  uint32_t forced;    // rounds whose threshold was forced for want of refinement passes
+  uint32_t pad;
 };
 
 // Everything one cloud's kernels touch.  Device pointers; passed by value to

@@ -47,6 +47,6 @@ constexpr uint32_t kProfWords = 24;
 // speculative-run engine
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, bool profile, hipStream_t st);
+                         uint32_t rounds, uint32_t passes, bool profile, hipStream_t st);
 
 }  // namespace nsfps

@@ -127,8 +127,12 @@ __device__ __forceinline__ uint32_t coarse_shift(uint32_t s0) {
 }
 
 // Replays the selection from the update pass's histograms and the first
-// `avail - 1` refinement histograms.
-__device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t *sc) {
+// `avail - 1` refinement histograms; `passes` refinement passes run this
+// round, so the threshold is forced at step `passes` (forced is set when that
+// rule, not the histograms, ended the selection with a list under a quarter
+// full).
+__device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, uint32_t *sc,
+                          bool *forced = nullptr) {
   const NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   Sel s;
   s.kref = rs.kref0;
@@ -151,7 +155,9 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t *sc) {
       return s;
     }
     s.total += st.before;
-    if (st.before >= s.cap / 2 || s.S == 0 || p == kRefinePasses) {
+    if (st.before >= s.cap / 2 || s.S == 0 || p == passes) {
+      // forced, and the list under a quarter full: refinement would have paid
+      if (forced) *forced = st.before < s.cap / 2 && s.S != 0 && s.total < kListCap / 4;
       s.bkey = s.kref - ((uint64_t)st.bs << s.S) + 1;  // keys above bin bs
       s.state = s.total ? 1u : 2u;
       return s;
@@ -305,13 +311,13 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
 // level-1 nodes: the pass is usually skipped, and then costs little more than
 // its launch.
 __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restrict__ clouds,
-                                                         uint32_t pass) {
+                                                         uint32_t pass, uint32_t passes) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ uint32_t s_sc[kPassWaves + 2];
   const CloudDev &c = clouds[blockIdx.y];
   if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const Sel s = sel_replay(c, pass, s_sc);
+  const Sel s = sel_replay(c, pass, passes, s_sc);
   if (s.state != 0 || s.pass != pass) return;
   const uint64_t wlo = window_lo(s.kref, s.S);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
@@ -348,14 +354,16 @@ __device__ __forceinline__ uint32_t bit_length(uint64_t v) { return v ? 64u - __
 // (more than kListCap keys inside the finest bin), the threshold is the
 // maximum key itself: a run of one sample.  Few workgroups, each striding over
 // the level-1 nodes; most nodes hold no key above the threshold.
-__global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restrict__ clouds) {
+__global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restrict__ clouds,
+                                                         uint32_t passes) {
   __shared__ uint32_t s_sc[kPassWaves + 2];
   __shared__ uint64_t s_wk[kPassWaves];
   const CloudDev &c = clouds[blockIdx.y];
   if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
-  const Sel s = sel_replay(c, kRefinePasses + 1, s_sc);
+  bool forced = false;
+  const Sel s = sel_replay(c, passes + 1, passes, s_sc, &forced);
   uint64_t bkey = s.bkey;
   if (s.state == 2) {
     uint64_t best = 0;
@@ -372,6 +380,9 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   }
   if (blockIdx.x == 0 && tid == 0) {
     rs.bkey = bkey;
+    // the first rounds start from windows over the whole key range and are
+    // forced as a rule; later forced rounds ask for refinement passes
+    rs.forced += forced && rs.rounds >= 2 ? 1u : 0u;
     // next round: fine bins of about 1/2048 of this round's key span
     uint32_t nx = bit_length(rs.kref0 - bkey + 1);
     nx = nx > 11u ? nx - 11u : 0u;
@@ -1076,6 +1087,7 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
     rs.nlist = 0;
     rs.rounds = 0;
     rs.err = 0;
+    rs.forced = 0;
     const float4 p0 = *gptr(c.root_pos);
     gptr(c.pick_p)[0] = make_float4(p0.x, p0.y, p0.z, INFINITY);
     gptr(c.pick_c)[0] =
@@ -1095,14 +1107,14 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 }
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, bool profile, hipStream_t st) {
+                         uint32_t rounds, uint32_t passes, bool profile, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
   for (uint32_t r = 0; r < rounds; ++r) {
     k_update<<<grid, kPassThreads, 0, st>>>(d_clouds);
-    for (uint32_t p = 1; p <= kRefinePasses; ++p)
-      k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p);
-    k_gather<<<sparse, kPassThreads, 0, st>>>(d_clouds);
+    for (uint32_t p = 1; p <= passes; ++p)
+      k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
+    k_gather<<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
     if (profile)
       k_run<true><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
     else
