@@ -99,6 +99,43 @@ __global__ __launch_bounds__(1024) void k_scan_excl(uint32_t *__restrict__ data,
   if (tid == 1023) data[len] = wsum[15];
 }
 
+// Longer scans: chunks of kScanChunk values, four consecutive per thread.
+// Pass 1 sums every chunk, k_scan_excl scans the sums, pass 2 rescans every
+// chunk from its offset.
+constexpr uint32_t kScanChunk = 4096;
+constexpr uint32_t kScanSingleMax = 16384;  // one workgroup up to here
+
+__device__ __forceinline__ uint4 scan_load4(const uint32_t *data, uint32_t len, uint32_t i) {
+  return make_uint4(i < len ? data[i] : 0u, i + 1 < len ? data[i + 1] : 0u,
+                    i + 2 < len ? data[i + 2] : 0u, i + 3 < len ? data[i + 3] : 0u);
+}
+
+__global__ __launch_bounds__(1024) void k_scan_sums(const uint32_t *__restrict__ data, uint32_t len,
+                                                    uint32_t *__restrict__ sums) {
+  __shared__ uint32_t wsum[16];
+  const uint4 v = scan_load4(data, len, blockIdx.x * kScanChunk + threadIdx.x * 4);
+  uint32_t tot;
+  block_excl_scan<16>(v.x + v.y + v.z + v.w, wsum, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(1024) void k_scan_apply(uint32_t *__restrict__ data, uint32_t len,
+                                                     const uint32_t *__restrict__ sums) {
+  __shared__ uint32_t wsum[16];
+  const uint32_t i = blockIdx.x * kScanChunk + threadIdx.x * 4;
+  const uint4 v = scan_load4(data, len, i);
+  uint32_t tot;
+  uint32_t run = sums[blockIdx.x] + block_excl_scan<16>(v.x + v.y + v.z + v.w, wsum, &tot);
+  if (i < len) data[i] = run;
+  run += v.x;
+  if (i + 1 < len) data[i + 1] = run;
+  run += v.y;
+  if (i + 2 < len) data[i + 2] = run;
+  run += v.z;
+  if (i + 3 < len) data[i + 3] = run;
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) data[len] = sums[gridDim.x];
+}
+
 // Stable scatter of one digit pass.  Each wave ranks its 1024 keys in order
 // (16 rounds of 64): lanes with the same digit are found with 8 ballots, the
 // running per-digit count of the wave lives in LDS; waves are then offset by
@@ -349,8 +386,17 @@ hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, con
   return hipGetLastError();
 }
 
-hipError_t launch_scan(uint32_t *data, uint32_t len, hipStream_t st) {
-  k_scan_excl<<<1, 1024, 0, st>>>(data, len);
+uint32_t scan_tmp_len(uint32_t len) { return cdiv(len, kScanChunk) + 1; }
+
+hipError_t launch_scan(uint32_t *data, uint32_t len, uint32_t *tmp, hipStream_t st) {
+  if (len <= kScanSingleMax) {
+    k_scan_excl<<<1, 1024, 0, st>>>(data, len);
+  } else {
+    const uint32_t nb = cdiv(len, kScanChunk);
+    k_scan_sums<<<nb, 1024, 0, st>>>(data, len, tmp);
+    k_scan_excl<<<1, 1024, 0, st>>>(tmp, nb);
+    k_scan_apply<<<nb, 1024, 0, st>>>(data, len, tmp);
+  }
   return hipGetLastError();
 }
 
@@ -358,15 +404,16 @@ uint32_t radix_hist_len(uint32_t n) { return 256u * cdiv(n, kSortTile) + 1; }
 
 hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
                              uint32_t *vals_tmp, uint32_t n, int key_bits, uint32_t *hist,
-                             bool iota_values, uint32_t **keys_out, uint32_t **vals_out,
-                             hipStream_t st) {
+                             uint32_t *scan_tmp, bool iota_values, uint32_t **keys_out,
+                             uint32_t **vals_out, hipStream_t st) {
   if (key_bits <= 0) return hipErrorInvalidValue;
   uint32_t nb = cdiv(n, kSortTile);
   uint32_t *ka = keys, *va = vals, *kb = keys_tmp, *vb = vals_tmp;
   bool first = true;
   for (int shift = 0; shift < key_bits; shift += 8) {
     k_radix_hist<<<nb, kSortThreads, 0, st>>>(ka, n, shift, hist, nb);
-    k_scan_excl<<<1, 1024, 0, st>>>(hist, 256u * nb);
+    const hipError_t e = launch_scan(hist, 256u * nb, scan_tmp, st);
+    if (e != hipSuccess) return e;
     k_radix_scatter<<<nb, kSortThreads, 0, st>>>(ka, (first && iota_values) ? nullptr : va, kb,
                                                  vb, n, shift, hist, nb);
     first = false;

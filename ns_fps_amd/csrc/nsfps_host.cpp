@@ -231,7 +231,7 @@ struct CloudPlan {
 };
 
 struct Scratch {
-  uint32_t *bucket, *fine, *kA, *kB, *vA, *vB, *vC, *hist;
+  uint32_t *bucket, *fine, *kA, *kB, *vA, *vB, *vC, *hist, *scan;
 };
 
 int key_bits_for(uint32_t T) {
@@ -293,7 +293,7 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.r = p.rng.dev;
 }
 
-void layout_scratch(Bump &bp, uint32_t n, Scratch &s) {
+void layout_scratch(Bump &bp, uint32_t n, uint32_t tmax, Scratch &s) {
   s.bucket = bp.take<uint32_t>(n);
   s.fine = bp.take<uint32_t>(n);
   s.kA = bp.take<uint32_t>(n);
@@ -302,6 +302,7 @@ void layout_scratch(Bump &bp, uint32_t n, Scratch &s) {
   s.vB = bp.take<uint32_t>(n);
   s.vC = bp.take<uint32_t>(n);
   s.hist = bp.take<uint32_t>(radix_hist_len(n) + 16);
+  s.scan = bp.take<uint32_t>(scan_tmp_len(std::max(radix_hist_len(n), tmax + 1)) + 16);
 }
 
 // LDS layout of the single-workgroup loop for one cloud: required regions,
@@ -365,8 +366,8 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   HIP_TRY(launch_cell_keys(xyz, n, p.rng.dev, p.d_lut, s.bucket, s.fine, p.d_counts, p.d_small,
                            st));
   HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, st));
-  HIP_TRY(launch_scan(p.d_counts, T, st));  // -> first dense position per bucket
-  HIP_TRY(launch_scan(p.d_lc, T, st));      // -> first leaf per bucket (dense)
+  HIP_TRY(launch_scan(p.d_counts, T, s.scan, st));  // -> first dense position per bucket
+  HIP_TRY(launch_scan(p.d_lc, T, s.scan, st));      // -> first leaf per bucket (dense)
   uint32_t hs[3] = {0, 0, 0};
   HIP_TRY(hipMemcpyAsync(&hs[0], p.d_small, 8, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipMemcpyAsync(&hs[2], p.d_lc + T, 4, hipMemcpyDeviceToHost, st));
@@ -391,7 +392,8 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   const int bt = std::max(1, key_bits_for(T));
   uint32_t *lorig = nullptr, *ko = nullptr;
   HIP_TRY(hipMemcpyAsync(s.kA, s.bucket, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, true, &ko, &lorig, st));
+  HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, s.scan, true, &ko, &lorig,
+                            st));
   // sort 2: (bucket, sub-cell) inside the logical order; values = logical rank
   const int fb = std::min<int>((int)kFineBits, 32 - bt);
   const int fshift = (int)kFineBits - fb;
@@ -400,7 +402,8 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   uint32_t *v2 = (lorig == s.vA) ? s.vB : s.vA;
   HIP_TRY(launch_key2(lorig, s.bucket, s.fine, n, fshift, fb, k2, st));
   uint32_t *prank = nullptr, *kdummy = nullptr;
-  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, bt + fb, s.hist, true, &kdummy, &prank, st));
+  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, bt + fb, s.hist, s.scan, true, &kdummy,
+                            &prank, st));
   if (padded) {
     HIP_TRY(hipMemsetAsync(c.P4, 0, (size_t)c.nslots * sizeof(float4), st));
     HIP_TRY(hipMemsetAsync(const_cast<uint2 *>(c.RO), 0, (size_t)c.nslots * sizeof(uint2), st));
@@ -499,18 +502,21 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   if (rc) return rc;
   Arena &a = *ap;
   hipStream_t st = user_stream ? user_stream : a.stream;
-  uint32_t nmax = 0;
-  for (auto &p : plans) nmax = std::max(nmax, p.n);
+  uint32_t nmax = 0, tmax = 0;
+  for (auto &p : plans) {
+    nmax = std::max(nmax, p.n);
+    tmax = std::max(tmax, p.rng.dev.T);
+  }
   Bump meas(nullptr);
   for (auto &p : plans) layout_cloud(meas, p);
   Scratch sc{};
-  layout_scratch(meas, nmax, sc);
+  layout_scratch(meas, nmax, tmax, sc);
   meas.take<CloudDev>(plans.size());
   rc = arena_reserve(a, meas.off + 4096);
   if (rc) return rc;
   Bump bp(a.base);
   for (auto &p : plans) layout_cloud(bp, p);
-  layout_scratch(bp, nmax, sc);
+  layout_scratch(bp, nmax, tmax, sc);
   CloudDev *d_clouds = bp.take<CloudDev>(plans.size());
 
   HIP_TRY(hipEventRecord(a.ev[0], st));

@@ -14,11 +14,14 @@ namespace nsfps {
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
                             hipStream_t st);
-hipError_t launch_scan(uint32_t *data, uint32_t len, hipStream_t st);
+// exclusive scan in place, data[len] = total; tmp holds scan_tmp_len(len) words
+uint32_t scan_tmp_len(uint32_t len);
+hipError_t launch_scan(uint32_t *data, uint32_t len, uint32_t *tmp, hipStream_t st);
 uint32_t radix_hist_len(uint32_t n);
 hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
                              uint32_t *vals_tmp, uint32_t n, int key_bits, uint32_t *hist,
-                             bool iota_values, uint32_t **keys_out, uint32_t **vals_out,
+                             uint32_t *scan_tmp, bool iota_values, uint32_t **keys_out,
+                             uint32_t **vals_out,
                              hipStream_t st);
 hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,
                        uint32_t n, int fine_shift, int fine_bits, uint32_t *key2,
