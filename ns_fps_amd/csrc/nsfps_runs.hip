@@ -36,6 +36,7 @@ constexpr uint32_t kPassWaves = kPassThreads / 64;
 constexpr uint32_t kLeavesPerWave = kFan / kPassWaves;
 constexpr uint32_t kMaxShift = 52;  // kHistBins << 52 covers the whole u64 key range
 constexpr uint32_t kSparseGroups = 128;  // workgroups per cloud of the refinement and gather passes
+constexpr uint32_t kGatherNodes = 16;    // nodes per list-range claim of the gather pass
 
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
   return x | (y << 10) | (z << 20);
@@ -388,11 +389,49 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     nx = nx > 11u ? nx - 11u : 0u;
     rs.s0_next = nx < kMaxShift ? nx : kMaxShift;
   }
-  for (uint32_t g = blockIdx.x; g < c.nl1; g += gridDim.x) {
-    if (gptr(c.l1_key)[g] < bkey) continue;
-    for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-      const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
-      if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < bkey) continue;
+  // Nodes in chunks of kGatherNodes: every wave counts the keys >= bkey in its
+  // leaves of the chunk, the workgroup takes one range of the list for all of
+  // them (one global atomic), and the waves read those leaves again (from L2)
+  // to write their entries.
+  __shared__ uint32_t s_cnt, s_base;
+  for (uint32_t c0 = blockIdx.x; c0 < c.nl1; c0 += kGatherNodes * gridDim.x) {
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    uint64_t lmask = 0;  // bit kLeavesPerWave * jn + k: leaf k of node jn has keys >= bkey
+    uint32_t mine = 0;
+    for (uint32_t jn = 0; jn < kGatherNodes; ++jn) {
+      const uint32_t g = c0 + jn * gridDim.x;
+      if (g >= c.nl1) break;
+      if (gptr(c.l1_key)[g] < bkey) continue;
+#pragma unroll
+      for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+        const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
+        if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < bkey) continue;
+        const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
+        const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
+        bool take = false;
+        if (lane < cnt) {
+          const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
+          take = (((uint64_t)__float_as_uint(d) << 32) | ~gptr(c.RO)[st + lane].x) >= bkey;
+        }
+        const uint64_t m = __ballot(take);
+        if (m) {
+          lmask |= 1ull << (kLeavesPerWave * jn + k);
+          mine += (uint32_t)__popcll(m);
+        }
+      }
+    }
+    uint32_t base = 0;
+    if (lane == 0 && mine) base = atomicAdd(&s_cnt, mine);
+    __syncthreads();
+    if (tid == 0) s_base = s_cnt ? atomicAdd(&rs.nlist, s_cnt) : 0u;
+    __syncthreads();
+    base = s_base + rdlane(base, 0);
+    while (lmask) {
+      const uint32_t j = (uint32_t)__builtin_ctzll(lmask);
+      lmask &= lmask - 1;
+      const uint32_t g = c0 + (j / kLeavesPerWave) * gridDim.x;
+      const uint32_t leaf = g * kFan + wave * kLeavesPerWave + j % kLeavesPerWave;
       const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
       const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
       const uint32_t cell = gptr(c.leaf_cell)[leaf];
@@ -405,10 +444,6 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       const bool take =
           lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
       const uint64_t m = __ballot(take);
-      if (!m) continue;
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&rs.nlist, (uint32_t)__popcll(m));
-      base = rdlane(base, 0);
       if (take) {
         const uint32_t i = base + lanes_below(m);
         if (i < kListCap) {
@@ -419,6 +454,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
           rs.err = 1;
         }
       }
+      base += (uint32_t)__popcll(m);
     }
   }
 }
