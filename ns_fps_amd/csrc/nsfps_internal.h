@@ -26,10 +26,10 @@ constexpr uint32_t kLdsBudget = 160 * 1024 - 1024;
 constexpr uint32_t kNone = 0xffffffffu;
 // Speculative-run engine: list entries (one per thread of the run kernel; also
 // the most picks one run can accept), bins per key histogram, histograms per
-// round (fine and coarse from the update pass, then two refinement passes).
+// round (one from the update pass, then two refinement passes).
 constexpr uint32_t kListCap = 1024;
 constexpr uint32_t kHistBins = 4096;
-constexpr uint32_t kHists = 4;
+constexpr uint32_t kHists = 3;
 constexpr uint32_t kRefinePasses = 2;  // refinement passes when they are launched
 
 // Range values the kernels need, all derived on the host exactly as the
@@ -69,7 +69,7 @@ struct LdsPlan {
 struct RunState {
   uint64_t kref0;     // every key is <= kref0 when the update pass runs
   uint64_t bkey;      // list threshold chosen by the selection
-  uint32_t s0;        // bin shift of the fine histogram of the update pass
+  uint32_t s0;        // bin shift of the update pass's key histogram
   uint32_t s0_next;   // bin shift proposed for the next round
   uint32_t npicks;    // picks of the last run (applied by the next update pass)
   uint32_t nlist;     // list entries gathered this round

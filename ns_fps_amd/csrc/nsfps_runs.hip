@@ -15,7 +15,7 @@
 // the leaf and level-1 keys and histograms the keys for the next threshold.
 //
 // One round, in stream order:
-//   k_update     picks -> points, leaf and level-1 keys, fine + coarse histograms
+//   k_update     picks -> points, leaf and level-1 keys, key histogram
 //   k_refine x2  finer histograms inside the crossing bin, only when needed
 //   k_gather     threshold B (<= kListCap keys above it), list of those points
 //   k_run        samples from the list
@@ -78,10 +78,12 @@ __device__ __forceinline__ uint32_t key_bin(uint64_t key, uint64_t kref, uint32_
 // A histogram over window (kref, S) gives the first bin where the cumulative
 // count exceeds the free capacity; the bins before it are taken.  If they
 // fill less than half of it, that crossing bin is histogrammed again 12 bits
-// finer by the next refinement pass.  The update pass counts two windows
-// below kref0: a fine one (shift s0) and a 4096x wider coarse one, used when
-// the fine window holds under half a list.  When nothing fits (more than
-// kListCap keys share the finest bin) the threshold is the maximum key.
+// finer by the next refinement pass.  The update pass counts one window below
+// kref0 (shift s0, set from the previous round's key span).  A window that
+// holds fewer keys than the list takes all of them: the run is shorter, and
+// the next round's window, sized from this round's span, is 4x wider.  When
+// nothing fits (more than kListCap keys share the finest bin) or the window is
+// empty, the threshold is the maximum key.
 struct Sel {
   uint64_t kref;
   uint64_t bkey;     // resolved threshold
@@ -123,10 +125,6 @@ __device__ Step hist_step(const uint32_t *H, uint32_t cap, uint32_t *sc) {
   return st;
 }
 
-__device__ __forceinline__ uint32_t coarse_shift(uint32_t s0) {
-  return s0 + 12 < kMaxShift ? s0 + 12 : kMaxShift;
-}
-
 // Replays the selection from the update pass's histograms and the first
 // `avail - 1` refinement histograms; `passes` refinement passes run this
 // round, so the threshold is forced at step `passes` (forced is set when that
@@ -144,10 +142,6 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, ui
   s.state = 0;
   s.pass = 0;
   Step st = hist_step(c.hist, s.cap, sc);
-  if (st.bs == kNone && st.tot < kListCap / 2) {
-    s.S = coarse_shift(s.S);
-    st = hist_step(c.hist + kHistBins, s.cap, sc);
-  }
   for (uint32_t p = 0;; ++p) {
     if (st.bs == kNone) {  // the whole window fits
       s.total += st.tot;
@@ -170,7 +164,7 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, ui
       s.pass = p + 1;
       return s;
     }
-    st = hist_step(c.hist + (2 + p) * kHistBins, s.cap, sc);
+    st = hist_step(c.hist + (1 + p) * kHistBins, s.cap, sc);
   }
 }
 
@@ -182,9 +176,10 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 
 // Applies the picks of the last run to the points of level-1 node blockIdx.x,
 // rewrites the keys of the touched leaves and of the node, and counts the keys
-// into the fine and the coarse histogram.
+// inside the histogram window.  Leaves no pick touches whose key lies below
+// the window keep their key and are not read.
 __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restrict__ clouds) {
-  __shared__ uint32_t s_hist[2][kHistBins];
+  __shared__ uint32_t s_hist[kHistBins];
   __shared__ float4 s_pp[kListCap];
   __shared__ uint2 s_pc[kListCap];
   __shared__ uint64_t s_lk[kFan];
@@ -197,18 +192,15 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
   const NSFPS_GLOBAL RunState &rs = rstate(c);
   const uint32_t npicks = min(rs.npicks, kListCap);
   const uint64_t kref = rs.kref0;
-  const uint32_t S = rs.s0, S1 = coarse_shift(S);
-  const uint64_t wlo = window_lo(kref, S1);
+  const uint32_t S = rs.s0;
+  const uint64_t wlo = window_lo(kref, S);
   const float4 nlo = gptr(c.l1_lo)[g], nhi = gptr(c.l1_hi)[g];
   if (nlo.x > nhi.x) return;  // no points
   const uint32_t clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y),
                                  cell_axis(c.r, 2, nlo.z));
   const uint32_t chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y),
                                  cell_axis(c.r, 2, nhi.z));
-  for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
-    s_hist[0][j] = 0;
-    s_hist[1][j] = 0;
-  }
+  for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   if (tid == 0) s_np = 0;
   __syncthreads();
   for (uint32_t i = tid; i < npicks; i += kPassThreads) {
@@ -275,10 +267,8 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
           gptr(c.leaf_pos)[leaf] = pos;
         }
         if (act) {
-          const uint64_t kk = ((uint64_t)hi << 32) | lo;
-          const uint32_t b = key_bin(kk, kref, S), b1 = key_bin(kk, kref, S1);
-          if (b != kNone) atomicAdd(&s_hist[0][b], 1u);
-          if (b1 != kNone) atomicAdd(&s_hist[1][b1], 1u);
+          const uint32_t b = key_bin(((uint64_t)hi << 32) | lo, kref, S);
+          if (b != kNone) atomicAdd(&s_hist[b], 1u);
         }
       }
     }
@@ -298,8 +288,8 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
     }
   }
   NSFPS_GLOBAL uint32_t *H = gptr(c.hist);
-  for (uint32_t j = tid; j < 2 * kHistBins; j += kPassThreads) {
-    const uint32_t v = s_hist[j / kHistBins][j % kHistBins];
+  for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
+    const uint32_t v = s_hist[j];
     if (v) atomicAdd(&H[j], v);
   }
 }
@@ -339,7 +329,7 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
     }
   }
   __syncthreads();
-  NSFPS_GLOBAL uint32_t *H = gptr(c.hist + (1 + pass) * kHistBins);
+  NSFPS_GLOBAL uint32_t *H = gptr(c.hist + pass * kHistBins);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
     const uint32_t v = s_hist[j];
     if (v) atomicAdd(&H[j], v);
