@@ -42,6 +42,35 @@ __device__ __forceinline__ float std_max(float a, float b) { return (a < b) ? b 
 // Point3D::compute_block_indices, one axis (src/yuezu_fps.cpp:170-193):
 // clamp into [min, max - 1e-6], scale by the stored reciprocal, truncate,
 // clamp to the last block.
+// Makes wave-uniform values live in scalar registers at this point.  The
+// compiler otherwise issues each kernel-argument or CloudDev field read at
+// its first use, behind the branches before it, one memory round trip each;
+// values named here are read together, ahead of the first branch.
+template <typename T>
+__device__ __forceinline__ void pin_sgpr1(T v) {
+  asm volatile("" : : "s"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void pin_sgpr(T... v) {  // by value: every read precedes every asm
+  (pin_sgpr1(v), ...);
+}
+
+// Per-lane values: the loads producing them complete here, so loads issued
+// before this point overlap instead of being moved behind a later branch.
+template <typename T>
+__device__ __forceinline__ void pin_vgpr1(T v) {
+  asm volatile("" : : "v"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void pin_vgpr(T... v) {
+  (pin_vgpr1(v), ...);
+}
+
+// The range values cell_axis reads, as arguments of pin_sgpr.
+#define NSFPS_CELL_RANGE(r)                                                                   \
+  (r).mn[0], (r).mn[1], (r).mn[2], (r).hiclamp[0], (r).hiclamp[1], (r).hiclamp[2],           \
+      (r).inv_bs[0], (r).inv_bs[1], (r).inv_bs[2], (r).blocks[0], (r).blocks[1], (r).blocks[2]
+
 __device__ __forceinline__ uint32_t cell_axis(const RangeDev &r, int a, float v) {
   float c = std_max(r.mn[a], std_min(v, r.hiclamp[a]));
   uint32_t i = (uint32_t)((c - r.mn[a]) * r.inv_bs[a]);

@@ -51,13 +51,14 @@ __device__ __forceinline__ bool cell_in(uint32_t cell, uint2 cube) {
 
 // Cube overlapping the cell range [lo, hi] (packed corners).
 __device__ __forceinline__ bool cube_overlaps(uint2 cube, uint32_t lo, uint32_t hi) {
+  bool ok = true;
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     const uint32_t s = 10u * a;
-    if (((cube.x >> s) & 1023u) > ((hi >> s) & 1023u)) return false;
-    if (((cube.y >> s) & 1023u) < ((lo >> s) & 1023u)) return false;
+    ok &= ((cube.x >> s) & 1023u) <= ((hi >> s) & 1023u);
+    ok &= ((cube.y >> s) & 1023u) >= ((lo >> s) & 1023u);
   }
-  return true;
+  return ok;
 }
 
 // Histogram window of a selection pass: kHistBins bins of 2^S keys each, bin
@@ -177,8 +178,14 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // Applies the picks of the last run to the points of level-1 node blockIdx.x,
 // rewrites the keys of the touched leaves and of the node, and counts the keys
 // inside the histogram window.  Leaves no pick touches whose key lies below
-// the window keep their key and are not read.
-__global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restrict__ clouds) {
+// the window keep their key and are not read.  A leaf keeps its key too when
+// no pick lowers the point that holds it (keys only decrease), so its maximum
+// is searched only otherwise.  Reads that do not depend on each other are
+// issued together: the wave's leaf records with the run state and the node's
+// record, a pick's cube with its position, and the points of every leaf of
+// the wave that needs reading.
+__global__ __launch_bounds__(kPassThreads) __attribute__((amdgpu_num_sgpr(60))) void k_update(
+    const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ float4 s_pp[kListCap];
   __shared__ uint2 s_pc[kListCap];
@@ -187,15 +194,31 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
   __shared__ uint32_t s_np;
   const CloudDev &c = clouds[blockIdx.y];
   const uint32_t g = blockIdx.x;
-  if (g >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // this wave's leaves: lane k < kLeavesPerWave holds leaf leaf0 + k's record
+  const uint32_t leaf0 = g * kFan + wave * kLeavesPerWave;
+  uint64_t mkey = 0;
+  uint32_t mcell = 0, mst = 0, mcnt = 0;
+  float4 mpos = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (lane < kLeavesPerWave && leaf0 + lane < c.nleaves) {
+    mkey = gptr(c.leaf_key)[leaf0 + lane];
+    mpos = gptr(c.leaf_pos)[leaf0 + lane];
+    mcell = gptr(c.leaf_cell)[leaf0 + lane];
+    mst = __float_as_uint(gptr(c.leaf_lo)[leaf0 + lane].w);
+    mcnt = __float_as_uint(gptr(c.leaf_hi)[leaf0 + lane].w);
+  }
   const NSFPS_GLOBAL RunState &rs = rstate(c);
+  const uint32_t done = *gptr(c.done);
   const uint32_t npicks = min(rs.npicks, kListCap);
   const uint64_t kref = rs.kref0;
   const uint32_t S = rs.s0;
+  const uint32_t gn = g < c.nl1 ? g : 0u;  // read unconditionally, used only if g < nl1
+  const uint64_t nkey = gptr(c.l1_key)[gn];
+  const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
+  // the run state and the node's record are read together, ahead of the exit
+  pin_sgpr(done, npicks, kref, S, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
+  if (g >= c.nl1 || done || nlo.x > nhi.x) return;  // finished, or no points
   const uint64_t wlo = window_lo(kref, S);
-  const float4 nlo = gptr(c.l1_lo)[g], nhi = gptr(c.l1_hi)[g];
-  if (nlo.x > nhi.x) return;  // no points
   const uint32_t clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y),
                                  cell_axis(c.r, 2, nlo.z));
   const uint32_t chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y),
@@ -205,68 +228,95 @@ __global__ __launch_bounds__(kPassThreads) void k_update(const CloudDev *__restr
   __syncthreads();
   for (uint32_t i = tid; i < npicks; i += kPassThreads) {
     const uint2 cb = gptr(c.pick_c)[i];
-    if (cube_overlaps(cb, clo, chi)) {
+    const float4 pp = gptr(c.pick_p)[i];
+    const float px = pp.x, py = pp.y, pz = pp.z;
+    const uint32_t c0 = cb.x, c1 = cb.y;
+    pin_vgpr(c0, c1, px, py, pz);  // both reads in flight together
+    if (cube_overlaps(make_uint2(c0, c1), clo, chi)) {
       const uint32_t k = atomicAdd(&s_np, 1u);
-      s_pp[k] = gptr(c.pick_p)[i];
-      s_pc[k] = cb;
+      s_pp[k] = make_float4(px, py, pz, 0.f);
+      s_pc[k] = make_uint2(c0, c1);
     }
   }
   __syncthreads();
   const uint32_t nsel = s_np;
-  if (nsel == 0 && gptr(c.l1_key)[g] < wlo) return;  // nothing changes, nothing to count
+  if (nsel == 0 && nkey < wlo) return;  // nothing changes, nothing to count
+  // which leaves a pick touches (hm: the first 64 picks whose cube holds the
+  // leaf's cell), and which must be read
+  uint32_t cell[kLeavesPerWave], st[kLeavesPerWave], cnt[kLeavesPerWave];
+  uint64_t okey[kLeavesPerWave], hm[kLeavesPerWave];
+  bool hit[kLeavesPerWave], need[kLeavesPerWave];
+#pragma unroll
+  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+    cell[k] = rdlane(mcell, k);
+    st[k] = rdlane(mst, k);
+    cnt[k] = rdlane(mcnt, k);
+    okey[k] = ((uint64_t)rdlane((uint32_t)(mkey >> 32), k) << 32) | rdlane((uint32_t)mkey, k);
+    hm[k] = __ballot(lane < nsel && cell_in(cell[k], s_pc[lane]));
+    bool h = hm[k] != 0;
+    for (uint32_t cb = 64; cb < nsel && !h; cb += 64)
+      h = __ballot(cb + lane < nsel && cell_in(cell[k], s_pc[cb + lane])) != 0;
+    hit[k] = h;
+    need[k] = leaf0 + k < c.nleaves && (h || okey[k] >= wlo);
+  }
+  float4 p[kLeavesPerWave];
+  uint2 ro[kLeavesPerWave];
+#pragma unroll
+  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+    p[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ro[k] = make_uint2(0u, 0u);
+    if (need[k] && lane < cnt[k]) {
+      p[k] = gptr(c.P4)[st[k] + lane];
+      ro[k] = gptr(c.RO)[st[k] + lane];
+    }
+  }
+#pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
     const uint32_t li = wave * kLeavesPerWave + k;
-    const uint32_t leaf = g * kFan + li;
     uint64_t key = 0;
     float4 pos = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (leaf < c.nleaves) {
-      const uint64_t okey = gptr(c.leaf_key)[leaf];
-      const uint32_t cell = gptr(c.leaf_cell)[leaf];
-      bool hit = false;
-      for (uint32_t cb = 0; cb < nsel && !hit; cb += 64)
-        hit = __ballot(cb + lane < nsel && cell_in(cell, s_pc[cb + lane])) != 0;
-      if (!hit && okey < wlo) {
-        key = okey;
-        pos = gptr(c.leaf_pos)[leaf];
-      } else {
-        const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-        const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
-        const bool act = lane < cnt;
-        float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
-        uint2 ro = make_uint2(0u, 0u);
-        if (act) {
-          p = gptr(c.P4)[st + lane];
-          ro = gptr(c.RO)[st + lane];
-        }
-        float d = p.w;
-        if (hit) {
+    if (leaf0 + k < c.nleaves) {
+      // unchanged unless the point holding the key is lowered below
+      key = okey[k];
+      pos = make_float4(__uint_as_float(rdlane(__float_as_uint(mpos.x), k)),
+                        __uint_as_float(rdlane(__float_as_uint(mpos.y), k)),
+                        __uint_as_float(rdlane(__float_as_uint(mpos.z), k)),
+                        __uint_as_float(rdlane(__float_as_uint(mpos.w), k)));
+      if (need[k]) {
+        const bool act = lane < cnt[k];
+        const uint32_t lo = ~ro[k].x;
+        float d = p[k].w;
+        if (hit[k]) {
           for (uint32_t cb = 0; cb < nsel; cb += 64) {
-            uint64_t m = __ballot(cb + lane < nsel && cell_in(cell, s_pc[cb + lane]));
+            uint64_t m =
+                cb == 0 ? hm[k] : __ballot(cb + lane < nsel && cell_in(cell[k], s_pc[cb + lane]));
             while (m) {
               const uint32_t j = (uint32_t)__ffsll((long long)m) - 1;
               m &= m - 1;
               const float4 q = s_pp[cb + j];
-              const float dd = sqdist(p.x, p.y, p.z, q.x, q.y, q.z);
+              const float dd = sqdist(p[k].x, p[k].y, p[k].z, q.x, q.y, q.z);
               d = dd < d ? dd : d;
             }
           }
-          if (act && d < p.w) ((NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3] = d;
-        }
-        const uint32_t hi = act ? __float_as_uint(d) : 0u, lo = ~ro.x;
-        uint32_t mh;
-        const uint32_t wl = key_winner(hi, lo, act, mh);
-        if (wl < 64) {
-          key = ((uint64_t)mh << 32) | rdlane(lo, wl);
-          pos = make_float4(__uint_as_float(rdlane(__float_as_uint(p.x), wl)),
-                            __uint_as_float(rdlane(__float_as_uint(p.y), wl)),
-                            __uint_as_float(rdlane(__float_as_uint(p.z), wl)),
-                            __uint_as_float(rdlane(ro.y, wl)));
-        }
-        if (hit && lane == 0 && key != okey) {
-          gptr(c.leaf_key)[leaf] = key;
-          gptr(c.leaf_pos)[leaf] = pos;
+          const bool lowered = act && d < p[k].w;
+          if (lowered) ((NSFPS_GLOBAL float *)gptr(c.P4 + st[k] + lane))[3] = d;
+          if (__ballot(lowered && lo == (uint32_t)okey[k])) {
+            const uint32_t hi = act ? __float_as_uint(d) : 0u;
+            uint32_t mh;
+            const uint32_t wl = key_winner(hi, lo, act, mh);
+            key = ((uint64_t)mh << 32) | rdlane(lo, wl);  // the leaf has points: wl < 64
+            pos = make_float4(__uint_as_float(rdlane(__float_as_uint(p[k].x), wl)),
+                              __uint_as_float(rdlane(__float_as_uint(p[k].y), wl)),
+                              __uint_as_float(rdlane(__float_as_uint(p[k].z), wl)),
+                              __uint_as_float(rdlane(ro[k].y, wl)));
+            if (lane == 0) {
+              gptr(c.leaf_key)[leaf0 + k] = key;
+              gptr(c.leaf_pos)[leaf0 + k] = pos;
+            }
+          }
         }
         if (act) {
+          const uint32_t hi = __float_as_uint(d);
           const uint32_t b = key_bin(((uint64_t)hi << 32) | lo, kref, S);
           if (b != kNone) atomicAdd(&s_hist[b], 1u);
         }
