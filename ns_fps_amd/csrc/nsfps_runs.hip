@@ -37,6 +37,7 @@ constexpr uint32_t kLeavesPerWave = kFan / kPassWaves;
 constexpr uint32_t kMaxShift = 52;  // kHistBins << 52 covers the whole u64 key range
 constexpr uint32_t kSparseGroups = 128;  // workgroups per cloud of the refinement and gather passes
 constexpr uint32_t kGatherNodes = 16;    // nodes per list-range claim of the gather pass
+constexpr uint32_t kGatherHold = 4;      // hot leaves per wave whose points stay in registers
 
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
   return x | (y << 10) | (z << 20);
@@ -429,62 +430,76 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     nx = nx > 11u ? nx - 11u : 0u;
     rs.s0_next = nx < kMaxShift ? nx : kMaxShift;
   }
-  // Nodes in chunks of kGatherNodes: every wave counts the keys >= bkey in its
-  // leaves of the chunk, the workgroup takes one range of the list for all of
-  // them (one global atomic), and the waves read those leaves again (from L2)
-  // to write their entries.
+  // Nodes in chunks of kGatherNodes; lane l of a wave holds leaf l % 4 of the
+  // wave's four leaves of node l / 4 of the chunk, so one read brings in all
+  // its leaf records.  The points of the first kGatherHold hot leaves stay in
+  // registers, the others are read again for writing; the workgroup takes one
+  // range of the list per chunk (one global atomic).
+  static_assert(kGatherNodes * kLeavesPerWave == 64, "one leaf record per lane");
   __shared__ uint32_t s_cnt, s_base;
   for (uint32_t c0 = blockIdx.x; c0 < c.nl1; c0 += kGatherNodes * gridDim.x) {
+    const uint32_t gq = c0 + (lane / kLeavesPerWave) * gridDim.x;
+    const uint32_t lf = gq * kFan + wave * kLeavesPerWave + lane % kLeavesPerWave;
+    bool hot = false;
+    uint32_t lst = 0, lcnt = 0, lcell = 0;
+    if (gq < c.nl1 && lf < c.nleaves) {
+      hot = gptr(c.leaf_key)[lf] >= bkey;
+      lst = __float_as_uint(gptr(c.leaf_lo)[lf].w);
+      lcnt = __float_as_uint(gptr(c.leaf_hi)[lf].w);
+      lcell = gptr(c.leaf_cell)[lf];
+    }
     if (tid == 0) s_cnt = 0;
-    __syncthreads();
-    uint64_t lmask = 0;  // bit kLeavesPerWave * jn + k: leaf k of node jn has keys >= bkey
-    uint32_t mine = 0;
-    for (uint32_t jn = 0; jn < kGatherNodes; ++jn) {
-      const uint32_t g = c0 + jn * gridDim.x;
-      if (g >= c.nl1) break;
-      if (gptr(c.l1_key)[g] < bkey) continue;
+    uint64_t rest = __ballot(hot);
+    float4 hp[kGatherHold];
+    uint2 hr[kGatherHold];
+    uint32_t hcell[kGatherHold], hn[kGatherHold];
+    uint64_t htk[kGatherHold];
 #pragma unroll
-      for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-        const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
-        if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < bkey) continue;
-        const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-        const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
-        bool take = false;
+    for (uint32_t u = 0; u < kGatherHold; ++u) {
+      hp[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      hr[u] = make_uint2(0u, 0u);
+      hcell[u] = 0;
+      hn[u] = 0;  // points of the held leaf (none: no leaf)
+      if (rest) {
+        const uint32_t j = (uint32_t)__builtin_ctzll(rest);
+        rest &= rest - 1;
+        const uint32_t st = rdlane(lst, j), cnt = rdlane(lcnt, j);
+        hcell[u] = rdlane(lcell, j);
+        hn[u] = cnt;
         if (lane < cnt) {
-          const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
-          take = (((uint64_t)__float_as_uint(d) << 32) | ~gptr(c.RO)[st + lane].x) >= bkey;
-        }
-        const uint64_t m = __ballot(take);
-        if (m) {
-          lmask |= 1ull << (kLeavesPerWave * jn + k);
-          mine += (uint32_t)__popcll(m);
+          hp[u] = gptr(c.P4)[st + lane];
+          hr[u] = gptr(c.RO)[st + lane];
         }
       }
     }
+    uint32_t mine = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kGatherHold; ++u) {
+      htk[u] = __ballot(lane < hn[u] &&
+                        (((uint64_t)__float_as_uint(hp[u].w) << 32) | ~hr[u].x) >= bkey);
+      mine += (uint32_t)__popcll(htk[u]);
+    }
+    const uint64_t later = rest;  // hot leaves beyond the first kGatherHold: counted now,
+    while (rest) {                // read again to be written
+      const uint32_t j = (uint32_t)__builtin_ctzll(rest);
+      rest &= rest - 1;
+      const uint32_t st = rdlane(lst, j), cnt = rdlane(lcnt, j);
+      bool take = false;
+      if (lane < cnt) {
+        const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
+        take = (((uint64_t)__float_as_uint(d) << 32) | ~gptr(c.RO)[st + lane].x) >= bkey;
+      }
+      mine += (uint32_t)__popcll(__ballot(take));
+    }
+    __syncthreads();  // s_cnt is zero
     uint32_t base = 0;
     if (lane == 0 && mine) base = atomicAdd(&s_cnt, mine);
     __syncthreads();
     if (tid == 0) s_base = s_cnt ? atomicAdd(&rs.nlist, s_cnt) : 0u;
     __syncthreads();
     base = s_base + rdlane(base, 0);
-    while (lmask) {
-      const uint32_t j = (uint32_t)__builtin_ctzll(lmask);
-      lmask &= lmask - 1;
-      const uint32_t g = c0 + (j / kLeavesPerWave) * gridDim.x;
-      const uint32_t leaf = g * kFan + wave * kLeavesPerWave + j % kLeavesPerWave;
-      const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-      const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
-      const uint32_t cell = gptr(c.leaf_cell)[leaf];
-      float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
-      uint2 ro = make_uint2(0u, 0u);
-      if (lane < cnt) {
-        p = gptr(c.P4)[st + lane];
-        ro = gptr(c.RO)[st + lane];
-      }
-      const bool take =
-          lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
-      const uint64_t m = __ballot(take);
-      if (take) {
+    const auto put = [&](const float4 &p, const uint2 &ro, uint32_t cell, uint64_t m) {
+      if ((m >> lane) & 1u) {
         const uint32_t i = base + lanes_below(m);
         if (i < kListCap) {
           gptr(c.list_p)[i] = p;
@@ -495,7 +510,24 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
         }
       }
       base += (uint32_t)__popcll(m);
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < kGatherHold; ++u) put(hp[u], hr[u], hcell[u], htk[u]);
+    rest = later;
+    while (rest) {
+      const uint32_t j = (uint32_t)__builtin_ctzll(rest);
+      rest &= rest - 1;
+      const uint32_t st = rdlane(lst, j), cnt = rdlane(lcnt, j);
+      float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+      uint2 ro = make_uint2(0u, 0u);
+      if (lane < cnt) {
+        p = gptr(c.P4)[st + lane];
+        ro = gptr(c.RO)[st + lane];
+      }
+      const bool take = lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
+      put(p, ro, rdlane(lcell, j), __ballot(take));
     }
+    __syncthreads();  // s_base is read before the next chunk's claim
   }
 }
 
