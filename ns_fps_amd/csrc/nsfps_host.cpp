@@ -474,7 +474,15 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     bool all = true;
     uint64_t samples = 0, rounds = 0;
     for (auto &q : pr) {
-      if (q.rs.err) return fail(NSFPS_EDEVICE, "internal: speculative list overflow");
+      if (q.rs.err) {
+        // 1: list overflow, 2: hot-copy overflow, 3: a live key above the hot
+        // histogram, 4: no crossing bin in a hot-threshold histogram
+        static const char *const what[] = {"", "list overflow", "hot-copy overflow",
+                                           "key above the hot histogram",
+                                           "no crossing bin in the hot histogram"};
+        return fail(NSFPS_EDEVICE, "internal: speculative run state: %s",
+                    q.rs.err < 5 ? what[q.rs.err] : "unknown");
+      }
       all = all && q.done;
       samples += q.iter;
       if (q.rs.forced) passes = kRefinePasses;

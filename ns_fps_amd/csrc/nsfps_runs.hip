@@ -644,23 +644,25 @@ __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   return v;
 }
 
-// Per-wave maximum and count of the live keys (>= bkey) among this thread's
-// entries, stored by lane 0 for the next hot set.
-__device__ __forceinline__ void publish_live(const float *d, const uint32_t *lo, uint64_t bkey,
-                                             uint64_t *s_wk, uint32_t *s_wn) {
-  uint64_t kmx = 0;
-  uint32_t nl = 0;
+// Bin shift of a hot-threshold histogram whose kSelBins bins end at kref and
+// cover every key down to bkey.
+__device__ __forceinline__ uint32_t sel_shift(uint64_t kref, uint64_t bkey) {
+  const uint32_t n = bit_length(kref - bkey);
+  return n > 8u ? n - 8u : 0u;
+}
+
+// Counts this thread's live keys (>= bkey) into histogram H (window kref, S);
+// every live key is <= kref.
+__device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, uint64_t bkey,
+                                          uint64_t kref, uint32_t S, uint32_t *H,
+                                          NSFPS_GLOBAL uint32_t *err) {
 #pragma unroll
   for (uint32_t s = 0; s < kOwnSlots; ++s) {
     const uint64_t key = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
-    const bool live = lo[s] != 0u && key >= bkey;
-    kmx = live && key > kmx ? key : kmx;
-    nl += (uint32_t)__popcll(__ballot(live));
-  }
-  kmx = wave_max_u64(kmx);
-  if (lane_id() == 0) {
-    s_wk[threadIdx.x >> 6] = kmx;
-    s_wn[threadIdx.x >> 6] = nl;
+    if (lo[s] != 0u && key >= bkey) {
+      if (key <= kref) atomicAdd(&H[(uint32_t)((kref - key) >> S)], 1u);
+      else *err = 3;  // cannot happen (kref bounds every live key)
+    }
   }
 }
 
@@ -677,13 +679,13 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
                                         //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
-  __shared__ uint4 s_rp[kHot];          // samples of a hot run in order: {x, y, z, row}
+  __shared__ uint4 s_rp[kHot];          // accepted hot copies at their slot: {x, y, z, row}
   __shared__ uint4 s_rc[kHot];          //   {cube lo, cube hi (clipped), cell, half-widths}
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
   __shared__ uint32_t s_big[2];                         // samples with large cubes
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
   __shared__ uint32_t s_nhot;
-  __shared__ uint64_t s_wk[kRunWaves];
+  __shared__ unsigned long long s_kmr;   // largest key of a hot copy left unaccepted
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
   __shared__ uint32_t s_wr[2][kRunWaves][2];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
@@ -714,7 +716,13 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   }
   const uint32_t ncx = ((b0 - 1) >> sx) + 1, ncy = ((b1 - 1) >> sy) + 1;
   for (uint32_t j = tid; j < kCells + 4; j += kRunThreads) s_cell[j] = 0;
+  if (tid < kSelBins) {
+    s_sel[0][tid] = 0;
+    s_sel[1][tid] = 0;
+  }
+  if (tid < kHot) s_hq[0][tid] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
   if (tid == 0) {
+    s_nhot = 0;
     s_geo[0] = sx | (sy << 8) | (sz << 16);
     s_geo[1] = ncx;
     s_geo[2] = ncy;
@@ -803,27 +811,20 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   NSFPS_GLOBAL int32_t *const out = gptr(c.out);
   NSFPS_GLOBAL float4 *const pick_p = gptr(c.pick_p);
   NSFPS_GLOBAL uint2 *const pick_c = gptr(c.pick_c);
+  NSFPS_GLOBAL uint32_t *const err = &rs.err;
   uint32_t np = 0;
   bool done = false;
-  publish_live(d, lo, bkey, s_wk, s_wn);
-  if (tid < kSelBins) s_sel[0][tid] = 0;
-  if (tid == 0) s_nhot = 0;
+  // The first hot set's histogram: every key is <= kref0 (keys only decrease).
+  // Later ones are counted right after each hot set's walk.
+  uint64_t kref = rs.kref0 > bkey ? rs.kref0 : bkey;
+  uint32_t S = sel_shift(kref, bkey);
+  hist_live(d, lo, bkey, kref, S, s_sel[0], err);
   __syncthreads();
   // coarse grid, kept in vector registers (the scalar file is full in the walk)
   const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
   const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
   NSFPS_RMARK(kRpLoad);
   while (true) {
-    // ---- hot threshold: live entries (key >= B); their maximum and count
-    // were published at the end of the previous hot set (or after the load)
-    uint64_t kmax = 0;
-    uint32_t nlive = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < kRunWaves; ++w) {
-      kmax = s_wk[w] > kmax ? s_wk[w] : kmax;
-      nlive += s_wn[w];
-    }
-    if (nlive == 0) break;  // every key is below B: the run ends
     uint64_t key[kOwnSlots];
     bool live[kOwnSlots];
 #pragma unroll
@@ -831,32 +832,27 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       key[s] = ((uint64_t)__float_as_uint(d[s]) << 32) | lo[s];
       live[s] = lo[s] != 0u && key[s] >= bkey;
     }
+    // ---- hot threshold.  Histogram 0 (window kref, S) holds every live key;
+    // windows of kSelBins bins are refined 8 bits at a time; buffer i % 3 of
+    // step i was zeroed a step (or a hot set) before, and every wave scans it
+    // itself: one barrier per refinement step.
     uint64_t hth = bkey;
-    if (nlive > kHot) {
-      // histogram windows of kSelBins bins below kref, refined 8 bits at a
-      // time; buffer i % 3 of step i was zeroed a step (or a hot set) before,
-      // and every wave scans it itself: one barrier per step
-      uint64_t kref = kmax;
-      uint32_t cap = kHot;
-      uint32_t S = bit_length(kmax - bkey);
-      S = S > 8u ? S - 8u : 0u;
+    uint32_t nlive = 0;
+    {
+      uint64_t wref = kref;
+      uint32_t wS = S, cap = kHot;
       for (uint32_t step = 0;; ++step) {
-        uint32_t *H = s_sel[step % 3];
-#pragma unroll
-        for (uint32_t s = 0; s < kOwnSlots; ++s) {
-          if (live[s] && key[s] <= kref) {
-            const uint64_t bb = (kref - key[s]) >> S;
-            if (bb < kSelBins) atomicAdd(&H[(uint32_t)bb], 1u);
-          }
-        }
-        if (tid < kSelBins) s_sel[(step + 1) % 3][tid] = 0;
-        __syncthreads();
-        const uint4 hv = reinterpret_cast<const uint4 *>(H)[lane];
+        const uint4 hv = reinterpret_cast<const uint4 *>(s_sel[step % 3])[lane];
         const uint32_t tot = hv.x + hv.y + hv.z + hv.w;
         const uint32_t incl = wave_incl_scan(tot);
+        if (step == 0) {
+          nlive = rdlane(incl, 63);
+          if (nlive <= kHot) break;  // every live entry is hot (or none is left)
+        }
         const uint64_t over = __ballot(incl > cap);  // running totals only grow
-        if (!over) {  // cannot happen (every window holds more than cap keys):
-          hth = kmax;  // then take the maximum alone
+        if (!over) {  // cannot happen (a refined window holds more than cap keys)
+          *err = 4;
+          nlive = 0;
           break;
         }
         const uint32_t c0 = incl - tot, c1 = c0 + hv.x, c2 = c1 + hv.y, c3 = c2 + hv.z;
@@ -864,67 +860,80 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         const uint32_t bf = c1 > cap ? c0 : c2 > cap ? c1 : c3 > cap ? c2 : c3;
         const uint32_t L = (uint32_t)__builtin_ctzll(over);
         const uint32_t bs = 4 * L + rdlane(jj, L), before = rdlane(bf, L);
-        if (before >= cap / 2 || S == 0) {
-          hth = kref - ((uint64_t)bs << S) + 1;
+        if (before >= cap / 2 || wS == 0) {
+          hth = wref - ((uint64_t)bs << wS) + 1;
           break;
         }
-        kref -= (uint64_t)bs << S;
+        wref -= (uint64_t)bs << wS;
         cap -= before;
-        S = S >= 8u ? S - 8u : 0u;
+        wS = wS >= 8u ? wS - 8u : 0u;
+        uint32_t *H = s_sel[(step + 1) % 3];
+#pragma unroll
+        for (uint32_t s = 0; s < kOwnSlots; ++s) {
+          if (live[s] && key[s] <= wref) {
+            const uint64_t bb = (wref - key[s]) >> wS;
+            if (bb < kSelBins) atomicAdd(&H[(uint32_t)bb], 1u);
+          }
+        }
+        if (tid < kSelBins) s_sel[(step + 2) % 3][tid] = 0;
+        __syncthreads();
       }
       hth = hth > bkey ? hth : bkey;
     }
+    if (nlive == 0) break;  // every key is below B: the run ends
     NSFPS_RMARK(kRpSelect);
-    // ---- hot copies -> LDS, placed by an LDS counter; their cube corners
-    // follow, one copy per thread
-    uint32_t nhot;
+    // ---- hot copies -> LDS, placed by an LDS counter, each with its cube
+    // computed by the thread that holds it; unused slots were cleared during
+    // the previous hot set's walk (key 0)
     {
+      uint64_t bal[kOwnSlots];
+      uint32_t tot = 0;
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        const bool hot = live[s] && key[s] >= hth;
-        const uint64_t bal = __ballot(hot);
-        if (bal) {
-          uint32_t base = 0;
-          if (lane == 0) base = atomicAdd(&s_nhot, (uint32_t)__popcll(bal));
-          base = rdlane(base, 0);
-          if (hot) {
-            const uint32_t hi = base + lanes_below(bal);
-            if (hi < kHot) {
-              s_hq[0][hot_slot(hi)] = make_uint4(0u, 0u, lo[s], __float_as_uint(d[s]));
-              s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), 0u);
-              s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
-                                    __float_as_uint(z[s]), row[s]);
-            } else {  // cannot happen (at most kHot keys are >= the hot threshold)
-              rs.err = 2;
-            }
+        bal[s] = __ballot(live[s] && key[s] >= hth);
+        tot += (uint32_t)__popcll(bal[s]);
+      }
+      uint32_t base = 0;
+      if (lane == 0 && tot) base = atomicAdd(&s_nhot, tot);
+      base = rdlane(base, 0);
+#pragma unroll
+      for (uint32_t s = 0; s < kOwnSlots; ++s) {
+        if ((bal[s] >> lane) & 1u) {
+          const uint32_t hi = base + lanes_below(bal[s]);
+          if (hi < kHot) {
+            const uint32_t h = packed_halves(c.r, d[s]);
+            uint32_t lo_c, hi_c;
+            cube_corners(cc[s], h, b0, b1, b2, lo_c, hi_c);
+            s_hq[0][hot_slot(hi)] =
+                make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, lo[s], __float_as_uint(d[s]));
+            s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), h);
+            s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
+                                  __float_as_uint(z[s]), row[s]);
+          } else {  // cannot happen (at most kHot keys are >= the hot threshold)
+            *err = 2;
           }
         }
+        base += (uint32_t)__popcll(bal[s]);
       }
       if (tid < 2) s_big[tid] = 0;
-      if (tid == 0) s_lowm[0] = 0;
-      __syncthreads();
-      nhot = min(s_nhot, kHot);
-      if (tid < nhot) {
-        const uint4 hq0 = s_hq[0][hot_slot(tid)];
-        const uint32_t cl = s_hx[tid].x;
-        const uint32_t h = packed_halves(c.r, __uint_as_float(hq0.w));
-        uint32_t lo_c, hi_c;
-        cube_corners(cl, h, b0, b1, b2, lo_c, hi_c);
-        s_hq[0][hot_slot(tid)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hq0.z, hq0.w);
-        s_hx[tid].w = h;
-      } else if (tid < kHot) {
-        s_hq[0][hot_slot(tid)] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
+      if (tid == 0) {
+        s_lowm[0] = 0;
+        s_kmr = 0;
       }
       __syncthreads();
     }
     NSFPS_RMARK(kRpGather);
     // ---- phases: thread (j, q) works for hot copy j against copies
-    // kCmp q .. kCmp q + kCmp - 1
+    // kCmp q .. kCmp q + kCmp - 1.  A copy's group keeps what the walk needs
+    // once the copy is accepted: its sample index and cube.
     const uint32_t hj = tid / kCopyLanes, hq = tid % kCopyLanes;
     const uint32_t room = m - it;  // samples left (>= 1)
     // Per phase, two barriers: after the ranks (the accepted prefix is known),
     // and after the next buffer of hot copies is written.
     uint32_t npk = 0, stop = 0, ph = 0;
+    bool my_acc = false;
+    uint64_t my_key = 0;  // the copy's key at the last phase (0: none, or accepted)
+    uint32_t my_out = 0, my_lo = 0, my_hi = 0, my_qc = 0, my_hh = 0;
     while (true) {
       const uint4 me = s_hq[ph][hot_slot(hj)];
       const uint4 mx = s_hx[hj];
@@ -934,6 +943,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       for (uint32_t u = 0; u < kCmp; ++u) og[u] = s_hq[ph][kCopyLanes * u + hq];  // copy kCmp hq + u
       __builtin_amdgcn_sched_barrier(0);
       const uint64_t mkey = ((uint64_t)me.w << 32) | me.z;
+      my_key = mkey;
       const bool remj = mkey != 0;  // copies taken earlier, and unused slots, have key 0
       // bit u of cand: copy kCmp q + u is remaining, ranked above j, and its cube holds j
       uint32_t cnt = 0, cand = 0;
@@ -989,11 +999,13 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       }
       // the prefix: samples npk .. npk + P - 1 in rank order
       const bool acc = remj && rank < P;
-      if (acc && hq == 0) {
-        uint32_t lo_c, hi_c;
-        cube_corners(mx.x, mx.w, b0, b1, b2, lo_c, hi_c);
-        s_rp[npk + rank] = s_hp[hj];
-        s_rc[npk + rank] = make_uint4(lo_c, hi_c, mx.x, mx.w);
+      if (acc) {
+        my_acc = true;
+        my_key = 0;
+        my_out = npk + rank;
+        my_qc = mx.x;
+        my_hh = mx.w;
+        cube_corners(mx.x, mx.w, b0, b1, b2, my_lo, my_hi);
       }
       npk += P;
       if (npk >= room) {  // the last sample needs no update
@@ -1059,24 +1071,30 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       NSFPS_RMARK(kRpPhases);
       if (PROF) pf[kRpPhaseCount] += 1;
     }
-    __syncthreads();  // the loop can leave right after the last records were written
     NSFPS_RMARK(kRpPhases);
     // ---- the hot run's samples -> global memory and every list entry.
-    // Lane group k takes sample k and walks the coarse rows its cube spans,
+    // The group of an accepted copy walks the coarse rows its cube spans,
     // min-ing distances into LDS.  A cube over more than kWalkRows rows, or a
     // lane meeting more than kWalkLaneEntries entries in its rows, flags the
     // sample instead; flagged samples are applied below by every thread to its
-    // own entries (applying a sample twice changes nothing).
+    // own entries (applying a sample twice changes nothing).  Meanwhile the
+    // next hot set's copy buffer and first histogram are cleared, and the
+    // largest key of a copy left unaccepted bounds the next histogram.
     {
-      const uint32_t k = tid / kCopyLanes, q = tid % kCopyLanes;
-      if (k < npk) {
-        const uint4 rp = s_rp[k], rc = s_rc[k];
-        const uint32_t lo_c = rc.x, hi_c = rc.y, qc = rc.z, hh = rc.w;
+      const uint32_t q = hq;
+      if (tid < kHot) s_hq[0][tid] = make_uint4(0u, 0u, 0u, 0u);
+      if (tid < kSelBins) s_sel[0][tid] = 0;
+      if (q == 0 && my_key != 0) atomicMax(&s_kmr, (unsigned long long)my_key);
+      if (my_acc) {
+        const uint4 rp = s_hp[hj];
+        const uint32_t lo_c = my_lo, hi_c = my_hi, qc = my_qc, hh = my_hh;
         if (q == 0) {
-          out[it + k] = (int32_t)rp.w;
-          pick_p[np + k] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
-                                       __uint_as_float(rp.z), 0.f);
-          pick_c[np + k] = make_uint2(lo_c, hi_c);
+          out[it + my_out] = (int32_t)rp.w;
+          pick_p[np + my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
+                                            __uint_as_float(rp.z), 0.f);
+          pick_c[np + my_out] = make_uint2(lo_c, hi_c);
+          s_rp[hj] = rp;
+          s_rc[hj] = make_uint4(lo_c, hi_c, qc, hh);
         }
         const uint32_t x0 = (lo_c & 1023u) >> gsx, x1 = (hi_c & 1023u) >> gsx;
         const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
@@ -1111,7 +1129,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
             }
           }
         }
-        if (big) atomicOr(&s_big[k >> 5], 1u << (k & 31u));
+        if (big) atomicOr(&s_big[hj >> 5], 1u << (hj & 31u));
       }
       NSFPS_RMARK(kRpWalk);
       __syncthreads();  // the walks' updates are in LDS
@@ -1143,20 +1161,25 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     it += npk;
     np += npk;
-    // the next hot set's live maximum and count, and its zeroed histogram and
-    // copy counter
-    NSFPS_RMARK(kRpApply);
-    publish_live(d, lo, bkey, s_wk, s_wn);
-    if (tid < kSelBins) s_sel[0][tid] = 0;
-    if (tid == 0) s_nhot = 0;
-    __syncthreads();  // s_hq / s_hp / s_rp / s_rc are rewritten by the next hot set
-    NSFPS_RMARK(kRpPublish);
     if (PROF) pf[kRpHotRounds] += 1;
     if (stop == 2) {
       done = true;
       break;
     }
     if (hth == bkey && stop == 1) break;  // every live entry was hot: all below B now
+    // ---- the next hot set's first histogram.  Live keys are below the hot
+    // threshold, or belong to a copy left unaccepted (at most its last key).
+    {
+      const uint64_t kmr = s_kmr;
+      kref = hth > bkey ? hth - 1 : bkey;
+      kref = kmr > kref ? kmr : kref;
+      S = sel_shift(kref, bkey);
+      hist_live(d, lo, bkey, kref, S, s_sel[0], err);
+      if (tid < kSelBins) s_sel[1][tid] = 0;
+      if (tid == 0) s_nhot = 0;
+      __syncthreads();
+    }
+    NSFPS_RMARK(kRpPublish);
   }
   if (tid == 0) {
     *gptr(c.iter) = it;
