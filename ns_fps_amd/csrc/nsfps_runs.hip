@@ -896,24 +896,35 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       uint32_t base = 0;
       if (lane == 0 && tot) base = atomicAdd(&s_nhot, tot);
       base = rdlane(base, 0);
+      // a thread rarely holds two hot entries: one pass over the cube code
+      // per hot entry of the thread, selected from its slots
+      static_assert(kOwnSlots == 2, "the hot-entry pass selects between two slots");
+      uint32_t pend = 0, slot[kOwnSlots];
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        if ((bal[s] >> lane) & 1u) {
-          const uint32_t hi = base + lanes_below(bal[s]);
-          if (hi < kHot) {
-            const uint32_t h = packed_halves(c.r, d[s]);
-            uint32_t lo_c, hi_c;
-            cube_corners(cc[s], h, b0, b1, b2, lo_c, hi_c);
-            s_hq[0][hot_slot(hi)] =
-                make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, lo[s], __float_as_uint(d[s]));
-            s_hx[hi] = make_uint4(cc[s], pack11(cc[s]) | kGuards, pack11(cc[s]), h);
-            s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
-                                  __float_as_uint(z[s]), row[s]);
-          } else {  // cannot happen (at most kHot keys are >= the hot threshold)
-            *err = 2;
-          }
-        }
+        pend |= (uint32_t)((bal[s] >> lane) & 1u) << s;
+        slot[s] = base + lanes_below(bal[s]);
         base += (uint32_t)__popcll(bal[s]);
+      }
+      while (pend) {
+        const uint32_t s = (uint32_t)__builtin_ctz(pend);
+        pend &= pend - 1;
+        const bool s1 = s != 0;
+        const uint32_t hi = s1 ? slot[1] : slot[0];
+        const float ds = s1 ? d[1] : d[0];
+        const uint32_t cs = s1 ? cc[1] : cc[0];
+        if (hi < kHot) {
+          const uint32_t h = packed_halves(c.r, ds);
+          uint32_t lo_c, hi_c;
+          cube_corners(cs, h, b0, b1, b2, lo_c, hi_c);
+          s_hq[0][hot_slot(hi)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards,
+                                             s1 ? lo[1] : lo[0], __float_as_uint(ds));
+          s_hx[hi] = make_uint4(cs, pack11(cs) | kGuards, pack11(cs), h);
+          s_hp[hi] = make_uint4(__float_as_uint(s1 ? x[1] : x[0]), __float_as_uint(s1 ? y[1] : y[0]),
+                                __float_as_uint(s1 ? z[1] : z[0]), s1 ? row[1] : row[0]);
+        } else {  // cannot happen (at most kHot keys are >= the hot threshold)
+          *err = 2;
+        }
       }
       if (tid < 2) s_big[tid] = 0;
       if (tid == 0) {
@@ -933,7 +944,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     uint32_t npk = 0, stop = 0, ph = 0;
     bool my_acc = false;
     uint64_t my_key = 0;  // the copy's key at the last phase (0: none, or accepted)
-    uint32_t my_out = 0, my_lo = 0, my_hi = 0, my_qc = 0, my_hh = 0;
+    uint32_t my_out = 0, my_qc = 0, my_hh = 0;
     while (true) {
       const uint4 me = s_hq[ph][hot_slot(hj)];
       const uint4 mx = s_hx[hj];
@@ -1005,7 +1016,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         my_out = npk + rank;
         my_qc = mx.x;
         my_hh = mx.w;
-        cube_corners(mx.x, mx.w, b0, b1, b2, my_lo, my_hi);
       }
       npk += P;
       if (npk >= room) {  // the last sample needs no update
@@ -1087,7 +1097,9 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       if (q == 0 && my_key != 0) atomicMax(&s_kmr, (unsigned long long)my_key);
       if (my_acc) {
         const uint4 rp = s_hp[hj];
-        const uint32_t lo_c = my_lo, hi_c = my_hi, qc = my_qc, hh = my_hh;
+        const uint32_t qc = my_qc, hh = my_hh;
+        uint32_t lo_c, hi_c;
+        cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
         if (q == 0) {
           out[it + my_out] = (int32_t)rp.w;
           pick_p[np + my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
