@@ -185,7 +185,7 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // issued together: the wave's leaf records with the run state and the node's
 // record, a pick's cube with its position, and the points of every leaf of
 // the wave that needs reading.
-__global__ __launch_bounds__(kPassThreads) __attribute__((amdgpu_num_sgpr(60))) void k_update(
+__global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ float4 s_pp[kListCap];
@@ -1129,15 +1129,22 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
               break;
             }
             budget -= e1 - e0;
-            for (uint32_t e = e0; e < e1; ++e) {
-              // one 16-byte read: the min is unconditional (a no-op outside the
-              // cube), so the cell is not read ahead of the coordinates
-              const uint4 p = s_pc[e];
-              const uint32_t dd =
-                  __float_as_uint(sqdist(__uint_as_float(p.x), __uint_as_float(p.y),
-                                         __uint_as_float(p.z), px, py, pz));
+            // two entries per step, their reads in flight together (an odd
+            // last entry is taken twice: min is idempotent); one 16-byte read
+            // each, and the min is unconditional (a no-op outside the cube),
+            // so the cell is not read ahead of the coordinates
+            for (uint32_t e = e0; e < e1; e += 2) {
+              const uint32_t eb = e + 1 < e1 ? e + 1 : e;
+              const uint4 pa = s_pc[e], pb = s_pc[eb];
+              const uint32_t da =
+                  __float_as_uint(sqdist(__uint_as_float(pa.x), __uint_as_float(pa.y),
+                                         __uint_as_float(pa.z), px, py, pz));
+              const uint32_t db =
+                  __float_as_uint(sqdist(__uint_as_float(pb.x), __uint_as_float(pb.y),
+                                         __uint_as_float(pb.z), px, py, pz));
               // non-negative floats order like their bits
-              atomicMin(&s_dd[e], in_cube_h(p.w, qc, hh) ? dd : 0xffffffffu);
+              atomicMin(&s_dd[e], in_cube_h(pa.w, qc, hh) ? da : 0xffffffffu);
+              atomicMin(&s_dd[eb], in_cube_h(pb.w, qc, hh) ? db : 0xffffffffu);
             }
           }
         }
