@@ -566,7 +566,8 @@ constexpr uint32_t kWalkRows = 64;        // cubes over more coarse rows, or wit
 constexpr uint32_t kWalkLaneEntries = 16;  // list entries in one lane's rows, are
                                           // applied by every thread
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
-static_assert((kCopyLanes == 4 || kCopyLanes == 8) && kHot == 64, "the run kernel layout");
+static_assert((kCopyLanes == 4 || kCopyLanes == 8 || kCopyLanes == 16) && kHot == 64,
+              "the run kernel layout");
 static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
@@ -634,13 +635,15 @@ __device__ __forceinline__ uint32_t hot_slot(uint32_t i) {
 __device__ __forceinline__ uint32_t group_sum(uint32_t v) {
   v += dpp_mov<kDppQuad1032>(v);
   v += dpp_mov<kDppQuad2301>(v);
-  if (kCopyLanes == 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
+  if (kCopyLanes >= 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
+  if (kCopyLanes >= 16) v += dpp_mov<kDppMirror>(v);     // lane i and 15 - i: the other half
   return v;
 }
 __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   v = min(v, dpp_mov<kDppQuad1032>(v));
   v = min(v, dpp_mov<kDppQuad2301>(v));
-  if (kCopyLanes == 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
+  if (kCopyLanes >= 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
+  if (kCopyLanes >= 16) v = min(v, dpp_mov<kDppMirror>(v));
   return v;
 }
 
@@ -898,7 +901,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       base = rdlane(base, 0);
       // a thread rarely holds two hot entries: one pass over the cube code
       // per hot entry of the thread, selected from its slots
-      static_assert(kOwnSlots == 2, "the hot-entry pass selects between two slots");
       uint32_t pend = 0, slot[kOwnSlots];
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
@@ -909,19 +911,29 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       while (pend) {
         const uint32_t s = (uint32_t)__builtin_ctz(pend);
         pend &= pend - 1;
-        const bool s1 = s != 0;
-        const uint32_t hi = s1 ? slot[1] : slot[0];
-        const float ds = s1 ? d[1] : d[0];
-        const uint32_t cs = s1 ? cc[1] : cc[0];
+        uint32_t hi = slot[0], cs = cc[0], ls = lo[0], rs_ = row[0];
+        float ds = d[0], xs = x[0], ys = y[0], zs = z[0];
+#pragma unroll
+        for (uint32_t t = 1; t < kOwnSlots; ++t) {
+          if (s == t) {
+            hi = slot[t];
+            cs = cc[t];
+            ls = lo[t];
+            rs_ = row[t];
+            ds = d[t];
+            xs = x[t];
+            ys = y[t];
+            zs = z[t];
+          }
+        }
         if (hi < kHot) {
           const uint32_t h = packed_halves(c.r, ds);
           uint32_t lo_c, hi_c;
           cube_corners(cs, h, b0, b1, b2, lo_c, hi_c);
-          s_hq[0][hot_slot(hi)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards,
-                                             s1 ? lo[1] : lo[0], __float_as_uint(ds));
+          s_hq[0][hot_slot(hi)] =
+              make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, ls, __float_as_uint(ds));
           s_hx[hi] = make_uint4(cs, pack11(cs) | kGuards, pack11(cs), h);
-          s_hp[hi] = make_uint4(__float_as_uint(s1 ? x[1] : x[0]), __float_as_uint(s1 ? y[1] : y[0]),
-                                __float_as_uint(s1 ? z[1] : z[0]), s1 ? row[1] : row[0]);
+          s_hp[hi] = make_uint4(__float_as_uint(xs), __float_as_uint(ys), __float_as_uint(zs), rs_);
         } else {  // cannot happen (at most kHot keys are >= the hot threshold)
           *err = 2;
         }
