@@ -144,17 +144,36 @@ def cpu_baseline(w, budget_s=30.0):
             "ms_per_call": round(el * 1e3, 2),
             "sample": f"one full call on cloud 0 of {w['name']} ({len(P)} points -> {m} samples), "
                       f"single thread, {os.path.basename(getattr(runner, 'path', 'liboracle.so'))}"}
+    o = Oracle()
+    # our C restatement on the same call, one core, against the reference
+    if kind == "reference":
+        try:
+            t = time.perf_counter()
+            o.fps(P, m, w["range"], w["blocks"])
+            el_port = time.perf_counter() - t
+            base["port_ms_per_call"] = round(el_port * 1e3, 2)
+            base["port_over_reference"] = round(el_port / el, 3)
+        except Exception as e:  # informational only
+            base["port_error"] = str(e)
     # naive O(N*M) FPS, first iterations extrapolated linearly (cost per
-    # iteration is constant)
+    # iteration is constant): one thread, then every core of the host
     try:
-        o = Oracle()
         k = max(16, min(m - 1, int(2e8 // max(len(P), 1))))
         t = time.perf_counter()
         o.fps_naive(P, m, tie="index", max_iters=k)
         el = time.perf_counter() - t
         base["naive_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
         base["naive_sample"] = f"first {k} of {m - 1} iterations, single thread, extrapolated"
-    except Exception as e:  # the naive timing is informational only
+        nt = o.max_threads()
+        k = max(16, min(m - 1, int(2e8 * nt // max(len(P), 1))))
+        t = time.perf_counter()
+        o.fps_naive_mt(P, m, max_iters=k, threads=nt)
+        el = time.perf_counter() - t
+        base["naive_mt_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
+        base["naive_mt_threads"] = nt
+        base["naive_mt_sample"] = (f"first {k} of {m - 1} iterations, {nt} OpenMP threads, "
+                                   "extrapolated")
+    except Exception as e:  # the naive timings are informational only
         base["naive_error"] = str(e)
     return base
 

@@ -25,6 +25,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <omp.h>
 
 #define ORC_BOUNDARY_EPS 1e-6f /* src/yuezu_fps.h:43-45 */
 #define ORC_LEAF 16u           /* MORTON_BLOCK_SIZE, src/yuezu_fps.h:20-22 */
@@ -477,6 +478,59 @@ int orc_fps_naive(const float *xyz, uint64_t n, uint64_t m,
   }
   *out_len = len;
   free(scan);
+  free(C);
+  return 0;
+}
+
+int orc_max_threads(void) { return omp_get_max_threads(); }
+
+int orc_fps_naive_mt(const float *xyz, uint64_t n, uint64_t m, int32_t *out,
+                     uint64_t *out_len, uint64_t max_iters, int threads) {
+  *out_len = 0;
+  if (n == 0 || m == 0) return 0;
+  if (n > 0x7fffffffull) return -2;
+  if (m >= n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = (int32_t)i;
+    *out_len = n;
+    return 0;
+  }
+  float *C = (float *)malloc(sizeof(float) * n);
+  if (!C) return -3;
+  const int nt = threads > 0 ? threads : omp_get_max_threads();
+  for (uint64_t i = 0; i < n; ++i) C[i] = FLT_MAX;
+  out[0] = 0;
+  uint64_t len = 1, last = 0;
+  for (uint64_t it = 1; it < m; ++it) {
+    if (max_iters && it > max_iters) break;
+    const float qx = xyz[3 * last], qy = xyz[3 * last + 1], qz = xyz[3 * last + 2];
+    float gbest = -1.0f;
+    int64_t gbi = 0;
+#pragma omp parallel num_threads(nt)
+    {
+      float best = -1.0f;
+      int64_t bi = 0;
+#pragma omp for schedule(static) nowait
+      for (int64_t j = 0; j < (int64_t)n; ++j) {
+        const float d = sqdist(xyz[3 * j], xyz[3 * j + 1], xyz[3 * j + 2], qx, qy, qz);
+        if (d < C[j]) C[j] = d;
+        if (C[j] > best) {
+          best = C[j];
+          bi = j;
+        }
+      }
+#pragma omp critical
+      {
+        if (best > gbest || (best == gbest && bi < gbi)) {
+          gbest = best;
+          gbi = bi;
+        }
+      }
+    }
+    if (gbest <= 0.0f) break;
+    out[len++] = (int32_t)gbi;
+    last = (uint64_t)gbi;
+  }
+  *out_len = len;
   free(C);
   return 0;
 }

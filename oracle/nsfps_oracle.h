@@ -77,6 +77,17 @@ int orc_fps_naive(const float *xyz, uint64_t n, uint64_t m,
                   const float *bounds6, const uint32_t *blocks3, int tie_mode,
                   int32_t *out, uint64_t *out_len, uint64_t max_iters);
 
+/* The naive FPS with ties to the lowest original index, each iteration's
+ * update and argmax split over `threads` OpenMP threads (0 = the OpenMP
+ * default): every thread scans a contiguous range in index order and the
+ * range maxima merge by (larger distance, then lower index), which is the
+ * leftmost maximum of the whole scan.  The all-cores CPU baseline. */
+int orc_fps_naive_mt(const float *xyz, uint64_t n, uint64_t m, int32_t *out,
+                     uint64_t *out_len, uint64_t max_iters, int threads);
+
+/* OpenMP threads orc_fps_naive_mt uses for threads = 0. */
+int orc_max_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

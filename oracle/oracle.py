@@ -152,6 +152,23 @@ class Oracle:
         return out[:ol.value].copy()
 
 
+    def fps_naive_mt(self, points, n_samples, max_iters=0, threads=0):
+        """Naive FPS, ties to the lowest index, over `threads` OpenMP threads
+        (0: the OpenMP default); the same indices as fps_naive(tie="index")."""
+        p = _pts(points)
+        out = np.zeros(max(int(n_samples), 1), np.int32)
+        ol = ctypes.c_uint64()
+        rc = self.lib.orc_fps_naive_mt(_ptr(p), _u64(len(p)), _u64(int(n_samples)), _ptr(out),
+                                       ctypes.byref(ol), _u64(int(max_iters)),
+                                       ctypes.c_int(int(threads)))
+        if rc:
+            raise ValueError(f"orc_fps_naive_mt failed ({rc})")
+        return out[:ol.value].copy()
+
+    def max_threads(self):
+        return int(self.lib.orc_max_threads())
+
+
 class Reference:
     """The reference library built from its own sources (oracle/_ref)."""
 

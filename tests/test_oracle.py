@@ -157,6 +157,31 @@ def test_tie_rule_is_discriminated_by_the_fixtures(oracle):
     assert np.array_equal(logical, lat.expected)
 
 
+@pytest.mark.parametrize("threads", [1, 3, 0])
+def test_threaded_naive_fps_equals_single_thread_and_numpy(oracle, threads):
+    """The all-cores CPU baseline: the same indices as the single-thread naive
+    FPS (ties to the lowest index) on tie-heavy clouds, and as a NumPy brute
+    force (float32, the distance's own operation order, np.argmax = first
+    maximum) on a small one."""
+    rs = np.random.RandomState(11)
+    lat = np.stack(np.meshgrid(*[np.arange(9, dtype=np.float32)] * 3, indexing="ij"),
+                   -1).reshape(-1, 3)
+    dup = rs.rand(3000, 3).astype(np.float32)
+    dup[::5] = dup[7]
+    for pts, m in [(lat, 300), (dup, 500)]:
+        want = oracle.fps_naive(pts, m, tie="index")
+        assert np.array_equal(oracle.fps_naive_mt(pts, m, threads=threads), want)
+    small = rs.randn(257, 3).astype(np.float32)
+    C = np.full(len(small), np.finfo(np.float32).max, np.float32)
+    idx, last = [0], 0
+    for _ in range(1, 60):
+        d = small - small[last]
+        C = np.minimum(C, (d[:, 0] * d[:, 0] + d[:, 1] * d[:, 1]) + d[:, 2] * d[:, 2])
+        last = int(np.argmax(C))
+        idx.append(last)
+    assert list(oracle.fps_naive_mt(small, 60, threads=threads)) == idx
+
+
 def test_fma_contraction_is_discriminated_when_reference_built():
     """The reference built with its own setup.py flags (FMA contraction) gives
     different indices on the LiDAR workload: the golden hash pins the
