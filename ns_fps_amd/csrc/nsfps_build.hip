@@ -200,25 +200,48 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
   }
 }
 
-// Secondary key per logical position: bucket, then the sub-cell code.
+// Sort key of the clouds of a call sorted together: cloud index above the
+// bucket (every cloud has n_per points, stored one cloud after another).
+__global__ void k_cloud_keys(const uint32_t *__restrict__ bucket, uint32_t total, uint32_t n_per,
+                             int bucket_bits, uint32_t *__restrict__ key) {
+  uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= total) return;
+  key[g] = bucket[g] | ((g / n_per) << bucket_bits);
+}
+
+// Secondary key per logical position: cloud (when clouds are sorted
+// together, position p belongs to cloud p / n_per), bucket, then the sub-cell
+// code.
 __global__ void k_key2(const uint32_t *__restrict__ lorig, const uint32_t *__restrict__ bucket,
-                       const uint32_t *__restrict__ fine, uint32_t n, int fine_shift,
-                       int fine_bits, uint32_t *__restrict__ key2) {
+                       const uint32_t *__restrict__ fine, uint32_t n, uint32_t n_per,
+                       int cloud_shift, int fine_shift, int fine_bits,
+                       uint32_t *__restrict__ key2) {
   uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= n) return;
   uint32_t o = lorig[p];
   uint32_t f = fine_bits > 0 ? (fine[o] >> fine_shift) : 0u;
-  key2[p] = (bucket[o] << fine_bits) | f;
+  key2[p] = ((p / n_per) << cloud_shift) | (bucket[o] << fine_bits) | f;
 }
 
-// Leaves per bucket, and the largest bucket population.
-__global__ void k_leaf_counts(const uint32_t *__restrict__ counts, uint32_t T,
-                              uint32_t *__restrict__ lc, uint32_t *__restrict__ maxocc) {
+// Leaves per bucket, the largest bucket population and the total of leaves.
+__global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict__ counts,
+                                                     uint32_t T, uint32_t *__restrict__ lc,
+                                                     uint32_t *__restrict__ maxocc,
+                                                     uint32_t *__restrict__ total) {
+  __shared__ uint32_t s_sum;
+  if (threadIdx.x == 0) s_sum = 0;
+  __syncthreads();
   uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= T) return;
-  uint32_t c = counts[b];
-  lc[b] = (c + kLeaf - 1) / kLeaf;
-  if (c) atomicMax(maxocc, c);
+  if (b < T) {
+    uint32_t c = counts[b];
+    lc[b] = (c + kLeaf - 1) / kLeaf;
+    if (c) {
+      atomicMax(maxocc, c);
+      atomicAdd(&s_sum, (c + kLeaf - 1) / kLeaf);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && s_sum) atomicAdd(total, s_sum);
 }
 
 __global__ void k_cell_info(const uint32_t *__restrict__ cell_start,
@@ -233,14 +256,18 @@ __global__ void k_cell_info(const uint32_t *__restrict__ cell_start,
 // (src/yuezu_fps.cpp:215-223).  Dense: slot = physical position p.  Padded:
 // slot = bucket * cap + (p - first position of the bucket).
 __global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__restrict__ lorig,
-                         const uint32_t *__restrict__ bucket, const uint32_t *__restrict__ cell_start,
+                         uint32_t base, const uint32_t *__restrict__ bucket,
+                         const uint32_t *__restrict__ cell_start,
                          const float *__restrict__ xyz, uint32_t n, uint32_t padded, uint32_t cap,
                          float4 *__restrict__ P4, uint2 *__restrict__ RO,
                          uint32_t *__restrict__ phys0) {
   uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= n) return;
-  uint32_t rk = prank[p];
-  uint32_t o = lorig[rk];
+  // ranks and rows come from sorts that may hold other clouds: this cloud's
+  // start in them is base
+  uint32_t rkg = prank[p];
+  uint32_t rk = rkg - base;
+  uint32_t o = lorig[rkg] - base;
   uint32_t slot = p;
   if (padded) {
     uint32_t b = bucket[o];
@@ -429,16 +456,23 @@ hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
   return hipGetLastError();
 }
 
+hipError_t launch_cloud_keys(const uint32_t *bucket, uint32_t total, uint32_t n_per,
+                             int bucket_bits, uint32_t *key, hipStream_t st) {
+  k_cloud_keys<<<cdiv(total, 256), 256, 0, st>>>(bucket, total, n_per, bucket_bits, key);
+  return hipGetLastError();
+}
+
 hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,
-                       uint32_t n, int fine_shift, int fine_bits, uint32_t *key2,
-                       hipStream_t st) {
-  k_key2<<<cdiv(n, 256), 256, 0, st>>>(lorig, bucket, fine, n, fine_shift, fine_bits, key2);
+                       uint32_t n, uint32_t n_per, int cloud_shift, int fine_shift, int fine_bits,
+                       uint32_t *key2, hipStream_t st) {
+  k_key2<<<cdiv(n, 256), 256, 0, st>>>(lorig, bucket, fine, n, n_per, cloud_shift, fine_shift,
+                                       fine_bits, key2);
   return hipGetLastError();
 }
 
 hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
-                              hipStream_t st) {
-  k_leaf_counts<<<cdiv(T, 256), 256, 0, st>>>(counts, T, lc, maxocc);
+                              uint32_t *total, hipStream_t st) {
+  k_leaf_counts<<<cdiv(T, 256), 256, 0, st>>>(counts, T, lc, maxocc, total);
   return hipGetLastError();
 }
 
@@ -448,12 +482,12 @@ hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_lea
   return hipGetLastError();
 }
 
-hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, const uint32_t *bucket,
-                         const uint32_t *cell_start, const float *xyz, uint32_t n,
-                         uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO, uint32_t *phys0,
-                         hipStream_t st) {
-  k_gather<<<cdiv(n, 256), 256, 0, st>>>(prank, lorig, bucket, cell_start, xyz, n, padded, cap, P4,
-                                         RO, phys0);
+hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
+                         const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
+                         uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
+                         uint32_t *phys0, hipStream_t st) {
+  k_gather<<<cdiv(n, 256), 256, 0, st>>>(prank, lorig, base, bucket, cell_start, xyz, n, padded,
+                                         cap, P4, RO, phys0);
   return hipGetLastError();
 }
 

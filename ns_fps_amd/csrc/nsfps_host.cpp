@@ -216,6 +216,13 @@ nsfps_status arena_reserve(Arena &a, size_t bytes) {
 
 // ------------------------------------------------------------ one cloud ----
 
+// Per-cloud words the host polls between batches of rounds, contiguous over
+// the clouds of a call so that one copy reads them all.
+struct CloudStatus {
+  uint32_t done, iter;
+  RunState rs;
+};
+
 struct CloudPlan {
   uint32_t n = 0, m = 0;
   HostRange rng;
@@ -228,10 +235,13 @@ struct CloudPlan {
   uint32_t *d_lut = nullptr, *d_counts = nullptr, *d_lc = nullptr;
   uint32_t *d_small = nullptr;  // [0] non-finite flag, [1] max occupancy, [2] phys0
   uint2 *d_cell_info = nullptr;
+  uint32_t *d_bucket = nullptr, *d_fine = nullptr;  // per point: bucket, sub-cell code
+  uint64_t cap = 0;                // slots per bucket in the padded layout
+  std::vector<uint32_t> lut_host;  // source of an asynchronous copy: lives until the sync
 };
 
 struct Scratch {
-  uint32_t *bucket, *fine, *kA, *kB, *vA, *vB, *vC, *hist, *scan;
+  uint32_t *kA, *kB, *vA, *vB, *vC, *hist, *scan;
 };
 
 int key_bits_for(uint32_t T) {
@@ -255,11 +265,9 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   p.leaves_ub = (uint32_t)leaves;
   p.l1_ub = (uint32_t)((leaves + kFan - 1) / kFan);
   CloudDev &c = p.dev;
-  if (p.h_xyz) p.d_xyz_stage = bp.take<float>((size_t)n * 3);
   p.d_lut = bp.take<uint32_t>(p.rng.dev.lut_total + 16);
   c.P4 = bp.take<float4>(slots);
   c.RO = bp.take<uint2>(slots);
-  p.d_counts = bp.take<uint32_t>((size_t)T + 1);
   p.d_lc = bp.take<uint32_t>((size_t)T + 1);
   p.d_cell_info = bp.take<uint2>((size_t)T + 1);
   c.cell_info = p.d_cell_info;
@@ -274,13 +282,9 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.l1_hi = bp.take<float4>(p.l1_ub);
   c.root_key = bp.take<uint64_t>(1);
   c.root_pos = bp.take<float4>(1);
-  c.iter = bp.take<uint32_t>(1);
-  c.done = bp.take<uint32_t>(1);
   c.counter = bp.take<uint32_t>(1);
-  p.d_small = bp.take<uint32_t>(4);
   c.out = bp.take<int32_t>(p.m);
   c.prof = bp.take<uint64_t>(kProfWords);
-  c.rs = bp.take<RunState>(1);
   c.hist = bp.take<uint32_t>((size_t)kHists * kHistBins);
   c.pick_p = bp.take<float4>(kListCap);
   c.pick_c = bp.take<uint2>(kListCap);
@@ -294,8 +298,6 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
 }
 
 void layout_scratch(Bump &bp, uint32_t n, uint32_t tmax, Scratch &s) {
-  s.bucket = bp.take<uint32_t>(n);
-  s.fine = bp.take<uint32_t>(n);
   s.kA = bp.take<uint32_t>(n);
   s.kB = bp.take<uint32_t>(n);
   s.vA = bp.take<uint32_t>(n);
@@ -348,37 +350,95 @@ LdsPlan plan_lds(const CloudDev &c) {
   return pl;
 }
 
-// Device build of one cloud up to the initial tree.  Two synchronising
-// read-backs of a few words (sizes decided on device data).
-nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
-  CloudDev &c = p.dev;
-  const uint32_t n = p.n, T = p.rng.dev.T;
-  std::vector<uint32_t> lut;
-  for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
-  HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
-  const float *xyz = p.d_xyz_in;
-  if (p.h_xyz) {
-    HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)n * 12, hipMemcpyHostToDevice, st));
-    xyz = p.d_xyz_stage;
+// Buffers of a call that every cloud gets a contiguous part of, so that one
+// copy or fill serves all clouds: staged host input, bucket populations, the
+// words read back after the first build phase ([0] non-finite flag, [1] the
+// largest bucket, [2] the slot of input row 0, [3] dense leaves), per-point
+// bucket and sub-cell codes.
+struct CallBuffers {
+  float *xyz_stage = nullptr;
+  uint32_t *counts = nullptr, *small = nullptr, *bucket = nullptr, *fine = nullptr;
+  size_t n_total = 0, counts_total = 0;
+};
+
+void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
+  size_t stage = 0;
+  cb.n_total = cb.counts_total = 0;
+  for (auto &p : plans) {
+    if (p.h_xyz) stage += (size_t)p.n * 3;
+    cb.n_total += p.n;
+    cb.counts_total += (size_t)p.rng.dev.T + 1;
   }
-  HIP_TRY(hipMemsetAsync(p.d_counts, 0, ((size_t)T + 1) * 4, st));
-  HIP_TRY(hipMemsetAsync(p.d_small, 0, 16, st));
-  HIP_TRY(launch_cell_keys(xyz, n, p.rng.dev, p.d_lut, s.bucket, s.fine, p.d_counts, p.d_small,
-                           st));
-  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, st));
+  cb.xyz_stage = stage ? bp.take<float>(stage) : nullptr;
+  cb.counts = bp.take<uint32_t>(cb.counts_total);
+  cb.small = bp.take<uint32_t>(4 * plans.size());
+  cb.bucket = bp.take<uint32_t>(cb.n_total);
+  cb.fine = bp.take<uint32_t>(cb.n_total);
+  size_t o_stage = 0, o_n = 0, o_c = 0;
+  for (size_t i = 0; i < plans.size(); ++i) {
+    CloudPlan &p = plans[i];
+    if (p.h_xyz) {
+      p.d_xyz_stage = cb.xyz_stage + o_stage;
+      o_stage += (size_t)p.n * 3;
+    }
+    p.d_counts = cb.counts + o_c;
+    o_c += (size_t)p.rng.dev.T + 1;
+    p.d_small = cb.small + 4 * i;
+    p.d_bucket = cb.bucket + o_n;
+    p.d_fine = cb.fine + o_n;
+    o_n += p.n;
+  }
+}
+
+// Clouds sorted together, cloud index above the bucket: every cloud has the
+// same point count and the keys fit 32 bits with room for sub-cell bits.
+bool sort_together(const std::vector<CloudPlan> &plans, int *cloud_bits, int *bucket_bits) {
+  if (plans.size() < 2) return false;
+  uint32_t tmax = 0;
+  for (auto &p : plans) {
+    if (p.n != plans[0].n) return false;
+    tmax = std::max(tmax, p.rng.dev.T);
+  }
+  *cloud_bits = key_bits_for((uint32_t)plans.size());
+  *bucket_bits = std::max(1, key_bits_for(tmax));
+  return *cloud_bits + *bucket_bits <= 28 && (uint64_t)plans[0].n * plans.size() < (1ull << 31);
+}
+
+// Device build of the clouds of a call up to the initial trees.  The first
+// phase (cell keys, bucket populations, their scans) runs for every cloud,
+// then the stream is synchronised once and a few words per cloud decide each
+// layout; then both sorts run (once for all clouds when they can be sorted
+// together), and each cloud's slots, leaves and tree are built.
+nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &s, hipStream_t st) {
+  const uint32_t T = p.rng.dev.T;
+  if (lut_of) {
+    p.d_lut = lut_of->d_lut;  // the same bit positions: the same tables
+    p.dev.lut = p.d_lut;
+  } else {
+    std::vector<uint32_t> &lut = p.lut_host;
+    lut.clear();
+    for (int a = 0; a < 3; ++a) lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
+    HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
+  }
+  const float *xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
+  HIP_TRY(launch_cell_keys(xyz, p.n, p.rng.dev, p.d_lut, p.d_bucket, p.d_fine, p.d_counts,
+                           p.d_small, st));
+  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, p.d_small + 3, st));
   HIP_TRY(launch_scan(p.d_counts, T, s.scan, st));  // -> first dense position per bucket
   HIP_TRY(launch_scan(p.d_lc, T, s.scan, st));      // -> first leaf per bucket (dense)
-  uint32_t hs[3] = {0, 0, 0};
-  HIP_TRY(hipMemcpyAsync(&hs[0], p.d_small, 8, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(&hs[2], p.d_lc + T, 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
+nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs) {
+  CloudDev &c = p.dev;
+  const uint32_t n = p.n, T = p.rng.dev.T;
   if (hs[0]) return fail(NSFPS_EINVAL, "points must be finite");
-  const uint32_t maxocc = hs[1], dense_leaves = hs[2];
-  // layout decision
+  const uint32_t maxocc = hs[1], dense_leaves = hs[3];
   uint64_t cap = (uint64_t)((maxocc + kLeaf - 1) / kLeaf) * kLeaf;
   uint64_t padded_slots = cap * T;
   bool padded = getenv("NSFPS_NO_PADDED") == nullptr && cap > 0 &&
                 padded_slots <= padded_slot_limit(n) && padded_slots <= p.slots_ub;
+  p.cap = padded ? cap : 0;
   c.padded = padded ? 1u : 0u;
   c.lpc = padded ? (uint32_t)(cap / kLeaf) : 0u;
   c.nslots = padded ? (uint32_t)padded_slots : n;
@@ -388,36 +448,117 @@ nsfps_status build_cloud(CloudPlan &p, const Scratch &s, hipStream_t st) {
   c.nl1 = (c.nleaves + kFan - 1) / kFan;
   if (c.nl1 > kMaxL1)
     return fail(NSFPS_EUNSUPPORTED, "cloud needs %u level-1 nodes (max %u)", c.nl1, kMaxL1);
-  // sort 1: bucket order (stable) -> logical order
-  const int bt = std::max(1, key_bits_for(T));
-  uint32_t *lorig = nullptr, *ko = nullptr;
-  HIP_TRY(hipMemcpyAsync(s.kA, s.bucket, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, n, bt, s.hist, s.scan, true, &ko, &lorig,
-                            st));
-  // sort 2: (bucket, sub-cell) inside the logical order; values = logical rank
-  const int fb = std::min<int>((int)kFineBits, 32 - bt);
+  return NSFPS_OK;
+}
+
+// Both stable sorts of `total` points: nclouds clouds of n_per points stored
+// one after another (nclouds = 1: one cloud).  Sort 1 by (cloud, bucket) gives
+// the logical order (values: rows); sort 2 by (cloud, bucket, sub-cell) inside
+// it gives the physical order (values: logical positions).  Rows and positions
+// count from the first cloud's start.
+nsfps_status sort_points(const uint32_t *bucket, const uint32_t *fine, uint32_t n_per,
+                         uint32_t nclouds, int cloud_bits, int bucket_bits, const Scratch &s,
+                         hipStream_t st, uint32_t **lorig, uint32_t **prank) {
+  const uint32_t total = n_per * nclouds;
+  uint32_t *ko = nullptr;
+  if (nclouds == 1)
+    HIP_TRY(hipMemcpyAsync(s.kA, bucket, (size_t)total * 4, hipMemcpyDeviceToDevice, st));
+  else
+    HIP_TRY(launch_cloud_keys(bucket, total, n_per, bucket_bits, s.kA, st));
+  HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, total, cloud_bits + bucket_bits, s.hist,
+                            s.scan, true, &ko, lorig, st));
+  const int fb = std::min<int>((int)kFineBits, 32 - bucket_bits - cloud_bits);
   const int fshift = (int)kFineBits - fb;
   uint32_t *k2 = (ko == s.kA) ? s.kB : s.kA;
   uint32_t *k2tmp = (k2 == s.kA) ? s.kB : s.kA;
-  uint32_t *v2 = (lorig == s.vA) ? s.vB : s.vA;
-  HIP_TRY(launch_key2(lorig, s.bucket, s.fine, n, fshift, fb, k2, st));
-  uint32_t *prank = nullptr, *kdummy = nullptr;
-  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, n, bt + fb, s.hist, s.scan, true, &kdummy,
-                            &prank, st));
-  if (padded) {
+  uint32_t *v2 = (*lorig == s.vA) ? s.vB : s.vA;
+  const int cloud_shift = std::min(bucket_bits + fb, 31);
+  HIP_TRY(launch_key2(*lorig, bucket, fine, total, n_per, cloud_shift, fshift, fb, k2, st));
+  uint32_t *kdummy = nullptr;
+  HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, total, cloud_bits + bucket_bits + fb, s.hist,
+                            s.scan, true, &kdummy, prank, st));
+  return NSFPS_OK;
+}
+
+// Slots, cell table, leaves and tree of one cloud from the sorts: its
+// physical order is prank[0 .. n), ranks and rows in prank / lorig count from
+// base.
+nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *prank,
+                          uint32_t base, hipStream_t st) {
+  CloudDev &c = p.dev;
+  const uint32_t n = p.n, T = p.rng.dev.T;
+  const float *xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
+  if (c.padded) {
     HIP_TRY(hipMemsetAsync(c.P4, 0, (size_t)c.nslots * sizeof(float4), st));
     HIP_TRY(hipMemsetAsync(const_cast<uint2 *>(c.RO), 0, (size_t)c.nslots * sizeof(uint2), st));
   }
-  HIP_TRY(launch_gather(prank, lorig, s.bucket, p.d_counts, xyz, n, c.padded,
-                        (uint32_t)(padded ? cap : 0), c.P4, const_cast<uint2 *>(c.RO),
-                        p.d_small + 2, st));
+  HIP_TRY(launch_gather(prank, lorig, base, p.d_bucket, p.d_counts, xyz, n, c.padded,
+                        (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), p.d_small + 2, st));
   HIP_TRY(launch_cell_info(p.d_counts, p.d_lc, T, p.d_cell_info, st));
-  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)cap, c.lpc, c.nleaves,
+  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.nleaves,
                             p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
                             const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
                             c.leaf_key, c.leaf_pos, st));
   HIP_TRY(launch_init_state(c, p.d_small + 2, st));
   c.lds = plan_lds(c);
+  return NSFPS_OK;
+}
+
+nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, const Scratch &s,
+                          hipStream_t st) {
+  const size_t nc = plans.size();
+  // input: one copy when the clouds lie one after another in host memory
+  bool one_copy = cb.xyz_stage != nullptr;
+  for (size_t i = 0; i < nc && one_copy; ++i)
+    one_copy = plans[i].h_xyz && (i == 0 || plans[i].h_xyz == plans[i - 1].h_xyz +
+                                                                (size_t)plans[i - 1].n * 3);
+  if (one_copy) {
+    HIP_TRY(hipMemcpyAsync(cb.xyz_stage, plans[0].h_xyz, cb.n_total * 12, hipMemcpyHostToDevice,
+                           st));
+  } else {
+    for (auto &p : plans)
+      if (p.h_xyz)
+        HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)p.n * 12, hipMemcpyHostToDevice,
+                               st));
+  }
+  HIP_TRY(hipMemsetAsync(cb.counts, 0, cb.counts_total * 4, st));
+  HIP_TRY(hipMemsetAsync(cb.small, 0, nc * 16, st));
+  for (size_t i = 0; i < nc; ++i) {
+    const CloudPlan *lut_of = nullptr;
+    if (i > 0 && plans[i].rng.lut[0] == plans[0].rng.lut[0] &&
+        plans[i].rng.lut[1] == plans[0].rng.lut[1] && plans[i].rng.lut[2] == plans[0].rng.lut[2])
+      lut_of = &plans[0];
+    nsfps_status rc = build_phase1(plans[i], lut_of, s, st);
+    if (rc) return rc;
+  }
+  std::vector<uint32_t> hs(4 * nc);
+  HIP_TRY(hipMemcpyAsync(hs.data(), cb.small, nc * 16, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  for (size_t i = 0; i < nc; ++i) {
+    nsfps_status rc = decide_layout(plans[i], &hs[4 * i]);
+    if (rc) return rc;
+  }
+  int cbits = 0, bbits = 0;
+  if (sort_together(plans, &cbits, &bbits)) {
+    uint32_t *lorig = nullptr, *prank = nullptr;
+    nsfps_status rc = sort_points(cb.bucket, cb.fine, plans[0].n, (uint32_t)nc, cbits, bbits, s,
+                                  st, &lorig, &prank);
+    if (rc) return rc;
+    for (size_t i = 0; i < nc; ++i) {
+      const uint32_t base = (uint32_t)(i * plans[0].n);
+      rc = finish_cloud(plans[i], lorig, prank + base, base, st);
+      if (rc) return rc;
+    }
+  } else {
+    for (auto &p : plans) {
+      uint32_t *lorig = nullptr, *prank = nullptr;
+      nsfps_status rc = sort_points(p.d_bucket, p.d_fine, p.n, 1, 0,
+                                    std::max(1, key_bits_for(p.rng.dev.T)), s, st, &lorig, &prank);
+      if (rc) return rc;
+      rc = finish_cloud(p, lorig, prank, 0, st);
+      if (rc) return rc;
+    }
+  }
   return NSFPS_OK;
 }
 
@@ -448,28 +589,21 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
 // windows nearly always resolve the threshold) until a round had to force it
 // and got a list under a quarter full; from the next batch on, every round
 // gets kRefinePasses passes.
-nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds, hipStream_t st,
-                        bool profile, uint64_t *rounds_out) {
+nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
+                        const CloudStatus *d_status, hipStream_t st, bool profile,
+                        uint64_t *rounds_out) {
   uint32_t max_nl1 = 1;
   for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
   const uint32_t nc = (uint32_t)plans.size();
   HIP_TRY(launch_runs_init(d_clouds, nc, st));
-  struct Probe {
-    uint32_t done, iter;
-    RunState rs;
-  };
-  std::vector<Probe> pr(nc);
+  std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0, passes = 0;
   while (true) {
     HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
     enqueued += batch;
-    for (uint32_t i = 0; i < nc; ++i) {
-      const CloudDev &c = plans[i].dev;
-      HIP_TRY(hipMemcpyAsync(&pr[i].done, c.done, 4, hipMemcpyDeviceToHost, st));
-      HIP_TRY(hipMemcpyAsync(&pr[i].iter, c.iter, 4, hipMemcpyDeviceToHost, st));
-      HIP_TRY(hipMemcpyAsync(&pr[i].rs, c.rs, sizeof(RunState), hipMemcpyDeviceToHost, st));
-    }
+    HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
+                           st));
     HIP_TRY(hipStreamSynchronize(st));
     bool all = true;
     uint64_t samples = 0, rounds = 0;
@@ -515,24 +649,38 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
     nmax = std::max(nmax, p.n);
     tmax = std::max(tmax, p.rng.dev.T);
   }
+  // sorts run over one cloud, or over all clouds of a call at once
+  const uint32_t nsort = std::max<uint64_t>(nmax, (uint64_t)nmax * plans.size()) <= 0x7fffffffu
+                             ? (uint32_t)std::max<uint64_t>(nmax, (uint64_t)nmax * plans.size())
+                             : nmax;
   Bump meas(nullptr);
   for (auto &p : plans) layout_cloud(meas, p);
+  CallBuffers cb{};
+  layout_call(meas, plans, cb);
   Scratch sc{};
-  layout_scratch(meas, nmax, tmax, sc);
+  layout_scratch(meas, nsort, tmax, sc);
   meas.take<CloudDev>(plans.size());
+  meas.take<CloudStatus>(plans.size());
   rc = arena_reserve(a, meas.off + 4096);
   if (rc) return rc;
   Bump bp(a.base);
   for (auto &p : plans) layout_cloud(bp, p);
-  layout_scratch(bp, nmax, tmax, sc);
+  layout_call(bp, plans, cb);
+  layout_scratch(bp, nsort, tmax, sc);
   CloudDev *d_clouds = bp.take<CloudDev>(plans.size());
+  CloudStatus *d_status = bp.take<CloudStatus>(plans.size());
+  for (size_t i = 0; i < plans.size(); ++i) {
+    plans[i].dev.done = &d_status[i].done;
+    plans[i].dev.iter = &d_status[i].iter;
+    plans[i].dev.rs = &d_status[i].rs;
+  }
 
   HIP_TRY(hipEventRecord(a.ev[0], st));
   uint64_t leaves = 0, points = 0, wide_total = 0;
   uint32_t lds_bytes = 0;
+  rc = build_clouds(plans, cb, sc, st);
+  if (rc) return rc;
   for (auto &p : plans) {
-    rc = build_cloud(p, sc, st);
-    if (rc) return rc;
     leaves += p.dev.nleaves;
     points += p.n;
     lds_bytes = std::max(lds_bytes, p.dev.lds.total);
@@ -552,7 +700,7 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
                            hipMemcpyHostToDevice, st));
     HIP_TRY(hipEventRecord(a.ev[4], st));
     if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
-    rc = run_rounds(plans, d_clouds, st, profile, &rounds);
+    rc = run_rounds(plans, d_clouds, d_status, st, profile, &rounds);
     if (rc) return rc;
   } else {
     if (plans.size() == 1) {
@@ -572,10 +720,12 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
                              st));
   }
   HIP_TRY(hipEventRecord(a.ev[2], st));
-  std::vector<uint32_t> lens(plans.size());
-  for (size_t i = 0; i < plans.size(); ++i)
-    HIP_TRY(hipMemcpyAsync(&lens[i], plans[i].dev.iter, 4, hipMemcpyDeviceToHost, st));
+  std::vector<CloudStatus> fin(plans.size());
+  HIP_TRY(hipMemcpyAsync(fin.data(), d_status, fin.size() * sizeof(CloudStatus),
+                         hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  std::vector<uint32_t> lens(plans.size());
+  for (size_t i = 0; i < plans.size(); ++i) lens[i] = fin[i].iter;
   uint64_t samples = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
     out_lens[i] = lens[i];

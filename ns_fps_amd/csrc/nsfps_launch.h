@@ -23,17 +23,23 @@ hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
                              uint32_t *scan_tmp, bool iota_values, uint32_t **keys_out,
                              uint32_t **vals_out,
                              hipStream_t st);
+// sort key (cloud << bucket_bits) | bucket of clouds of n_per points stored
+// one after another
+hipError_t launch_cloud_keys(const uint32_t *bucket, uint32_t total, uint32_t n_per,
+                             int bucket_bits, uint32_t *key, hipStream_t st);
 hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,
-                       uint32_t n, int fine_shift, int fine_bits, uint32_t *key2,
-                       hipStream_t st);
+                       uint32_t n, uint32_t n_per, int cloud_shift, int fine_shift, int fine_bits,
+                       uint32_t *key2, hipStream_t st);
 hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
-                              hipStream_t st);
+                              uint32_t *total, hipStream_t st);
 hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
                             uint2 *info, hipStream_t st);
-hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, const uint32_t *bucket,
-                         const uint32_t *cell_start, const float *xyz, uint32_t n,
-                         uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO, uint32_t *phys0,
-                         hipStream_t st);
+// prank / lorig may come from sorts holding other clouds too: ranks and rows
+// of this cloud are base + 0 .. base + n - 1 (prank points at this cloud's part)
+hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
+                         const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
+                         uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
+                         uint32_t *phys0, hipStream_t st);
 hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
                              uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
                              const RangeDev &r, const float4 *P4, const uint2 *RO,

@@ -108,6 +108,25 @@ def test_batched_matches_per_cloud_calls(yf, oracle):
         assert np.array_equal(idx2[b, :lens2[b]], want)
 
 
+def test_batched_mixed_grids_and_many_clouds(yf, oracle):
+    """Clouds sorted together with the cloud index above the bucket: grids of
+    different bucket counts in one call (tables shared only between equal
+    grids), and a call of 100 clouds."""
+    rs = np.random.RandomState(9)
+    clouds = rs.randn(5, 2000, 3).astype(np.float32)
+    clouds[1, 500:700] = clouds[1, :200]  # duplicates
+    blocks = [(8, 8, 8), (16, 16, 16), (4, 8, 16), (16, 16, 16), (32, 2, 8)]
+    rngs = [yf.make_range(-5, 5, -5, 5, -5, 5, *b) for b in blocks]
+    idx, lens = yf.fps_batched(clouds, 400, rngs)
+    for b in range(5):
+        want = oracle.fps(clouds[b], 400, (-5, 5, -5, 5, -5, 5, *blocks[b]))
+        assert np.array_equal(idx[b, :lens[b]], want), b
+    many = rs.rand(100, 600, 3).astype(np.float32)
+    idx, lens = yf.fps_batched(many, 64)
+    for b in range(0, 100, 9):
+        assert np.array_equal(idx[b, :lens[b]], oracle.fps(many[b], 64, None, (16, 16, 16))), b
+
+
 def test_device_pointer_entry_point(lib):
     from ns_fps_amd.capi import Hip
     hip = Hip()
