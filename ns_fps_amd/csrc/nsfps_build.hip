@@ -15,11 +15,12 @@
 namespace nsfps {
 
 // Bucket and sub-cell code per input row; bucket populations; non-finite flag.
-__global__ void k_cell_keys(const float *__restrict__ xyz, uint32_t n, RangeDev r,
-                            const uint32_t *__restrict__ lut, uint32_t *__restrict__ bucket,
-                            uint32_t *__restrict__ fine, uint32_t *__restrict__ counts,
-                            uint32_t *__restrict__ bad) {
-  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void cell_keys_at(uint32_t i, const float *__restrict__ xyz, uint32_t n,
+                                             const RangeDev &r, const uint32_t *__restrict__ lut,
+                                             uint32_t *__restrict__ bucket,
+                                             uint32_t *__restrict__ fine,
+                                             uint32_t *__restrict__ counts,
+                                             uint32_t *__restrict__ bad) {
   if (i >= n) return;
   float v[3] = {xyz[3 * (size_t)i], xyz[3 * (size_t)i + 1], xyz[3 * (size_t)i + 2]};
   uint32_t c[3], f = 0;
@@ -40,6 +41,13 @@ __global__ void k_cell_keys(const float *__restrict__ xyz, uint32_t n, RangeDev 
   bucket[i] = b;
   fine[i] = f;
   atomicAdd(&counts[b], 1u);
+}
+
+__global__ void k_cell_keys(const float *__restrict__ xyz, uint32_t n, RangeDev r,
+                            const uint32_t *__restrict__ lut, uint32_t *__restrict__ bucket,
+                            uint32_t *__restrict__ fine, uint32_t *__restrict__ counts,
+                            uint32_t *__restrict__ bad) {
+  cell_keys_at(blockIdx.x * blockDim.x + threadIdx.x, xyz, n, r, lut, bucket, fine, counts, bad);
 }
 
 // --- stable LSD radix sort (8-bit digits), u32 keys and values -------------
@@ -65,8 +73,8 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const uint32_t *__r
 
 // Exclusive scan of len u32 in place by one 1024-thread workgroup; data[len]
 // receives the total.
-__global__ __launch_bounds__(1024) void k_scan_excl(uint32_t *__restrict__ data, uint32_t len) {
-  __shared__ uint32_t wsum[16];
+__device__ __forceinline__ void scan_excl_block(uint32_t *__restrict__ data, uint32_t len,
+                                                uint32_t *wsum) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t per = (len + 1023) / 1024;
   uint32_t b = tid * per, e = b + per < len ? b + per : len;
@@ -97,6 +105,11 @@ __global__ __launch_bounds__(1024) void k_scan_excl(uint32_t *__restrict__ data,
     run += t;
   }
   if (tid == 1023) data[len] = wsum[15];
+}
+
+__global__ __launch_bounds__(1024) void k_scan_excl(uint32_t *__restrict__ data, uint32_t len) {
+  __shared__ uint32_t wsum[16];
+  scan_excl_block(data, len, wsum);
 }
 
 // Longer scans: chunks of kScanChunk values, four consecutive per thread.
@@ -224,14 +237,13 @@ __global__ void k_key2(const uint32_t *__restrict__ lorig, const uint32_t *__res
 }
 
 // Leaves per bucket, the largest bucket population and the total of leaves.
-__global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict__ counts,
-                                                     uint32_t T, uint32_t *__restrict__ lc,
-                                                     uint32_t *__restrict__ maxocc,
-                                                     uint32_t *__restrict__ total) {
-  __shared__ uint32_t s_sum;
+__device__ __forceinline__ void leaf_counts_block(uint32_t blk, const uint32_t *__restrict__ counts,
+                                                  uint32_t T, uint32_t *__restrict__ lc,
+                                                  uint32_t *__restrict__ maxocc,
+                                                  uint32_t *__restrict__ total, uint32_t &s_sum) {
   if (threadIdx.x == 0) s_sum = 0;
   __syncthreads();
-  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t b = blk * blockDim.x + threadIdx.x;
   if (b < T) {
     uint32_t c = counts[b];
     lc[b] = (c + kLeaf - 1) / kLeaf;
@@ -244,24 +256,37 @@ __global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict_
   if (threadIdx.x == 0 && s_sum) atomicAdd(total, s_sum);
 }
 
+__global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict__ counts,
+                                                     uint32_t T, uint32_t *__restrict__ lc,
+                                                     uint32_t *__restrict__ maxocc,
+                                                     uint32_t *__restrict__ total) {
+  __shared__ uint32_t s_sum;
+  leaf_counts_block(blockIdx.x, counts, T, lc, maxocc, total, s_sum);
+}
+
+__device__ __forceinline__ void cell_info_at(uint32_t b, const uint32_t *__restrict__ cell_start,
+                                             const uint32_t *__restrict__ cell_leaf, uint32_t T,
+                                             uint2 *__restrict__ info) {
+  if (b > T) return;
+  info[b] = make_uint2(cell_start[b], cell_leaf[b]);
+}
+
 __global__ void k_cell_info(const uint32_t *__restrict__ cell_start,
                             const uint32_t *__restrict__ cell_leaf, uint32_t T,
                             uint2 *__restrict__ info) {
-  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b > T) return;
-  info[b] = make_uint2(cell_start[b], cell_leaf[b]);
+  cell_info_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, info);
 }
 
 // Gather into physical slots; min-distance starts at FLT_MAX
 // (src/yuezu_fps.cpp:215-223).  Dense: slot = physical position p.  Padded:
 // slot = bucket * cap + (p - first position of the bucket).
-__global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__restrict__ lorig,
-                         uint32_t base, const uint32_t *__restrict__ bucket,
-                         const uint32_t *__restrict__ cell_start,
-                         const float *__restrict__ xyz, uint32_t n, uint32_t padded, uint32_t cap,
-                         float4 *__restrict__ P4, uint2 *__restrict__ RO,
-                         uint32_t *__restrict__ phys0) {
-  uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void gather_at(uint32_t p, const uint32_t *__restrict__ prank,
+                                          const uint32_t *__restrict__ lorig, uint32_t base,
+                                          const uint32_t *__restrict__ bucket,
+                                          const uint32_t *__restrict__ cell_start,
+                                          const float *__restrict__ xyz, uint32_t n,
+                                          uint32_t padded, uint32_t cap, float4 *__restrict__ P4,
+                                          uint2 *__restrict__ RO, uint32_t *__restrict__ phys0) {
   if (p >= n) return;
   // ranks and rows come from sorts that may hold other clouds: this cloud's
   // start in them is base
@@ -279,13 +304,24 @@ __global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__r
   if (o == 0) *phys0 = slot;
 }
 
+__global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__restrict__ lorig,
+                         uint32_t base, const uint32_t *__restrict__ bucket,
+                         const uint32_t *__restrict__ cell_start,
+                         const float *__restrict__ xyz, uint32_t n, uint32_t padded, uint32_t cap,
+                         float4 *__restrict__ P4, uint2 *__restrict__ RO,
+                         uint32_t *__restrict__ phys0) {
+  gather_at(blockIdx.x * blockDim.x + threadIdx.x, prank, lorig, base, bucket, cell_start, xyz, n,
+            padded, cap, P4, RO, phys0);
+}
+
 // Leaf descriptors (first slot, point count, cell) of every leaf of bucket b.
-__global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
-                            const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
-                            uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
-                            float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
-                            uint32_t *__restrict__ leaf_cell) {
-  uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restrict__ cell_start,
+                                             const uint32_t *__restrict__ cell_leaf, uint32_t T,
+                                             uint32_t padded, uint32_t cap, uint32_t lpc,
+                                             const RangeDev &r, const float4 *__restrict__ P4,
+                                             float4 *__restrict__ leaf_lo,
+                                             float4 *__restrict__ leaf_hi,
+                                             uint32_t *__restrict__ leaf_cell) {
   if (b >= T) return;
   uint32_t s = cell_start[b], e = cell_start[b + 1];
   uint32_t cntb = e - s;
@@ -306,15 +342,24 @@ __global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
   }
 }
 
+__global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
+                            const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
+                            uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
+                            float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
+                            uint32_t *__restrict__ leaf_cell) {
+  leaf_desc_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, padded, cap, lpc,
+               r, P4, leaf_lo, leaf_hi, leaf_cell);
+}
+
 // Leaf bounding boxes and initial keys (FLT_MAX with the smallest rank of the
 // leaf); empty leaves get an empty box and key 0.  One wave per leaf.
-__global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float4 *__restrict__ P4,
-                                                   const uint2 *__restrict__ RO,
-                                                   float4 *__restrict__ leaf_lo,
-                                                   float4 *__restrict__ leaf_hi,
-                                                   uint64_t *__restrict__ leaf_key,
-                                                   float4 *__restrict__ leaf_pos) {
-  uint32_t leaf = blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void leaf_bbox_at(uint32_t leaf, uint32_t nleaves,
+                                             const float4 *__restrict__ P4,
+                                             const uint2 *__restrict__ RO,
+                                             float4 *__restrict__ leaf_lo,
+                                             float4 *__restrict__ leaf_hi,
+                                             uint64_t *__restrict__ leaf_key,
+                                             float4 *__restrict__ leaf_pos) {
   uint32_t lane = lane_id();
   if (leaf >= nleaves) return;
   float4 lo = leaf_lo[leaf], hi = leaf_hi[leaf];
@@ -352,18 +397,27 @@ __global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float
   }
 }
 
+__global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float4 *__restrict__ P4,
+                                                   const uint2 *__restrict__ RO,
+                                                   float4 *__restrict__ leaf_lo,
+                                                   float4 *__restrict__ leaf_hi,
+                                                   uint64_t *__restrict__ leaf_key,
+                                                   float4 *__restrict__ leaf_pos) {
+  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
+               leaf_pos);
+}
+
 // Level-1 nodes from the initial leaves: max key, its position, and the union
 // of the leaf boxes.  One wave per node.
-__global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
-                                                 const uint64_t *__restrict__ leaf_key,
-                                                 const float4 *__restrict__ leaf_pos,
-                                                 const float4 *__restrict__ leaf_lo,
-                                                 const float4 *__restrict__ leaf_hi,
-                                                 uint64_t *__restrict__ l1_key,
-                                                 float4 *__restrict__ l1_pos,
-                                                 float4 *__restrict__ l1_lo,
-                                                 float4 *__restrict__ l1_hi) {
-  uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void l1_init_at(uint32_t g, uint32_t nleaves, uint32_t nl1,
+                                           const uint64_t *__restrict__ leaf_key,
+                                           const float4 *__restrict__ leaf_pos,
+                                           const float4 *__restrict__ leaf_lo,
+                                           const float4 *__restrict__ leaf_hi,
+                                           uint64_t *__restrict__ l1_key,
+                                           float4 *__restrict__ l1_pos,
+                                           float4 *__restrict__ l1_lo,
+                                           float4 *__restrict__ l1_hi) {
   uint32_t lane = lane_id();
   if (g >= nl1) return;
   uint32_t j = g * kFan + lane;
@@ -391,14 +445,29 @@ __global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
   }
 }
 
+__global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
+                                                 const uint64_t *__restrict__ leaf_key,
+                                                 const float4 *__restrict__ leaf_pos,
+                                                 const float4 *__restrict__ leaf_lo,
+                                                 const float4 *__restrict__ leaf_hi,
+                                                 uint64_t *__restrict__ l1_key,
+                                                 float4 *__restrict__ l1_pos,
+                                                 float4 *__restrict__ l1_lo,
+                                                 float4 *__restrict__ l1_hi) {
+  l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, nl1, leaf_key, leaf_pos, leaf_lo,
+             leaf_hi, l1_key, l1_pos, l1_lo, l1_hi);
+}
+
+__device__ __forceinline__ void init_state_of(const CloudDev &c, const uint32_t *phys0) {
+  *c.iter = 0;
+  *c.done = 0;
+  *c.counter = 0;
+  *c.root_key = 0;
+  *c.root_pos = c.P4[*phys0];
+}
+
 __global__ void k_init_state(CloudDev c, const uint32_t *__restrict__ phys0) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    *c.iter = 0;
-    *c.done = 0;
-    *c.counter = 0;
-    *c.root_key = 0;
-    *c.root_pos = c.P4[*phys0];
-  }
+  if (threadIdx.x == 0 && blockIdx.x == 0) init_state_of(c, phys0);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -511,6 +580,91 @@ hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStre
                                               const_cast<float4 *>(c.l1_lo),
                                               const_cast<float4 *>(c.l1_hi));
   k_init_state<<<1, 64, 0, st>>>(c, d_phys0);
+  return hipGetLastError();
+}
+
+// ---- the build steps of many clouds, one launch each (grid y = cloud) -----
+
+__global__ void kb_cell_keys(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  cell_keys_at(blockIdx.x * blockDim.x + threadIdx.x, b.xyz, b.n, b.c.r, b.c.lut, b.bucket, b.fine,
+               b.counts, b.small);
+}
+
+__global__ __launch_bounds__(256) void kb_leaf_counts(const BuildDev *__restrict__ bd) {
+  __shared__ uint32_t s_sum;
+  const BuildDev &b = bd[blockIdx.y];
+  if (blockIdx.x * blockDim.x >= b.T) return;  // the whole block: no barrier is split
+  leaf_counts_block(blockIdx.x, b.counts, b.T, b.lc, b.small + 1, b.small + 3, s_sum);
+}
+
+// block 2i scans cloud i's bucket populations, block 2i + 1 its leaf counts
+__global__ __launch_bounds__(1024) void kb_scans(const BuildDev *__restrict__ bd) {
+  __shared__ uint32_t wsum[16];
+  const BuildDev &b = bd[blockIdx.x >> 1];
+  scan_excl_block((blockIdx.x & 1) ? b.lc : b.counts, b.T, wsum);
+}
+
+__global__ void kb_zero_slots(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (!b.c.padded || i >= b.c.nslots) return;
+  b.c.P4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const_cast<uint2 *>(b.c.RO)[i] = make_uint2(0u, 0u);
+}
+
+__global__ void kb_gather(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  gather_at(blockIdx.x * blockDim.x + threadIdx.x, b.prank, b.lorig, b.base, b.bucket, b.counts,
+            b.xyz, b.n, b.c.padded, b.cap, b.c.P4, const_cast<uint2 *>(b.c.RO), b.small + 2);
+}
+
+__global__ void kb_cells(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  cell_info_at(i, b.counts, b.lc, b.T, const_cast<uint2 *>(b.c.cell_info));
+  leaf_desc_at(i, b.counts, b.lc, b.T, b.c.padded, b.cap, b.c.lpc, b.c.r, b.c.P4,
+               const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
+               const_cast<uint32_t *>(b.c.leaf_cell));
+}
+
+__global__ __launch_bounds__(256) void kb_leaf_bbox(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), b.c.nleaves, b.c.P4, b.c.RO,
+               const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
+               b.c.leaf_key, b.c.leaf_pos);
+}
+
+__global__ __launch_bounds__(256) void kb_l1_init(const BuildDev *__restrict__ bd) {
+  const BuildDev &b = bd[blockIdx.y];
+  const CloudDev &c = b.c;
+  l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), c.nleaves, c.nl1, c.leaf_key, c.leaf_pos,
+             c.leaf_lo, c.leaf_hi, c.l1_key, c.l1_pos, const_cast<float4 *>(c.l1_lo),
+             const_cast<float4 *>(c.l1_hi));
+}
+
+__global__ void kb_init_state(const BuildDev *__restrict__ bd) {
+  if (threadIdx.x == 0) init_state_of(bd[blockIdx.x].c, bd[blockIdx.x].small + 2);
+}
+
+hipError_t launch_build_first_many(const BuildDev *d_bd, uint32_t nclouds, uint32_t nmax,
+                                   uint32_t tmax, hipStream_t st) {
+  if (tmax + 1 > kScanSingleMax) return hipErrorInvalidValue;
+  if (nmax) kb_cell_keys<<<dim3(cdiv(nmax, 256), nclouds), 256, 0, st>>>(d_bd);
+  kb_leaf_counts<<<dim3(cdiv(tmax, 256), nclouds), 256, 0, st>>>(d_bd);
+  kb_scans<<<2 * nclouds, 1024, 0, st>>>(d_bd);
+  return hipGetLastError();
+}
+
+hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32_t nmax,
+                                  uint32_t tmax, uint32_t slots_max, uint32_t leaves_max,
+                                  uint32_t l1_max, hipStream_t st) {
+  if (slots_max) kb_zero_slots<<<dim3(cdiv(slots_max, 256), nclouds), 256, 0, st>>>(d_bd);
+  if (nmax) kb_gather<<<dim3(cdiv(nmax, 256), nclouds), 256, 0, st>>>(d_bd);
+  kb_cells<<<dim3(cdiv((uint64_t)tmax + 1, 256), nclouds), 256, 0, st>>>(d_bd);
+  if (leaves_max) kb_leaf_bbox<<<dim3(cdiv(leaves_max, 4), nclouds), 256, 0, st>>>(d_bd);
+  if (l1_max) kb_l1_init<<<dim3(cdiv(l1_max, 4), nclouds), 256, 0, st>>>(d_bd);
+  kb_init_state<<<nclouds, 64, 0, st>>>(d_bd);
   return hipGetLastError();
 }
 

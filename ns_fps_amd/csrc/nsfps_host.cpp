@@ -358,6 +358,7 @@ LdsPlan plan_lds(const CloudDev &c) {
 struct CallBuffers {
   float *xyz_stage = nullptr;
   uint32_t *counts = nullptr, *small = nullptr, *bucket = nullptr, *fine = nullptr;
+  BuildDev *bd = nullptr;  // per-cloud parameters of the many-cloud build steps
   size_t n_total = 0, counts_total = 0;
 };
 
@@ -374,6 +375,7 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   cb.small = bp.take<uint32_t>(4 * plans.size());
   cb.bucket = bp.take<uint32_t>(cb.n_total);
   cb.fine = bp.take<uint32_t>(cb.n_total);
+  cb.bd = bp.take<BuildDev>(plans.size());
   size_t o_stage = 0, o_n = 0, o_c = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
     CloudPlan &p = plans[i];
@@ -504,8 +506,10 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
   return NSFPS_OK;
 }
 
+// bd: host copies of the many-cloud build parameters, sources of
+// asynchronous copies; the caller keeps them until the stream is synchronised.
 nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, const Scratch &s,
-                          hipStream_t st) {
+                          std::vector<BuildDev> &bd, hipStream_t st) {
   const size_t nc = plans.size();
   // input: one copy when the clouds lie one after another in host memory
   bool one_copy = cb.xyz_stage != nullptr;
@@ -523,13 +527,53 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   }
   HIP_TRY(hipMemsetAsync(cb.counts, 0, cb.counts_total * 4, st));
   HIP_TRY(hipMemsetAsync(cb.small, 0, nc * 16, st));
+  // many clouds sorted together, of few buckets each: one launch per build
+  // step for all of them
+  uint32_t nmax = 0, tmax = 0;
+  for (auto &p : plans) {
+    nmax = std::max(nmax, p.n);
+    tmax = std::max(tmax, p.rng.dev.T);
+  }
+  int cbits = 0, bbits = 0;
+  const bool together = sort_together(plans, &cbits, &bbits);
+  const bool many = together && tmax <= kManyMaxBuckets;
+  bd.assign(many ? nc : 0, BuildDev{});
   for (size_t i = 0; i < nc; ++i) {
     const CloudPlan *lut_of = nullptr;
     if (i > 0 && plans[i].rng.lut[0] == plans[0].rng.lut[0] &&
         plans[i].rng.lut[1] == plans[0].rng.lut[1] && plans[i].rng.lut[2] == plans[0].rng.lut[2])
       lut_of = &plans[0];
+    if (many) {
+      CloudPlan &p = plans[i];
+      if (lut_of) {
+        p.d_lut = lut_of->d_lut;
+        p.dev.lut = p.d_lut;
+      } else {
+        std::vector<uint32_t> &lut = p.lut_host;
+        lut.clear();
+        for (int a = 0; a < 3; ++a)
+          lut.insert(lut.end(), p.rng.lut[a].begin(), p.rng.lut[a].end());
+        HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
+      }
+      BuildDev &b = bd[i];
+      b = BuildDev{};
+      b.c = p.dev;
+      b.xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
+      b.bucket = p.d_bucket;
+      b.fine = p.d_fine;
+      b.counts = p.d_counts;
+      b.lc = p.d_lc;
+      b.small = p.d_small;
+      b.n = p.n;
+      b.T = p.rng.dev.T;
+      continue;
+    }
     nsfps_status rc = build_phase1(plans[i], lut_of, s, st);
     if (rc) return rc;
+  }
+  if (many) {
+    HIP_TRY(hipMemcpyAsync(cb.bd, bd.data(), nc * sizeof(BuildDev), hipMemcpyHostToDevice, st));
+    HIP_TRY(launch_build_first_many(cb.bd, (uint32_t)nc, nmax, tmax, st));
   }
   std::vector<uint32_t> hs(4 * nc);
   HIP_TRY(hipMemcpyAsync(hs.data(), cb.small, nc * 16, hipMemcpyDeviceToHost, st));
@@ -538,12 +582,31 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     nsfps_status rc = decide_layout(plans[i], &hs[4 * i]);
     if (rc) return rc;
   }
-  int cbits = 0, bbits = 0;
-  if (sort_together(plans, &cbits, &bbits)) {
+  if (together) {
     uint32_t *lorig = nullptr, *prank = nullptr;
     nsfps_status rc = sort_points(cb.bucket, cb.fine, plans[0].n, (uint32_t)nc, cbits, bbits, s,
                                   st, &lorig, &prank);
     if (rc) return rc;
+    if (many) {
+      uint32_t slots_max = 0, leaves_max = 0, l1_max = 0;
+      for (size_t i = 0; i < nc; ++i) {
+        CloudPlan &p = plans[i];
+        BuildDev &b = bd[i];
+        b.c = p.dev;
+        b.cap = (uint32_t)p.cap;
+        b.base = (uint32_t)(i * plans[0].n);
+        b.prank = prank + b.base;
+        b.lorig = lorig;
+        if (p.dev.padded) slots_max = std::max(slots_max, p.dev.nslots);
+        leaves_max = std::max(leaves_max, p.dev.nleaves);
+        l1_max = std::max(l1_max, p.dev.nl1);
+        p.dev.lds = plan_lds(p.dev);
+      }
+      HIP_TRY(hipMemcpyAsync(cb.bd, bd.data(), nc * sizeof(BuildDev), hipMemcpyHostToDevice, st));
+      HIP_TRY(launch_build_rest_many(cb.bd, (uint32_t)nc, nmax, tmax, slots_max, leaves_max,
+                                     l1_max, st));
+      return NSFPS_OK;
+    }
     for (size_t i = 0; i < nc; ++i) {
       const uint32_t base = (uint32_t)(i * plans[0].n);
       rc = finish_cloud(plans[i], lorig, prank + base, base, st);
@@ -678,7 +741,8 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   HIP_TRY(hipEventRecord(a.ev[0], st));
   uint64_t leaves = 0, points = 0, wide_total = 0;
   uint32_t lds_bytes = 0;
-  rc = build_clouds(plans, cb, sc, st);
+  std::vector<BuildDev> bd_host;  // lives until the stream is synchronised below
+  rc = build_clouds(plans, cb, sc, bd_host, st);
   if (rc) return rc;
   for (auto &p : plans) {
     leaves += p.dev.nleaves;

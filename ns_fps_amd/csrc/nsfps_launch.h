@@ -47,6 +47,30 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
                              uint64_t *leaf_key, float4 *leaf_pos, hipStream_t st);
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st);
 
+// The build of many clouds, each step one launch for all of them (grid y =
+// cloud), when every cloud has at most kManyMaxBuckets buckets.  Parameters
+// per cloud live in device memory.
+struct BuildDev {
+  CloudDev c;                // the cloud's buffers and sizes
+  const float *xyz;          // input (device)
+  uint32_t *bucket, *fine;   // per input row
+  uint32_t *counts, *lc;     // per bucket, scanned to first slot / first leaf
+  uint32_t *small;           // [0] non-finite flag, [1] largest bucket, [2] slot of row 0,
+                             // [3] dense leaves
+  const uint32_t *prank;     // the sorts: this cloud's part of the physical order
+  const uint32_t *lorig;     //   and the logical order of all clouds sorted together
+  uint32_t n, T, cap, base;  // cap: slots per bucket when padded; base: this cloud's
+                             // first rank / row in the sorts
+};
+constexpr uint32_t kManyMaxBuckets = 16383;
+// cell keys, bucket populations, leaf counts and both scans
+hipError_t launch_build_first_many(const BuildDev *d_bd, uint32_t nclouds, uint32_t nmax,
+                                   uint32_t tmax, hipStream_t st);
+// slots, cell table, leaves, level-1 nodes, initial state
+hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32_t nmax,
+                                  uint32_t tmax, uint32_t slots_max, uint32_t leaves_max,
+                                  uint32_t l1_max, hipStream_t st);
+
 // sampling
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
 hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t lds_bytes,
