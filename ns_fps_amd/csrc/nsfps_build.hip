@@ -240,28 +240,31 @@ __global__ void k_key2(const uint32_t *__restrict__ lorig, const uint32_t *__res
 __device__ __forceinline__ void leaf_counts_block(uint32_t blk, const uint32_t *__restrict__ counts,
                                                   uint32_t T, uint32_t *__restrict__ lc,
                                                   uint32_t *__restrict__ maxocc,
-                                                  uint32_t *__restrict__ total, uint32_t &s_sum) {
-  if (threadIdx.x == 0) s_sum = 0;
+                                                  uint32_t *__restrict__ total, uint32_t *s_red) {
+  // s_red[0]: leaves of the block, s_red[1]: its largest bucket (one global
+  // atomic each per block)
+  if (threadIdx.x < 2) s_red[threadIdx.x] = 0;
   __syncthreads();
   uint32_t b = blk * blockDim.x + threadIdx.x;
   if (b < T) {
     uint32_t c = counts[b];
     lc[b] = (c + kLeaf - 1) / kLeaf;
     if (c) {
-      atomicMax(maxocc, c);
-      atomicAdd(&s_sum, (c + kLeaf - 1) / kLeaf);
+      atomicMax(&s_red[1], c);
+      atomicAdd(&s_red[0], (c + kLeaf - 1) / kLeaf);
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0 && s_sum) atomicAdd(total, s_sum);
+  if (threadIdx.x == 0 && s_red[0]) atomicAdd(total, s_red[0]);
+  if (threadIdx.x == 1 && s_red[1]) atomicMax(maxocc, s_red[1]);
 }
 
 __global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict__ counts,
                                                      uint32_t T, uint32_t *__restrict__ lc,
                                                      uint32_t *__restrict__ maxocc,
                                                      uint32_t *__restrict__ total) {
-  __shared__ uint32_t s_sum;
-  leaf_counts_block(blockIdx.x, counts, T, lc, maxocc, total, s_sum);
+  __shared__ uint32_t s_red[2];
+  leaf_counts_block(blockIdx.x, counts, T, lc, maxocc, total, s_red);
 }
 
 __device__ __forceinline__ void cell_info_at(uint32_t b, const uint32_t *__restrict__ cell_start,
@@ -592,10 +595,10 @@ __global__ void kb_cell_keys(const BuildDev *__restrict__ bd) {
 }
 
 __global__ __launch_bounds__(256) void kb_leaf_counts(const BuildDev *__restrict__ bd) {
-  __shared__ uint32_t s_sum;
+  __shared__ uint32_t s_red[2];
   const BuildDev &b = bd[blockIdx.y];
   if (blockIdx.x * blockDim.x >= b.T) return;  // the whole block: no barrier is split
-  leaf_counts_block(blockIdx.x, b.counts, b.T, b.lc, b.small + 1, b.small + 3, s_sum);
+  leaf_counts_block(blockIdx.x, b.counts, b.T, b.lc, b.small + 1, b.small + 3, s_red);
 }
 
 // block 2i scans cloud i's bucket populations, block 2i + 1 its leaf counts
