@@ -885,9 +885,10 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     }
     if (nlive == 0) break;  // every key is below B: the run ends
     NSFPS_RMARK(kRpSelect);
-    // ---- hot copies -> LDS, placed by an LDS counter, each with its cube
-    // computed by the thread that holds it; unused slots were cleared during
-    // the previous hot set's walk (key 0)
+    // ---- hot copies -> LDS, placed by an LDS counter; then one wave computes
+    // every copy's cube (one pass over the cube code rather than one per wave
+    // holding a hot entry).  Unused slots were cleared during the previous
+    // hot set's walk (key 0).
     {
       uint64_t bal[kOwnSlots];
       uint32_t tot = 0;
@@ -899,49 +900,34 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       uint32_t base = 0;
       if (lane == 0 && tot) base = atomicAdd(&s_nhot, tot);
       base = rdlane(base, 0);
-      // a thread rarely holds two hot entries: one pass over the cube code
-      // per hot entry of the thread, selected from its slots
-      uint32_t pend = 0, slot[kOwnSlots];
+      // raw copies: {cell, ~rank, distance} and {x, y, z, row}
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s) {
-        pend |= (uint32_t)((bal[s] >> lane) & 1u) << s;
-        slot[s] = base + lanes_below(bal[s]);
+        const uint32_t hi = base + lanes_below(bal[s]);
         base += (uint32_t)__popcll(bal[s]);
-      }
-      while (pend) {
-        const uint32_t s = (uint32_t)__builtin_ctz(pend);
-        pend &= pend - 1;
-        uint32_t hi = slot[0], cs = cc[0], ls = lo[0], rs_ = row[0];
-        float ds = d[0], xs = x[0], ys = y[0], zs = z[0];
-#pragma unroll
-        for (uint32_t t = 1; t < kOwnSlots; ++t) {
-          if (s == t) {
-            hi = slot[t];
-            cs = cc[t];
-            ls = lo[t];
-            rs_ = row[t];
-            ds = d[t];
-            xs = x[t];
-            ys = y[t];
-            zs = z[t];
+        if ((bal[s] >> lane) & 1u) {
+          if (hi < kHot) {
+            s_hx[hi] = make_uint4(cc[s], lo[s], __float_as_uint(d[s]), 0u);
+            s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
+                                  __float_as_uint(z[s]), row[s]);
+          } else {  // cannot happen (at most kHot keys are >= the hot threshold)
+            *err = 2;
           }
-        }
-        if (hi < kHot) {
-          const uint32_t h = packed_halves(c.r, ds);
-          uint32_t lo_c, hi_c;
-          cube_corners(cs, h, b0, b1, b2, lo_c, hi_c);
-          s_hq[0][hot_slot(hi)] =
-              make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, ls, __float_as_uint(ds));
-          s_hx[hi] = make_uint4(cs, pack11(cs) | kGuards, pack11(cs), h);
-          s_hp[hi] = make_uint4(__float_as_uint(xs), __float_as_uint(ys), __float_as_uint(zs), rs_);
-        } else {  // cannot happen (at most kHot keys are >= the hot threshold)
-          *err = 2;
         }
       }
       if (tid < 2) s_big[tid] = 0;
       if (tid == 0) {
         s_lowm[0] = 0;
         s_kmr = 0;
+      }
+      __syncthreads();
+      if (wave == 0 && lane < min(s_nhot, kHot)) {
+        const uint4 hx = s_hx[lane];
+        const uint32_t h = packed_halves(c.r, __uint_as_float(hx.z));
+        uint32_t lo_c, hi_c;
+        cube_corners(hx.x, h, b0, b1, b2, lo_c, hi_c);
+        s_hq[0][hot_slot(lane)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hx.y, hx.z);
+        s_hx[lane] = make_uint4(hx.x, pack11(hx.x) | kGuards, pack11(hx.x), h);
       }
       __syncthreads();
     }
