@@ -5,6 +5,8 @@
   fps_batched), built from csrc/ by ``python -m ns_fps_amd.build``.
 * ``ns_fps_amd.capi`` -- ctypes binding of the C ABI (include/nsfps.h).
 * ``ns_fps_amd.workloads`` -- seeded synthetic clouds of the benchmark.
+* ``ns_fps_amd.kitti`` -- KITTI scan files: reader, z filter, bounds range
+  and the reference drivers' sampling runs.
 
 There is no CPU implementation: without the built HIP library and a device,
 compute calls raise.
