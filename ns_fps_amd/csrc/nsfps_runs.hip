@@ -694,7 +694,23 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  if (*gptr(c.done)) return;
+  NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
+  // every input of the run is read at once: the done flag, the run state and
+  // the whole list buffer (entries at or beyond the list length are stale
+  // and ignored)
+  const uint32_t done_in = *gptr(c.done);
+  const uint32_t nlist = min(rs.nlist, kListCap);
+  const uint64_t bkey = rs.bkey, kref0 = rs.kref0;
+  float4 P[kOwnSlots];
+  uint2 R[kOwnSlots];
+  uint32_t C[kOwnSlots];
+#pragma unroll
+  for (uint32_t s = 0; s < kOwnSlots; ++s) {
+    const uint32_t i = s * kRunThreads + tid;
+    P[s] = gptr(c.list_p)[i];
+    R[s] = gptr(c.list_r)[i];
+    C[s] = gptr(c.list_c)[i];
+  }
   uint64_t pf[kRpWords] = {}, tl = 0;
   if (PROF) tl = __builtin_amdgcn_s_memtime();
 #define NSFPS_RMARK(ph)                                  \
@@ -705,7 +721,6 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       tl = t_;                                           \
     }                                                    \
   } while (0)
-  NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   const uint32_t b0 = c.r.blocks[0], b1 = c.r.blocks[1], b2 = c.r.blocks[2];
   // coarse cells (x >> sx, y >> sy, z >> sz), at most kCells of them: the
   // longest coarse axis is halved until they fit
@@ -730,22 +745,16 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     s_geo[1] = ncx;
     s_geo[2] = ncy;
   }
-  const uint32_t nlist = min(rs.nlist, kListCap);
-  const uint64_t bkey = rs.bkey;
   __syncthreads();
+  if (done_in) return;  // uniform: the whole workgroup leaves
 
   // ---- list -> LDS in coarse-cell order (counting sort)
   {
-    float4 P[kOwnSlots];
-    uint2 R[kOwnSlots];
-    uint32_t C[kOwnSlots], G[kOwnSlots], K[kOwnSlots];
+    uint32_t G[kOwnSlots], K[kOwnSlots];
 #pragma unroll
     for (uint32_t s = 0; s < kOwnSlots; ++s) {
       const uint32_t i = s * kRunThreads + tid;
       if (i < nlist) {
-        P[s] = gptr(c.list_p)[i];
-        R[s] = gptr(c.list_r)[i];
-        C[s] = gptr(c.list_c)[i];
         G[s] = (((C[s] >> 20) >> sz) * ncy + (((C[s] >> 10) & 1023u) >> sy)) * ncx +
                ((C[s] & 1023u) >> sx);
         K[s] = atomicAdd(&s_cell[G[s]], 1u);
@@ -819,7 +828,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   bool done = false;
   // The first hot set's histogram: every key is <= kref0 (keys only decrease).
   // Later ones are counted right after each hot set's walk.
-  uint64_t kref = rs.kref0 > bkey ? rs.kref0 : bkey;
+  uint64_t kref = kref0 > bkey ? kref0 : bkey;
   uint32_t S = sel_shift(kref, bkey);
   hist_live(d, lo, bkey, kref, S, s_sel[0], err);
   __syncthreads();
