@@ -18,6 +18,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "nsfps_internal.h"
@@ -133,24 +134,94 @@ void derive(const nsfps_range &r, HostRange &h) {
   d.bijective = bij ? 1u : 0u;
 }
 
-void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) {
-  // compute_bbox, src/yuezu_fps.cpp:648-670 (std::min/std::max comparisons)
-  if (n == 0) {
-    r.min_x = 0; r.max_x = 1; r.min_y = 0; r.max_y = 1; r.min_z = 0; r.max_z = 1;
-    r.x_blocks = r.y_blocks = r.z_blocks = 1;
-    return;
-  }
-  float mn[3] = {xyz[0], xyz[1], xyz[2]}, mx[3] = {xyz[0], xyz[1], xyz[2]};
-  for (uint64_t i = 0; i < n; ++i)
-    for (int a = 0; a < 3; ++a) {
-      float v = xyz[3 * i + a];
-      mn[a] = (v < mn[a]) ? v : mn[a];
-      mx[a] = (mx[a] < v) ? v : mx[a];
+// compute_bbox (src/yuezu_fps.cpp:648-670) keeps, per axis, the running
+// (v < mn ? v : mn) and (mx < v ? v : mx) from point 0.  Here points
+// [lo, hi) run through 24 independent lanes (eight points a step; lane k
+// holds axis k % 3), every lane started from point 0 of the cloud, and the
+// lanes are folded with the same selects.  Minimum and maximum of the finite
+// values do not depend on the order, a NaN point 0 stays NaN and any later
+// NaN is skipped, exactly as in the single running pass; so pieces of one
+// cloud may run on different threads and fold in any order.
+void bounds_piece(const float *xyz, uint64_t lo, uint64_t hi, const float *p0, float *mn3,
+                  float *mx3) {
+  constexpr int kL = 24;
+  float mn[kL], mx[kL];
+  for (int k = 0; k < kL; ++k) mn[k] = mx[k] = p0[k % 3];
+  const float *p = xyz + 3 * lo;
+  const uint64_t nf = 3 * (hi - lo);
+  uint64_t j = 0;
+  for (; j + kL <= nf; j += kL)
+    for (int k = 0; k < kL; ++k) {
+      const float v = p[j + k];
+      mn[k] = v < mn[k] ? v : mn[k];
+      mx[k] = mx[k] < v ? v : mx[k];
     }
-  r.min_x = mn[0] - kBoundaryEps; r.max_x = mx[0] + kBoundaryEps;
-  r.min_y = mn[1] - kBoundaryEps; r.max_y = mx[1] + kBoundaryEps;
-  r.min_z = mn[2] - kBoundaryEps; r.max_z = mx[2] + kBoundaryEps;
+  for (; j < nf; ++j) {
+    const int k = (int)(j % 3);
+    const float v = p[j];
+    mn[k] = v < mn[k] ? v : mn[k];
+    mx[k] = mx[k] < v ? v : mx[k];
+  }
+  for (int a = 0; a < 3; ++a) {
+    float m = mn[a], M = mx[a];
+    for (int k = a + 3; k < kL; k += 3) {
+      m = mn[k] < m ? mn[k] : m;
+      M = M < mx[k] ? mx[k] : M;
+    }
+    mn3[a] = m;
+    mx3[a] = M;
+  }
 }
+
+// compute_bbox of `count` clouds of n points each (ranges[b] gets cloud b's
+// bounds +- 1e-6; block counts untouched).  Pieces of at least kPiece points
+// are spread over up to 16 threads when there is enough work.
+void bboxes(const float *xyz, uint64_t count, uint64_t n, nsfps_range *ranges) {
+  constexpr uint64_t kPiece = 1u << 16;
+  const uint64_t per = n ? (n + kPiece - 1) / kPiece : 0;  // pieces per cloud
+  const uint64_t pieces = count * per;
+  std::vector<float> part(6 * std::max<uint64_t>(pieces, 1));
+  auto run = [&](uint64_t q) {
+    const uint64_t b = q / per, k = q % per;
+    const float *c = xyz + b * n * 3;
+    bounds_piece(c, k * kPiece, std::min(n, (k + 1) * kPiece), c, &part[6 * q], &part[6 * q + 3]);
+  };
+  const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const uint64_t nt = std::min<uint64_t>(hw, pieces);
+  if (nt <= 1 || count * n < 4 * kPiece) {
+    for (uint64_t q = 0; q < pieces; ++q) run(q);
+  } else {
+    std::vector<std::thread> th;
+    for (uint64_t t = 0; t < nt; ++t)
+      th.emplace_back([&, t] {
+        for (uint64_t q = t; q < pieces; q += nt) run(q);
+      });
+    for (auto &x : th) x.join();
+  }
+  for (uint64_t b = 0; b < count; ++b) {
+    nsfps_range &r = ranges[b];
+    if (n == 0) {
+      r.min_x = 0; r.max_x = 1; r.min_y = 0; r.max_y = 1; r.min_z = 0; r.max_z = 1;
+      r.x_blocks = r.y_blocks = r.z_blocks = 1;
+      continue;
+    }
+    float mn[3], mx[3];
+    for (int a = 0; a < 3; ++a) {
+      mn[a] = part[6 * b * per + a];
+      mx[a] = part[6 * b * per + 3 + a];
+      for (uint64_t k = 1; k < per; ++k) {
+        const float lo = part[6 * (b * per + k) + a], hi = part[6 * (b * per + k) + 3 + a];
+        mn[a] = lo < mn[a] ? lo : mn[a];
+        mx[a] = mx[a] < hi ? hi : mx[a];
+      }
+    }
+    r.min_x = mn[0] - kBoundaryEps; r.max_x = mx[0] + kBoundaryEps;
+    r.min_y = mn[1] - kBoundaryEps; r.max_y = mx[1] + kBoundaryEps;
+    r.min_z = mn[2] - kBoundaryEps; r.max_z = mx[2] + kBoundaryEps;
+  }
+}
+
+void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) { bboxes(xyz, 1, n, &r); }
 
 // ------------------------------------------------------------ workspace ----
 
@@ -947,16 +1018,14 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n, uin
   if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
   if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
   std::vector<nsfps_range> rs(batch);
+  if (!ranges) bboxes(xyz, batch, n, rs.data());
   for (uint64_t b = 0; b < batch; ++b) {
     if (ranges) {
       rs[b] = ranges[b];
-    } else {
-      bbox_of(xyz + b * n * 3, n, rs[b]);
-      if (n) {
-        rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
-        rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
-        rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
-      }
+    } else if (n) {
+      rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
+      rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
+      rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
     }
     nsfps_status rc = check_range(rs[b]);
     if (rc) return rc;

@@ -66,14 +66,41 @@ def test_capi_range_derive_matches_oracle(capi, oracle):
         assert info.total_blocks == rng[6] * rng[7] * rng[8]
 
 
-def test_capi_bbox_matches_oracle(capi, oracle):
-    pts = np.random.RandomState(3).randn(777, 3).astype(np.float32) * 5
+def _capi_bbox(capi, pts):
     out = Range()
     assert capi.nsfps_bbox(pts.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint64(len(pts)), 16, 8, 4,
                            ctypes.byref(out)) == 0
-    got = np.array([out.min_x, out.max_x, out.min_y, out.max_y, out.min_z, out.max_z], np.float32)
-    assert got.tobytes() == oracle.bbox(pts).tobytes()
     assert (out.x_blocks, out.y_blocks, out.z_blocks) == (16, 8, 4)
+    return np.array([out.min_x, out.max_x, out.min_y, out.max_y, out.min_z, out.max_z], np.float32)
+
+
+# sizes around the 8-point lane step, the 65,536-point pieces and the
+# threaded split (from 262,144 points)
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 777, 65536, 65537, 300001, 1 << 20])
+def test_capi_bbox_matches_oracle(capi, oracle, n):
+    pts = np.random.RandomState(n).randn(n, 3).astype(np.float32) * 5
+    got = _capi_bbox(capi, pts)
+    assert got.tobytes() == oracle.bbox(pts).tobytes()
+    # the exact float32 extremes, widened by 1e-6 in float32
+    e = np.float32(1e-6)
+    want = np.array([pts[:, 0].min() - e, pts[:, 0].max() + e, pts[:, 1].min() - e,
+                     pts[:, 1].max() + e, pts[:, 2].min() - e, pts[:, 2].max() + e], np.float32)
+    assert got.tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("n", [9, 300001])
+def test_capi_bbox_nan_rules_match_the_running_pass(capi, oracle, n):
+    """A NaN at point 0 poisons its axis; a later NaN is skipped (the
+    reference's running compare-select from point 0)."""
+    base = np.random.RandomState(5).randn(n, 3).astype(np.float32)
+    for where in (0, n // 2, n - 1):
+        pts = base.copy()
+        pts[where, 1] = np.nan
+        got = _capi_bbox(capi, pts)
+        want = oracle.bbox(pts)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+        assert np.isnan(got[2]) == (where == 0)
 
 
 def test_capi_rejects_bad_arguments(capi):
