@@ -1,0 +1,78 @@
+"""Seeded sweep of cloud shapes, grids and ranges: the HIP path against the
+oracle (GPU), and the oracle against the reference library built from its
+own sources (CPU, where oracle/_ref is built).
+
+Shapes: uniform box, Gaussian, tight clusters, a flat plane (one axis
+constant), a line, an integer lattice (many equal distances), and clouds
+reaching outside the range (clamped into the boundary cells).  Grids mix
+powers of two (runs engine) with other block counts (tree engine), from 1 to
+64 blocks per axis.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+SHAPES = ["box", "gauss", "clusters", "plane", "line", "lattice", "outside"]
+
+
+def make_case(seed):
+    rs = np.random.RandomState(1000 + seed)
+    shape = SHAPES[seed % len(SHAPES)]
+    n = int(rs.randint(200, 40000))
+    if shape == "box":
+        p = rs.uniform(-1, 1, (n, 3))
+    elif shape == "gauss":
+        p = rs.randn(n, 3) * 0.4
+    elif shape == "clusters":
+        c = rs.uniform(-0.8, 0.8, (int(rs.randint(2, 30)), 3))
+        p = c[rs.randint(0, len(c), n)] + rs.randn(n, 3) * 0.02
+    elif shape == "plane":
+        p = rs.uniform(-1, 1, (n, 3))
+        p[:, rs.randint(0, 3)] = 0.25
+    elif shape == "line":
+        t = rs.uniform(-1, 1, n)
+        p = np.stack([t, 0.5 * t, -0.3 * t], 1)
+    elif shape == "lattice":
+        p = rs.randint(-6, 7, (n, 3)) / 6.0
+    else:  # outside: a third of the points beyond the range
+        p = rs.uniform(-1.5, 1.5, (n, 3))
+    p = np.ascontiguousarray(p, dtype=np.float32)
+    choices = [1, 2, 3, 4, 5, 7, 8, 12, 16, 20, 32, 64]
+    blocks = tuple(int(rs.choice(choices)) for _ in range(3))
+    if seed % 3 == 0:  # a power-of-two grid on every third case at least
+        blocks = tuple(int(rs.choice([1, 2, 4, 8, 16, 32, 64])) for _ in range(3))
+    m = int(rs.randint(1, n + 1)) if seed % 5 else int(rs.randint(1, min(n, 64) + 1))
+    rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks)
+    return shape, p, m, rng
+
+
+SEEDS = list(range(42))
+
+
+def _ids(seed):
+    shape, p, m, rng = make_case(seed)
+    return f"{seed}-{shape}-{len(p)}-{m}-{'x'.join(map(str, rng[6:]))}"
+
+
+@pytest.mark.parametrize("seed", SEEDS, ids=_ids)
+def test_oracle_matches_reference_on_sweep(oracle, seed):
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libyuezu_ref.so")
+    if not os.path.exists(ref_so):
+        pytest.skip("oracle/_ref not built (needs the reference sources)")
+    from oracle import Reference
+    shape, p, m, rng = make_case(seed)
+    assert np.array_equal(oracle.fps(p, m, rng), Reference(ref_so).fps(p, m, rng))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", SEEDS, ids=_ids)
+def test_gpu_matches_oracle_on_sweep(yf, oracle, seed):
+    shape, p, m, rng = make_case(seed)
+    got = yf.fps(p, m, yf.make_range(*rng))
+    want = oracle.fps(p, m, rng)
+    assert got.dtype == np.int32
+    assert np.array_equal(got, want), f"first difference at {np.argmax(got[:len(want)] != want[:len(got)])}"
