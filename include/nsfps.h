@@ -116,7 +116,8 @@ nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples,
 
 /* B independent clouds of n points each (xyz: B x n x 3, host).  ranges: B
  * ranges, or NULL for a per-cloud compute_bbox with blocks3 (NULL -> 16^3).
- * out: B x n_samples int32 (row b holds cloud b's samples); out_lens: B. */
+ * out: B x n_samples int32 (row b holds cloud b's samples; entries past
+ * out_lens[b] are unspecified); out_lens: B. */
 nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
                                uint64_t n_samples, const nsfps_range *ranges,
                                const uint32_t *blocks3, int32_t *out,

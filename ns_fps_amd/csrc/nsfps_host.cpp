@@ -354,7 +354,6 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.root_key = bp.take<uint64_t>(1);
   c.root_pos = bp.take<float4>(1);
   c.counter = bp.take<uint32_t>(1);
-  c.out = bp.take<int32_t>(p.m);
   c.prof = bp.take<uint64_t>(kProfWords);
   c.hist = bp.take<uint32_t>((size_t)kHists * kHistBins);
   c.pick_p = bp.take<float4>(kListCap);
@@ -430,6 +429,7 @@ struct CallBuffers {
   float *xyz_stage = nullptr;
   uint32_t *counts = nullptr, *small = nullptr, *bucket = nullptr, *fine = nullptr;
   BuildDev *bd = nullptr;  // per-cloud parameters of the many-cloud build steps
+  int32_t *out = nullptr;  // every cloud's samples, m entries per cloud
   size_t n_total = 0, counts_total = 0;
 };
 
@@ -447,7 +447,11 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   cb.bucket = bp.take<uint32_t>(cb.n_total);
   cb.fine = bp.take<uint32_t>(cb.n_total);
   cb.bd = bp.take<BuildDev>(plans.size());
-  size_t o_stage = 0, o_n = 0, o_c = 0;
+  // the clouds' outputs back to back, rows of m entries: one read-back
+  size_t outs = 0;
+  for (auto &p : plans) outs += p.m;
+  cb.out = bp.take<int32_t>(outs);
+  size_t o_stage = 0, o_n = 0, o_c = 0, o_out = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
     CloudPlan &p = plans[i];
     if (p.h_xyz) {
@@ -460,6 +464,8 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
     p.d_bucket = cb.bucket + o_n;
     p.d_fine = cb.fine + o_n;
     o_n += p.n;
+    p.dev.out = cb.out + o_out;
+    o_out += p.m;
   }
 }
 
@@ -862,12 +868,24 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   std::vector<uint32_t> lens(plans.size());
   for (size_t i = 0; i < plans.size(); ++i) lens[i] = fin[i].iter;
   uint64_t samples = 0;
+  uint32_t maxlen = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
     out_lens[i] = lens[i];
     samples += lens[i];
-    if (out_on_host && lens[i])
-      HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
+    maxlen = std::max(maxlen, lens[i]);
+  }
+  if (out_on_host && maxlen) {
+    if (plans.size() > 1 && out_stride == plans[0].m) {
+      // rows of m entries on both sides: one copy (entries past a cloud's
+      // length are left unspecified, as the interface says)
+      HIP_TRY(hipMemcpyAsync(h_out, cb.out, plans.size() * (size_t)out_stride * 4,
                              hipMemcpyDeviceToHost, st));
+    } else {
+      for (size_t i = 0; i < plans.size(); ++i)
+        if (lens[i])
+          HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
+                                 hipMemcpyDeviceToHost, st));
+    }
   }
   if (profile)
     HIP_TRY(hipMemcpyAsync(g_prof, plans[0].dev.prof, sizeof(g_prof), hipMemcpyDeviceToHost, st));
