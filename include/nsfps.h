@@ -19,6 +19,9 @@
  *   nsfps_fps_device     yuezu_fps() on device-resident input (cf. the
  *                        reference GPU driver's FpsGPU::sample,
  *                        eval/src_gpu/yuezu_fps_gpu.h:90-126)
+ *   nsfps_gather_points, nsfps_ball_query (and _device)
+ *                        no counterpart: the grouping step the reference's
+ *                        callers run on its output (see their declarations)
  */
 #ifndef NSFPS_H
 #define NSFPS_H
@@ -130,6 +133,32 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
 nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples,
                               const nsfps_range *range, int32_t *d_out,
                               uint64_t *out_len, void *stream);
+
+/* The step after sampling: set-abstraction grouping on the samples.  No
+ * counterpart in the reference, which stops at the indices; the next step of
+ * its callers is PointNet++'s sample-and-group (query_ball_point).
+ *
+ * nsfps_gather_points: out[i] = xyz[idx[i]], m x 3 float32.  An index outside
+ * [0, n) fails with NSFPS_EINVAL (checked on the host for host pointers; the
+ * device variant zeroes that row and reports it after the stream work).
+ *
+ * nsfps_ball_query: out is m x nsample int32; row j holds, in input order,
+ * the first nsample indices i whose ((dx*dx + dy*dy) + dz*dz) to center j is
+ * below radius*radius (float32, no contraction: the FPS distance); a row with
+ * fewer hits repeats its first hit, a row with none is all zeros.  radius
+ * must be finite and >= 0, nsample >= 1.
+ *
+ * The _device variants take device pointers and a hipStream_t (NULL = default
+ * stream) and return after the stream work completes. */
+nsfps_status nsfps_gather_points(const float *xyz, uint64_t n, const int32_t *idx, uint64_t m,
+                                 float *out);
+nsfps_status nsfps_gather_points_device(const float *d_xyz, uint64_t n, const int32_t *d_idx,
+                                        uint64_t m, float *d_out, void *stream);
+nsfps_status nsfps_ball_query(const float *xyz, uint64_t n, const float *centers, uint64_t m,
+                              float radius, uint32_t nsample, int32_t *out);
+nsfps_status nsfps_ball_query_device(const float *d_xyz, uint64_t n, const float *d_centers,
+                                     uint64_t m, float radius, uint32_t nsample, int32_t *d_out,
+                                     void *stream);
 
 /* Measurements of the last compute call made on this thread. */
 nsfps_status nsfps_get_stats(nsfps_stats *stats);

@@ -45,7 +45,8 @@ def module_path():
 
 
 def build_lib():
-    srcs = [os.path.join(CSRC, f) for f in ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_host.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_group.hip",
+                                             "nsfps_host.cpp")]
     tmp = LIB + ".tmp"
     _run([HIPCC, *DEVICE_FLAGS, "-shared", "-I", INCLUDE, "-I", CSRC, *srcs, "-o", tmp])
     os.replace(tmp, LIB)

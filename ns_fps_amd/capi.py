@@ -110,6 +110,35 @@ class Lib:
                                               ctypes.byref(n_out), _vp(stream)))
         return n_out.value
 
+    def gather_points(self, points, idx):
+        p = np.ascontiguousarray(points, dtype=np.float32)
+        ix = np.ascontiguousarray(idx, dtype=np.int32).ravel()
+        out = np.zeros((len(ix), 3), np.float32)
+        self._check(self.lib.nsfps_gather_points(p.ctypes.data_as(_vp), _u64(len(p)),
+                                                 ix.ctypes.data_as(_vp), _u64(len(ix)),
+                                                 out.ctypes.data_as(_vp)))
+        return out
+
+    def ball_query(self, points, centers, radius, nsample):
+        p = np.ascontiguousarray(points, dtype=np.float32)
+        c = np.ascontiguousarray(centers, dtype=np.float32)
+        out = np.zeros((len(c), int(nsample)), np.int32)
+        self._check(self.lib.nsfps_ball_query(p.ctypes.data_as(_vp), _u64(len(p)),
+                                              c.ctypes.data_as(_vp), _u64(len(c)),
+                                              ctypes.c_float(radius), ctypes.c_uint32(int(nsample)),
+                                              out.ctypes.data_as(_vp)))
+        return out
+
+    def gather_points_device(self, d_xyz, n, d_idx, m, d_out, stream=None):
+        self._check(self.lib.nsfps_gather_points_device(_vp(d_xyz), _u64(n), _vp(d_idx), _u64(m),
+                                                        _vp(d_out), _vp(stream)))
+
+    def ball_query_device(self, d_xyz, n, d_centers, m, radius, nsample, d_out, stream=None):
+        self._check(self.lib.nsfps_ball_query_device(_vp(d_xyz), _u64(n), _vp(d_centers), _u64(m),
+                                                     ctypes.c_float(radius),
+                                                     ctypes.c_uint32(int(nsample)), _vp(d_out),
+                                                     _vp(stream)))
+
     def stats(self):
         s = Stats()
         self._check(self.lib.nsfps_get_stats(ctypes.byref(s)))

@@ -1107,6 +1107,207 @@ nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords) {
   return NSFPS_OK;
 }
 
+// ------------------------------------------------------------ grouping ----
+
+namespace {
+
+nsfps_status check_group(uint64_t n, uint64_t m, uint64_t row) {
+  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+  if (m > 0xffffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^32-1 centers or indices");
+  if (row && m > ((uint64_t)1 << 40) / row) return fail(NSFPS_EUNSUPPORTED, "output too large");
+  return NSFPS_OK;
+}
+
+nsfps_status check_ball(float radius, uint32_t nsample) {
+  if (!std::isfinite(radius) || radius < 0.f)
+    return fail(NSFPS_EINVAL, "radius must be finite and >= 0");
+  if (nsample == 0) return fail(NSFPS_EINVAL, "nsample must be >= 1");
+  return NSFPS_OK;
+}
+
+// Workspace bytes in front of the grouping calls' buffers (the bad-index flag).
+constexpr size_t kGroupFlag = 256;
+
+}  // namespace
+
+nsfps_status nsfps_gather_points_device(const float *d_xyz, uint64_t n, const int32_t *d_idx,
+                                        uint64_t m, float *d_out, void *stream) {
+  if (m == 0) return NSFPS_OK;
+  if (!d_idx || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  nsfps_status rc = check_group(n, m, 0);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Arena *ap = nullptr;
+  rc = arena_for_device(&ap);
+  if (rc) return rc;
+  rc = arena_reserve(*ap, kGroupFlag);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t *d_bad = (uint32_t *)ap->base;
+  uint32_t bad = 0;
+  HIP_TRY(hipMemsetAsync(d_bad, 0, 4, st));
+  HIP_TRY(launch_gather_points(d_xyz, (uint32_t)n, d_idx, (uint32_t)m, d_out, d_bad, st));
+  HIP_TRY(hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (bad) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
+  return NSFPS_OK;
+}
+
+nsfps_status nsfps_gather_points(const float *xyz, uint64_t n, const int32_t *idx, uint64_t m,
+                                 float *out) {
+  if (m == 0) return NSFPS_OK;
+  if (!idx || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  nsfps_status rc = check_group(n, m, 0);
+  if (rc) return rc;
+  for (uint64_t i = 0; i < m; ++i)
+    if (idx[i] < 0 || (uint64_t)idx[i] >= n) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
+  std::lock_guard<std::mutex> lk(g_mu);
+  Arena *ap = nullptr;
+  rc = arena_for_device(&ap);
+  if (rc) return rc;
+  const size_t o_x = kGroupFlag, o_i = o_x + ((n * 12 + 255) & ~(size_t)255),
+               o_o = o_i + ((m * 4 + 255) & ~(size_t)255), total = o_o + m * 12;
+  rc = arena_reserve(*ap, total);
+  if (rc) return rc;
+  hipStream_t st = ap->stream;
+  char *b = ap->base;
+  if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(b + o_i, idx, m * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemsetAsync(b, 0, 4, st));
+  HIP_TRY(launch_gather_points((const float *)(b + o_x), (uint32_t)n, (const int32_t *)(b + o_i),
+                               (uint32_t)m, (float *)(b + o_o), (uint32_t *)b, st));
+  HIP_TRY(hipMemcpyAsync(out, b + o_o, m * 12, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
+namespace {
+
+// The ordered scan costs up to n * m distance tests; the grid's set-up (bounds,
+// a sort of the points, 16 MB of cell ranges) pays from about 2^26 of them.
+// NSFPS_BALL_QUERY=grid or =scan forces a path (diagnostics; results agree).
+bool bq_use_grid(uint64_t n, uint64_t m) {
+  const char *mode = getenv("NSFPS_BALL_QUERY");
+  if (mode && strcmp(mode, "grid") == 0) return n > 0;
+  if (mode && strcmp(mode, "scan") == 0) return false;
+  return n > 8192 && n * m > ((uint64_t)1 << 26);
+}
+
+size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace bytes of the grid path for n points and m centers.
+size_t bq_grid_bytes(uint64_t n, uint64_t m) {
+  const size_t cells = (size_t)kBqMaxDim * kBqMaxDim * kBqMaxDim;
+  const uint32_t hl = radix_hist_len((uint32_t)n);
+  return 3 * 256 + 4 * up256(n * 4) + up256(((size_t)hl + 16) * 4) +
+         up256(((size_t)scan_tmp_len(hl) + 16) * 4) + 2 * up256(cells * 4) + up256(n * 16) +
+         up256(m * 4);
+}
+
+// Ball query of device buffers on stream st; ws: bq_grid_bytes(n, m) of
+// workspace (unused for small clouds).
+nsfps_status ball_query_on(hipStream_t st, const float *xyz, uint64_t n, const float *centers,
+                           uint64_t m, float radius, uint32_t nsample, int32_t *out, char *ws) {
+  const float r2 = radius * radius;
+  if (n == 0 || !(r2 > 0.f)) {  // nothing lies closer than the radius: rows of zeros
+    HIP_TRY(hipMemsetAsync(out, 0, (size_t)m * nsample * 4, st));
+  } else if (!bq_use_grid(n, m)) {
+    HIP_TRY(launch_ball_query(xyz, (uint32_t)n, centers, nullptr, (uint32_t)m, r2, nsample, out,
+                              st));
+  } else {
+    const size_t cells = (size_t)kBqMaxDim * kBqMaxDim * kBqMaxDim;
+    const uint32_t hl = radix_hist_len((uint32_t)n);
+    char *b = ws;
+    auto take = [&](size_t bytes) {
+      char *p = b;
+      b += up256(bytes);
+      return p;
+    };
+    uint32_t *bnd = (uint32_t *)take(32);
+    BqGrid *grid = (BqGrid *)take(sizeof(BqGrid));
+    uint32_t *novf_d = (uint32_t *)take(4);
+    uint32_t *keys = (uint32_t *)take(n * 4), *vals = (uint32_t *)take(n * 4);
+    uint32_t *keys2 = (uint32_t *)take(n * 4), *vals2 = (uint32_t *)take(n * 4);
+    uint32_t *hist = (uint32_t *)take(((size_t)hl + 16) * 4);
+    uint32_t *scan = (uint32_t *)take(((size_t)scan_tmp_len(hl) + 16) * 4);
+    uint32_t *cstart = (uint32_t *)take(cells * 4), *cend = (uint32_t *)take(cells * 4);
+    float4 *spts = (float4 *)take(n * 16);
+    uint32_t *ovf = (uint32_t *)take(m * 4);
+    HIP_TRY(hipMemsetAsync(bnd, 0xff, 12, st));
+    HIP_TRY(hipMemsetAsync(bnd + 3, 0, 12, st));
+    HIP_TRY(hipMemsetAsync(novf_d, 0, 4, st));
+    HIP_TRY(hipMemsetAsync(cstart, 0, cells * 4, st));
+    HIP_TRY(hipMemsetAsync(cend, 0, cells * 4, st));
+    HIP_TRY(launch_bq_grid_build(xyz, (uint32_t)n, radius, bnd, grid, keys, st));
+    uint32_t *sk = nullptr, *sv = nullptr;
+    HIP_TRY(launch_radix_sort(keys, vals, keys2, vals2, (uint32_t)n, 22, hist, scan, true, &sk,
+                              &sv, st));
+    HIP_TRY(launch_bq_cells(sk, sv, (uint32_t)n, xyz, grid, cstart, cend, spts, st));
+    HIP_TRY(launch_bq_query(spts, grid, cstart, cend, centers, (uint32_t)m, r2, nsample, out, ovf,
+                            novf_d, st));
+    uint32_t novf = 0;
+    HIP_TRY(hipMemcpyAsync(&novf, novf_d, 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    if (novf > m) return fail(NSFPS_EDEVICE, "internal: %u ball-query overflows for %llu centers",
+                              novf, (unsigned long long)m);
+    if (novf)
+      HIP_TRY(launch_ball_query(xyz, (uint32_t)n, centers, ovf, novf, r2, nsample, out, st));
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
+}  // namespace
+
+nsfps_status nsfps_ball_query_device(const float *d_xyz, uint64_t n, const float *d_centers,
+                                     uint64_t m, float radius, uint32_t nsample, int32_t *d_out,
+                                     void *stream) {
+  nsfps_status rc = check_ball(radius, nsample);
+  if (rc) return rc;
+  if (m == 0) return NSFPS_OK;
+  if (!d_centers || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  rc = check_group(n, m, nsample);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Arena *ap = nullptr;
+  rc = arena_for_device(&ap);
+  if (rc) return rc;
+  if (bq_use_grid(n, m)) {
+    rc = arena_reserve(*ap, bq_grid_bytes(n, m));
+    if (rc) return rc;
+  }
+  return ball_query_on((hipStream_t)stream, d_xyz, n, d_centers, m, radius, nsample, d_out,
+                       ap->base);
+}
+
+nsfps_status nsfps_ball_query(const float *xyz, uint64_t n, const float *centers, uint64_t m,
+                              float radius, uint32_t nsample, int32_t *out) {
+  nsfps_status rc = check_ball(radius, nsample);
+  if (rc) return rc;
+  if (m == 0) return NSFPS_OK;
+  if (!centers || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  rc = check_group(n, m, nsample);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Arena *ap = nullptr;
+  rc = arena_for_device(&ap);
+  if (rc) return rc;
+  const size_t o_x = 0, o_c = o_x + up256(n * 12), o_o = o_c + up256(m * 12),
+               o_w = o_o + up256(m * (size_t)nsample * 4);
+  rc = arena_reserve(*ap, o_w + (bq_use_grid(n, m) ? bq_grid_bytes(n, m) : 0));
+  if (rc) return rc;
+  hipStream_t st = ap->stream;
+  char *b = ap->base;
+  if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(b + o_c, centers, m * 12, hipMemcpyHostToDevice, st));
+  rc = ball_query_on(st, (const float *)(b + o_x), n, (const float *)(b + o_c), m, radius, nsample,
+                     (int32_t *)(b + o_o), b + o_w);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(out, b + o_o, m * (size_t)nsample * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return NSFPS_OK;
+}
+
 nsfps_status nsfps_get_stats(nsfps_stats *stats) {
   if (!stats) return fail(NSFPS_EINVAL, "null pointer");
   *stats = g_stats;

@@ -1,5 +1,5 @@
-// Kernel launchers (defined in nsfps_build.hip / nsfps_sample.hip, called by
-// nsfps_host.cpp).
+// Kernel launchers (defined in nsfps_build.hip, nsfps_sample.hip,
+// nsfps_runs.hip and nsfps_group.hip; called by nsfps_host.cpp).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -81,5 +81,34 @@ constexpr uint32_t kProfWords = 24;
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, hipStream_t st);
+
+// grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
+// for an index outside [0, n), whose row is zeroed); ball query rows of
+// nsample indices by the ordered scan (ids: the centers to do, or null for
+// 0 .. m - 1) or by the grid: build (bnd preset to 3 x 0xffffffff, 3 x 0),
+// stable sort of keys by the caller, cells (cstart/cend zeroed, kBqMaxDim^3
+// words each), query (centers with more than the hit capacity are listed in
+// ovf_ids / ovf_count for the scan)
+constexpr uint32_t kBqMaxDim = 128;
+struct BqGrid {
+  float mn[3];
+  float inv_cs[3];
+  uint32_t dim[3];
+  uint32_t ncells;
+};
+hipError_t launch_gather_points(const float *xyz, uint32_t n, const int32_t *idx, uint32_t m,
+                                float *out, uint32_t *bad, hipStream_t st);
+hipError_t launch_ball_query(const float *xyz, uint32_t n, const float *centers,
+                             const uint32_t *ids, uint32_t m, float r2, uint32_t nsample,
+                             int32_t *out, hipStream_t st);
+hipError_t launch_bq_grid_build(const float *xyz, uint32_t n, float radius, uint32_t *bnd,
+                                BqGrid *grid, uint32_t *keys, hipStream_t st);
+hipError_t launch_bq_cells(const uint32_t *skeys, const uint32_t *sidx, uint32_t n,
+                           const float *xyz, const BqGrid *grid, uint32_t *cstart, uint32_t *cend,
+                           float4 *spts, hipStream_t st);
+hipError_t launch_bq_query(const float4 *spts, const BqGrid *grid, const uint32_t *cstart,
+                           const uint32_t *cend, const float *centers, uint32_t m, float r2,
+                           uint32_t nsample, int32_t *out, uint32_t *ovf_ids,
+                           uint32_t *ovf_count, hipStream_t st);
 
 }  // namespace nsfps

@@ -222,6 +222,40 @@ py::tuple fps_batched_py(py::handle points, uint64_t n_samples, py::object range
   return py::make_tuple(out, lens);
 }
 
+// The grouping step after sampling (no counterpart in the reference):
+// gather_points(points (N, 3), idx (M,)) -> (M, 3) float32;
+// ball_query(points (N, 3), centers (M, 3), radius, nsample) -> (M, nsample) int32.
+py::array_t<float> gather_points_py(py::handle points, py::handle idx) {
+  FArray p = as_points(points);
+  auto ia = py::array_t<int32_t, py::array::c_style | py::array::forcecast>::ensure(idx);
+  if (!ia) raise_input("indices must be convertible to an int32 array");
+  if (ia.ndim() != 1) raise_input("indices must be one-dimensional");
+  const uint64_t n = (uint64_t)p.shape(0), m = (uint64_t)ia.shape(0);
+  py::array_t<float> out({(py::ssize_t)m, (py::ssize_t)3});
+  nsfps_status s;
+  {
+    py::gil_scoped_release nogil;
+    s = nsfps_gather_points(p.data(), n, ia.data(), m, out.mutable_data());
+  }
+  if (s != NSFPS_OK) raise_status(s);
+  return out;
+}
+
+py::array_t<int32_t> ball_query_py(py::handle points, py::handle centers, float radius,
+                                   uint32_t nsample) {
+  FArray p = as_points(points);
+  FArray c = as_points(centers);
+  const uint64_t n = (uint64_t)p.shape(0), m = (uint64_t)c.shape(0);
+  py::array_t<int32_t> out({(py::ssize_t)m, (py::ssize_t)nsample});
+  nsfps_status s;
+  {
+    py::gil_scoped_release nogil;
+    s = nsfps_ball_query(p.data(), n, c.data(), m, radius, nsample, out.mutable_data());
+  }
+  if (s != NSFPS_OK) raise_status(s);
+  return out;
+}
+
 py::dict last_stats_py() {
   nsfps_stats s{};
   nsfps_get_stats(&s);
@@ -305,6 +339,9 @@ PYBIND11_MODULE(yuezu_fps_module, m) {
         py::arg("range") = py::none(), py::arg("x_blocks") = NSFPS_DEFAULT_X_BLOCKS,
         py::arg("y_blocks") = NSFPS_DEFAULT_Y_BLOCKS, py::arg("z_blocks") = NSFPS_DEFAULT_Z_BLOCKS);
 
+  m.def("gather_points", &gather_points_py, py::arg("points"), py::arg("idx"));
+  m.def("ball_query", &ball_query_py, py::arg("points"), py::arg("centers"), py::arg("radius"),
+        py::arg("nsample"));
   m.def("last_stats", &last_stats_py);
   m.def("last_loop_profile", []() {
     std::vector<uint64_t> w(24, 0);

@@ -534,3 +534,39 @@ int orc_fps_naive_mt(const float *xyz, uint64_t n, uint64_t m, int32_t *out,
   free(C);
   return 0;
 }
+
+/* ---- grouping after sampling: a literal scan per center ------------------ */
+
+int orc_gather_points(const float *xyz, uint64_t n, const int32_t *idx, uint64_t m,
+                      float *out) {
+  int bad = 0;
+  for (uint64_t i = 0; i < m; ++i) {
+    if (idx[i] < 0 || (uint64_t)idx[i] >= n) {
+      bad = 1;
+      continue;
+    }
+    for (int a = 0; a < 3; ++a) out[3 * i + a] = xyz[3 * (uint64_t)idx[i] + a];
+  }
+  return bad;
+}
+
+int orc_ball_query(const float *xyz, uint64_t n, const float *centers, uint64_t m,
+                   float r2, uint32_t nsample, int32_t *out) {
+  for (uint64_t j = 0; j < m; ++j) {
+    int32_t *row = out + j * nsample;
+    uint32_t cnt = 0;
+    for (uint32_t k = 0; k < nsample; ++k) row[k] = 0;
+    for (uint64_t i = 0; i < n && cnt < nsample; ++i) {
+      const float *p = xyz + 3 * i, *c = centers + 3 * j;
+      float dx = p[0] - c[0], dy = p[1] - c[1], dz = p[2] - c[2];
+      float s = dx * dx + dy * dy;
+      float d2 = s + dz * dz;
+      if (d2 < r2) {
+        if (cnt == 0)
+          for (uint32_t k = 0; k < nsample; ++k) row[k] = (int32_t)i;
+        row[cnt++] = (int32_t)i;
+      }
+    }
+  }
+  return 0;
+}

@@ -88,6 +88,17 @@ int orc_fps_naive_mt(const float *xyz, uint64_t n, uint64_t m, int32_t *out,
 /* OpenMP threads orc_fps_naive_mt uses for threads = 0. */
 int orc_max_threads(void);
 
+/* Grouping after sampling (no counterpart in the reference; PointNet++'s
+ * query_ball_point on the FPS distance).  orc_gather_points: out[i] =
+ * xyz[idx[i]]; returns 1 if an index lies outside [0, n) (nothing written
+ * for it).  orc_ball_query: row j of out (m x nsample) holds the first
+ * nsample indices i, in input order, with sqdist(p_i, c_j) < r2; fewer hits
+ * repeat the first hit, none gives zeros. */
+int orc_gather_points(const float *xyz, uint64_t n, const int32_t *idx, uint64_t m,
+                      float *out);
+int orc_ball_query(const float *xyz, uint64_t n, const float *centers, uint64_t m,
+                   float r2, uint32_t nsample, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

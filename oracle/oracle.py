@@ -169,6 +169,26 @@ class Oracle:
         return int(self.lib.orc_max_threads())
 
 
+def gather_points(orc, points, idx):
+    """orc_gather_points: (M, 3) float32; ValueError for an index outside [0, N)."""
+    p = _pts(points)
+    ix = np.ascontiguousarray(idx, dtype=np.int32).ravel()
+    out = np.zeros((len(ix), 3), np.float32)
+    if orc.lib.orc_gather_points(_ptr(p), _u64(len(p)), _ptr(ix), _u64(len(ix)), _ptr(out)):
+        raise ValueError("index outside the cloud")
+    return out
+
+
+def ball_query(orc, points, centers, radius, nsample):
+    """orc_ball_query with r2 = radius * radius in float32: (M, nsample) int32."""
+    p, c = _pts(points), _pts(centers)
+    r = np.float32(radius)
+    out = np.zeros((len(c), int(nsample)), np.int32)
+    orc.lib.orc_ball_query(_ptr(p), _u64(len(p)), _ptr(c), _u64(len(c)),
+                           ctypes.c_float(float(r * r)), ctypes.c_uint32(int(nsample)), _ptr(out))
+    return out
+
+
 class Reference:
     """The reference library built from its own sources (oracle/_ref)."""
 
