@@ -178,6 +178,38 @@ def cpu_baseline(w, budget_s=30.0):
     return base
 
 
+def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
+    """The grouping step after FPS on the uniform cube: 65,536 FPS centers,
+    ball query on device-resident buffers; 256 rows checked against the
+    oracle's scan."""
+    from ns_fps_amd.workloads import make_workload
+    w = make_workload("uniform_cube")
+    P = w["clouds"][0]
+    idx = lib.fps(P, int(w["n_samples"]), w["range"])
+    C = np.ascontiguousarray(P[idx])
+    d_p, d_c = hip.upload(P), hip.upload(C)
+    d_o = hip.malloc(len(C) * nsample * 4)
+    try:
+        lib.ball_query_device(d_p, len(P), d_c, len(C), radius, nsample, d_o)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            lib.ball_query_device(d_p, len(P), d_c, len(C), radius, nsample, d_o)
+        t1 = time.perf_counter()
+        out = hip.download(d_o, len(C) * nsample, np.int32).reshape(len(C), nsample)
+    finally:
+        for b in (d_p, d_c, d_o):
+            hip.free(b)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, ball_query
+    rows = np.linspace(0, len(C) - 1, 256).astype(np.int64)
+    exact = bool(np.array_equal(out[rows], ball_query(Oracle(), P, C[rows], radius, nsample)))
+    ms = (t1 - t0) * 1e3 / steps
+    return {"workload": "ball_query_uniform_cube", "points": len(P), "centers": len(C),
+            "radius": radius, "nsample": nsample, "ms_per_call": round(ms, 3),
+            "centers_per_s": round(len(C) / (ms / 1e3), 1), "rows_checked_vs_oracle": len(rows),
+            "exact": exact}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,6 +218,8 @@ def main():
     ap.add_argument("--workload", default="uniform_cube")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also print a line per workload")
+    ap.add_argument("--ball-query", action="store_true",
+                    help="time only the grouping step after FPS (ball query) and print its line")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device (a copy kernel of known size for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -212,6 +246,10 @@ def main():
         hip.synchronize()
         hip.free(src)
         hip.free(dst)
+
+    if args.ball_query:
+        print(json.dumps(run_ball_query(lib, hip, args.steps)), flush=True)
+        return
 
     if args.all:
         for wname in ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]:

@@ -114,13 +114,25 @@ __global__ __launch_bounds__(256) void k_bq_bounds(const float *__restrict__ xyz
       }
     }
   }
+  // one atomic per value and workgroup: the six addresses are shared by the
+  // whole grid, and contended atomics on one address serialise
+  __shared__ uint32_t s_b[4][6];
+  const uint32_t wave = threadIdx.x >> 6;
 #pragma unroll
   for (int a = 0; a < 3; ++a) {
     const uint32_t l = wave_min_u32(lo[a]), h = wave_max_u32(hi[a]);
     if ((threadIdx.x & 63u) == 0) {
-      atomicMin(&bnd[a], l);
-      atomicMax(&bnd[3 + a], h);
+      s_b[wave][a] = l;
+      s_b[wave][3 + a] = h;
     }
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const uint32_t a = threadIdx.x;
+    uint32_t v = s_b[0][a];
+    for (uint32_t w = 1; w < 4; ++w) v = a < 3 ? min(v, s_b[w][a]) : max(v, s_b[w][a]);
+    if (a < 3) atomicMin(&bnd[a], v);
+    else atomicMax(&bnd[a], v);
   }
 }
 
@@ -289,8 +301,8 @@ hipError_t launch_ball_query(const float *xyz, uint32_t n, const float *centers,
 
 hipError_t launch_bq_grid_build(const float *xyz, uint32_t n, float radius, uint32_t *bnd,
                                 BqGrid *grid, uint32_t *keys, hipStream_t st) {
-  const uint32_t nb = std::min<uint32_t>((n + 255) / 256, 1024);
-  k_bq_bounds<<<nb, 256, 0, st>>>(xyz, n, bnd);
+  const uint32_t nb = std::min<uint32_t>((n + 255) / 256, 512);
+  k_bq_bounds<<<nb, 256, 0, st>>>(xyz, n, bnd);  // 256 threads: four waves (s_b)
   k_bq_grid<<<1, 64, 0, st>>>(bnd, radius, grid);
   k_bq_keys<<<(n + 255) / 256, 256, 0, st>>>(xyz, n, grid, keys);
   return hipGetLastError();
