@@ -218,36 +218,40 @@ __global__ __launch_bounds__(256) void k_bq_query(const float4 *__restrict__ spt
   const int gx = (int)bq_axis(g, 0, cx), gy = (int)bq_axis(g, 1, cy), gz = (int)bq_axis(g, 2, cz);
   uint32_t *const hits = s_hits[wave];
   uint32_t *const runs = s_runs[wave];
+  // the 27 cells' ranges, read at once: lane l < 27 takes cell offset
+  // (l % 3 - 1, l / 3 % 3 - 1, l / 9 - 1)
+  uint32_t cb = 0, ce = 0;
+  if (lane < 27) {
+    const int x = gx + (int)(lane % 3) - 1, y = gy + (int)(lane / 3 % 3) - 1,
+              z = gz + (int)(lane / 9) - 1;
+    if (x >= 0 && x < (int)g.dim[0] && y >= 0 && y < (int)g.dim[1] && z >= 0 &&
+        z < (int)g.dim[2]) {
+      const uint32_t cell = ((uint32_t)z * g.dim[1] + (uint32_t)y) * g.dim[0] + (uint32_t)x;
+      cb = cstart[cell];
+      ce = cend[cell];
+    }
+  }
+  uint64_t cells = __ballot(cb < ce);
   uint32_t cnt = 0, nruns = 0;
-  for (int dz = -1; dz <= 1; ++dz) {
-    const int z = gz + dz;
-    if (z < 0 || z >= (int)g.dim[2]) continue;
-    for (int dy = -1; dy <= 1; ++dy) {
-      const int y = gy + dy;
-      if (y < 0 || y >= (int)g.dim[1]) continue;
-      for (int dx = -1; dx <= 1; ++dx) {
-        const int x = gx + dx;
-        if (x < 0 || x >= (int)g.dim[0]) continue;
-        const uint32_t cell = ((uint32_t)z * g.dim[1] + (uint32_t)y) * g.dim[0] + (uint32_t)x;
-        const uint32_t b = cstart[cell], e = cend[cell];
-        if (b >= e) continue;
-        if (lane == 0) runs[nruns] = cnt;  // this cell's hits start a run
-        ++nruns;
-        for (uint32_t s = b; s < e; s += 64) {
-          const uint32_t i = s + lane;
-          bool hit = false;
-          uint32_t idx = 0;
-          if (i < e) {
-            const float4 q = spts[i];
-            hit = sqdist(q.x, q.y, q.z, cx, cy, cz) < r2;
-            idx = __float_as_uint(q.w);
-          }
-          const uint64_t mask = __ballot(hit);
-          const uint32_t pos = cnt + lanes_below(mask);
-          if (hit && pos < kBqCap) hits[pos] = idx;
-          cnt += (uint32_t)__popcll(mask);
-        }
+  while (cells) {
+    const uint32_t l = (uint32_t)__builtin_ctzll(cells);
+    cells &= cells - 1;
+    const uint32_t b = rdlane(cb, l), e = rdlane(ce, l);
+    if (lane == 0) runs[nruns] = cnt;  // this cell's hits start a run
+    ++nruns;
+    for (uint32_t s = b; s < e; s += 64) {
+      const uint32_t i = s + lane;
+      bool hit = false;
+      uint32_t idx = 0;
+      if (i < e) {
+        const float4 q = spts[i];
+        hit = sqdist(q.x, q.y, q.z, cx, cy, cz) < r2;
+        idx = __float_as_uint(q.w);
       }
+      const uint64_t mask = __ballot(hit);
+      const uint32_t pos = cnt + lanes_below(mask);
+      if (hit && pos < kBqCap) hits[pos] = idx;
+      cnt += (uint32_t)__popcll(mask);
     }
   }
   int32_t *const row = out + (size_t)j * nsample;
