@@ -16,7 +16,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <mutex>
+#include <new>
 #include <string>
 #include <thread>
 #include <vector>
@@ -192,10 +194,17 @@ void bboxes(const float *xyz, uint64_t count, uint64_t n, nsfps_range *ranges) {
     for (uint64_t q = 0; q < pieces; ++q) run(q);
   } else {
     std::vector<std::thread> th;
-    for (uint64_t t = 0; t < nt; ++t)
-      th.emplace_back([&, t] {
-        for (uint64_t q = t; q < pieces; q += nt) run(q);
-      });
+    uint64_t started = 0;
+    try {  // a thread that cannot be started leaves its share to this one
+      th.reserve(nt);
+      for (; started < nt; ++started)
+        th.emplace_back([&, t = started] {
+          for (uint64_t q = t; q < pieces; q += nt) run(q);
+        });
+    } catch (...) {
+    }
+    for (uint64_t t = started; t < nt; ++t)
+      for (uint64_t q = t; q < pieces; q += nt) run(q);
     for (auto &x : th) x.join();
   }
   for (uint64_t b = 0; b < count; ++b) {
@@ -938,6 +947,25 @@ void reset_stats() { memset(&g_stats, 0, sizeof(g_stats)); }
 
 using namespace nsfps;
 
+namespace {
+
+// No C++ exception crosses the C ABI: host allocation failures and any other
+// exception become a status with a message.
+template <class F>
+nsfps_status guarded(F &&f) {
+  try {
+    return f();
+  } catch (const std::bad_alloc &) {
+    return fail(NSFPS_ENOMEM, "host allocation failed");
+  } catch (const std::exception &e) {
+    return fail(NSFPS_EDEVICE, "internal error: %s", e.what());
+  } catch (...) {
+    return fail(NSFPS_EDEVICE, "internal error");
+  }
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *nsfps_last_error(void) { return g_err.c_str(); }
@@ -952,34 +980,38 @@ int nsfps_device_count(void) {
 
 nsfps_status nsfps_range_derive(const nsfps_range *range, nsfps_range_info *info, uint32_t *luts,
                                 uint64_t lut_cap) {
-  if (!range || !info) return fail(NSFPS_EINVAL, "range and info must be non-NULL");
-  const uint32_t bl[3] = {range->x_blocks, range->y_blocks, range->z_blocks};
-  for (uint32_t v : bl)
-    if (v == 0 || v > (1u << 20)) return fail(NSFPS_EINVAL, "block counts must be in [1, 2^20]");
-  HostRange h;
-  derive(*range, h);
-  *info = h.info;
-  if (luts) {
-    uint64_t need = h.lut[0].size() + h.lut[1].size() + h.lut[2].size();
-    if (need > lut_cap) return fail(NSFPS_EINVAL, "lut buffer too small (%llu needed)",
-                                    (unsigned long long)need);
-    uint64_t o = 0;
-    for (int a = 0; a < 3; ++a)
-      for (uint32_t v : h.lut[a]) luts[o++] = v;
-  }
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (!range || !info) return fail(NSFPS_EINVAL, "range and info must be non-NULL");
+    const uint32_t bl[3] = {range->x_blocks, range->y_blocks, range->z_blocks};
+    for (uint32_t v : bl)
+      if (v == 0 || v > (1u << 20)) return fail(NSFPS_EINVAL, "block counts must be in [1, 2^20]");
+    HostRange h;
+    derive(*range, h);
+    *info = h.info;
+    if (luts) {
+      uint64_t need = h.lut[0].size() + h.lut[1].size() + h.lut[2].size();
+      if (need > lut_cap) return fail(NSFPS_EINVAL, "lut buffer too small (%llu needed)",
+                                      (unsigned long long)need);
+      uint64_t o = 0;
+      for (int a = 0; a < 3; ++a)
+        for (uint32_t v : h.lut[a]) luts[o++] = v;
+    }
+    return NSFPS_OK;
+  });
 }
 
 nsfps_status nsfps_bbox(const float *xyz, uint64_t n, uint32_t xb, uint32_t yb, uint32_t zb,
                         nsfps_range *out) {
-  if (!out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  bbox_of(xyz, n, *out);
-  if (n) {
-    out->x_blocks = xb;
-    out->y_blocks = yb;
-    out->z_blocks = zb;
-  }
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (!out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    bbox_of(xyz, n, *out);
+    if (n) {
+      out->x_blocks = xb;
+      out->y_blocks = yb;
+      out->z_blocks = zb;
+    }
+    return NSFPS_OK;
+  });
 }
 
 static nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m,
@@ -1003,108 +1035,118 @@ static nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m,
 
 nsfps_status nsfps_fps(const float *xyz, uint64_t n, uint64_t n_samples, const nsfps_range *range,
                        int32_t *out, uint64_t *out_len) {
-  nsfps_range r;
-  if (range) {
-    r = *range;
-  } else {
-    if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
-    bbox_of(xyz, n, r);
-    if (n) r.x_blocks = r.y_blocks = r.z_blocks = NSFPS_DEFAULT_X_BLOCKS;
-  }
-  return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+  return guarded([&]() -> nsfps_status {
+    nsfps_range r;
+    if (range) {
+      r = *range;
+    } else {
+      if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
+      bbox_of(xyz, n, r);
+      if (n) r.x_blocks = r.y_blocks = r.z_blocks = NSFPS_DEFAULT_X_BLOCKS;
+    }
+    return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+  });
 }
 
 nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples, uint32_t xb,
                             uint32_t yb, uint32_t zb, int32_t *out, uint64_t *out_len) {
-  if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
-  nsfps_range r;
-  bbox_of(xyz, n, r);
-  if (n) {
-    r.x_blocks = xb;
-    r.y_blocks = yb;
-    r.z_blocks = zb;
-  }
-  return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+  return guarded([&]() -> nsfps_status {
+    if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
+    nsfps_range r;
+    bbox_of(xyz, n, r);
+    if (n) {
+      r.x_blocks = xb;
+      r.y_blocks = yb;
+      r.z_blocks = zb;
+    }
+    return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+  });
 }
 
 nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n, uint64_t m,
                                const nsfps_range *ranges, const uint32_t *blocks3, int32_t *out,
                                uint64_t *out_lens) {
-  reset_stats();
-  if (batch == 0) return NSFPS_OK;
-  if (!out_lens || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
-  if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
-  std::vector<nsfps_range> rs(batch);
-  if (!ranges) bboxes(xyz, batch, n, rs.data());
-  for (uint64_t b = 0; b < batch; ++b) {
-    if (ranges) {
-      rs[b] = ranges[b];
-    } else if (n) {
-      rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
-      rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
-      rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (batch == 0) return NSFPS_OK;
+    if (!out_lens || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+    if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
+    std::vector<nsfps_range> rs(batch);
+    if (!ranges) bboxes(xyz, batch, n, rs.data());
+    for (uint64_t b = 0; b < batch; ++b) {
+      if (ranges) {
+        rs[b] = ranges[b];
+      } else if (n) {
+        rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
+        rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
+        rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
+      }
+      nsfps_status rc = check_range(rs[b]);
+      if (rc) return rc;
     }
-    nsfps_status rc = check_range(rs[b]);
-    if (rc) return rc;
-  }
-  bool all_trivial = true;
-  for (uint64_t b = 0; b < batch; ++b) {
-    uint64_t len = 0;
-    if (!trivial(n, m, out + b * m, &len)) {
-      all_trivial = false;
-      break;
+    bool all_trivial = true;
+    for (uint64_t b = 0; b < batch; ++b) {
+      uint64_t len = 0;
+      if (!trivial(n, m, out + b * m, &len)) {
+        all_trivial = false;
+        break;
+      }
+      out_lens[b] = len;
     }
-    out_lens[b] = len;
-  }
-  if (all_trivial) return NSFPS_OK;
-  std::lock_guard<std::mutex> lk(g_mu);
-  std::vector<CloudPlan> plans(batch);
-  for (uint64_t b = 0; b < batch; ++b) {
-    plans[b].n = (uint32_t)n;
-    plans[b].m = (uint32_t)m;
-    derive(rs[b], plans[b].rng);
-    plans[b].h_xyz = xyz + b * n * 3;
-  }
-  return run_clouds(plans, nullptr, true, out, m, out_lens);
+    if (all_trivial) return NSFPS_OK;
+    std::lock_guard<std::mutex> lk(g_mu);
+    std::vector<CloudPlan> plans(batch);
+    for (uint64_t b = 0; b < batch; ++b) {
+      plans[b].n = (uint32_t)n;
+      plans[b].m = (uint32_t)m;
+      derive(rs[b], plans[b].rng);
+      plans[b].h_xyz = xyz + b * n * 3;
+    }
+    return run_clouds(plans, nullptr, true, out, m, out_lens);
+  });
 }
 
 nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const nsfps_range *range,
                               int32_t *d_out, uint64_t *out_len, void *stream) {
-  reset_stats();
-  if (!range || !out_len || (m && !d_out) || (n && !d_xyz))
-    return fail(NSFPS_EINVAL, "null pointer");
-  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
-  nsfps_status rc = check_range(*range);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  hipStream_t st = (hipStream_t)stream;
-  if (n == 0 || m == 0 || m >= n || m == 1) {
-    std::vector<int32_t> tmp((size_t)std::min<uint64_t>(std::max<uint64_t>(n, 1), m ? m : 1));
-    trivial(n, m, tmp.data(), out_len);
-    if (*out_len) {
-      HIP_TRY(hipMemcpyAsync(d_out, tmp.data(), *out_len * 4, hipMemcpyHostToDevice, st));
-      HIP_TRY(hipStreamSynchronize(st));
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (!range || !out_len || (m && !d_out) || (n && !d_xyz))
+      return fail(NSFPS_EINVAL, "null pointer");
+    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+    nsfps_status rc = check_range(*range);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    hipStream_t st = (hipStream_t)stream;
+    if (n == 0 || m == 0 || m >= n || m == 1) {
+      std::vector<int32_t> tmp((size_t)std::min<uint64_t>(std::max<uint64_t>(n, 1), m ? m : 1));
+      trivial(n, m, tmp.data(), out_len);
+      if (*out_len) {
+        HIP_TRY(hipMemcpyAsync(d_out, tmp.data(), *out_len * 4, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipStreamSynchronize(st));
+      }
+      return NSFPS_OK;
     }
+    std::vector<CloudPlan> plans(1);
+    CloudPlan &p = plans[0];
+    p.n = (uint32_t)n;
+    p.m = (uint32_t)m;
+    derive(*range, p.rng);
+    p.d_xyz_in = d_xyz;
+    rc = run_clouds(plans, st, false, nullptr, 0, out_len);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
     return NSFPS_OK;
-  }
-  std::vector<CloudPlan> plans(1);
-  CloudPlan &p = plans[0];
-  p.n = (uint32_t)n;
-  p.m = (uint32_t)m;
-  derive(*range, p.rng);
-  p.d_xyz_in = d_xyz;
-  rc = run_clouds(plans, st, false, nullptr, 0, out_len);
-  if (rc) return rc;
-  HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return NSFPS_OK;
+  });
 }
 
 nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords) {
-  if (!words) return fail(NSFPS_EINVAL, "null pointer");
-  for (uint32_t i = 0; i < nwords; ++i) words[i] = i < kProfWords ? g_prof[i] : 0;
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (!words) return fail(NSFPS_EINVAL, "null pointer");
+    for (uint32_t i = 0; i < nwords; ++i) words[i] = i < kProfWords ? g_prof[i] : 0;
+    return NSFPS_OK;
+  });
 }
 
 // ------------------------------------------------------------ grouping ----
@@ -1132,53 +1174,57 @@ constexpr size_t kGroupFlag = 256;
 
 nsfps_status nsfps_gather_points_device(const float *d_xyz, uint64_t n, const int32_t *d_idx,
                                         uint64_t m, float *d_out, void *stream) {
-  if (m == 0) return NSFPS_OK;
-  if (!d_idx || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  nsfps_status rc = check_group(n, m, 0);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  Arena *ap = nullptr;
-  rc = arena_for_device(&ap);
-  if (rc) return rc;
-  rc = arena_reserve(*ap, kGroupFlag);
-  if (rc) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  uint32_t *d_bad = (uint32_t *)ap->base;
-  uint32_t bad = 0;
-  HIP_TRY(hipMemsetAsync(d_bad, 0, 4, st));
-  HIP_TRY(launch_gather_points(d_xyz, (uint32_t)n, d_idx, (uint32_t)m, d_out, d_bad, st));
-  HIP_TRY(hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  if (bad) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (m == 0) return NSFPS_OK;
+    if (!d_idx || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    nsfps_status rc = check_group(n, m, 0);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    rc = arena_for_device(&ap);
+    if (rc) return rc;
+    rc = arena_reserve(*ap, kGroupFlag);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t *d_bad = (uint32_t *)ap->base;
+    uint32_t bad = 0;
+    HIP_TRY(hipMemsetAsync(d_bad, 0, 4, st));
+    HIP_TRY(launch_gather_points(d_xyz, (uint32_t)n, d_idx, (uint32_t)m, d_out, d_bad, st));
+    HIP_TRY(hipMemcpyAsync(&bad, d_bad, 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    if (bad) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
+    return NSFPS_OK;
+  });
 }
 
 nsfps_status nsfps_gather_points(const float *xyz, uint64_t n, const int32_t *idx, uint64_t m,
                                  float *out) {
-  if (m == 0) return NSFPS_OK;
-  if (!idx || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  nsfps_status rc = check_group(n, m, 0);
-  if (rc) return rc;
-  for (uint64_t i = 0; i < m; ++i)
-    if (idx[i] < 0 || (uint64_t)idx[i] >= n) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
-  std::lock_guard<std::mutex> lk(g_mu);
-  Arena *ap = nullptr;
-  rc = arena_for_device(&ap);
-  if (rc) return rc;
-  const size_t o_x = kGroupFlag, o_i = o_x + ((n * 12 + 255) & ~(size_t)255),
-               o_o = o_i + ((m * 4 + 255) & ~(size_t)255), total = o_o + m * 12;
-  rc = arena_reserve(*ap, total);
-  if (rc) return rc;
-  hipStream_t st = ap->stream;
-  char *b = ap->base;
-  if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
-  HIP_TRY(hipMemcpyAsync(b + o_i, idx, m * 4, hipMemcpyHostToDevice, st));
-  HIP_TRY(hipMemsetAsync(b, 0, 4, st));
-  HIP_TRY(launch_gather_points((const float *)(b + o_x), (uint32_t)n, (const int32_t *)(b + o_i),
-                               (uint32_t)m, (float *)(b + o_o), (uint32_t *)b, st));
-  HIP_TRY(hipMemcpyAsync(out, b + o_o, m * 12, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (m == 0) return NSFPS_OK;
+    if (!idx || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    nsfps_status rc = check_group(n, m, 0);
+    if (rc) return rc;
+    for (uint64_t i = 0; i < m; ++i)
+      if (idx[i] < 0 || (uint64_t)idx[i] >= n) return fail(NSFPS_EINVAL, "an index lies outside [0, n)");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    rc = arena_for_device(&ap);
+    if (rc) return rc;
+    const size_t o_x = kGroupFlag, o_i = o_x + ((n * 12 + 255) & ~(size_t)255),
+                 o_o = o_i + ((m * 4 + 255) & ~(size_t)255), total = o_o + m * 12;
+    rc = arena_reserve(*ap, total);
+    if (rc) return rc;
+    hipStream_t st = ap->stream;
+    char *b = ap->base;
+    if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(b + o_i, idx, m * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemsetAsync(b, 0, 4, st));
+    HIP_TRY(launch_gather_points((const float *)(b + o_x), (uint32_t)n, (const int32_t *)(b + o_i),
+                                 (uint32_t)m, (float *)(b + o_o), (uint32_t *)b, st));
+    HIP_TRY(hipMemcpyAsync(out, b + o_o, m * 12, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return NSFPS_OK;
+  });
 }
 
 namespace {
@@ -1262,56 +1308,62 @@ nsfps_status ball_query_on(hipStream_t st, const float *xyz, uint64_t n, const f
 nsfps_status nsfps_ball_query_device(const float *d_xyz, uint64_t n, const float *d_centers,
                                      uint64_t m, float radius, uint32_t nsample, int32_t *d_out,
                                      void *stream) {
-  nsfps_status rc = check_ball(radius, nsample);
-  if (rc) return rc;
-  if (m == 0) return NSFPS_OK;
-  if (!d_centers || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  rc = check_group(n, m, nsample);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  Arena *ap = nullptr;
-  rc = arena_for_device(&ap);
-  if (rc) return rc;
-  if (bq_use_grid(n, m)) {
-    rc = arena_reserve(*ap, bq_grid_bytes(n, m));
+  return guarded([&]() -> nsfps_status {
+    nsfps_status rc = check_ball(radius, nsample);
     if (rc) return rc;
-  }
-  return ball_query_on((hipStream_t)stream, d_xyz, n, d_centers, m, radius, nsample, d_out,
-                       ap->base);
+    if (m == 0) return NSFPS_OK;
+    if (!d_centers || !d_out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    rc = check_group(n, m, nsample);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    rc = arena_for_device(&ap);
+    if (rc) return rc;
+    if (bq_use_grid(n, m)) {
+      rc = arena_reserve(*ap, bq_grid_bytes(n, m));
+      if (rc) return rc;
+    }
+    return ball_query_on((hipStream_t)stream, d_xyz, n, d_centers, m, radius, nsample, d_out,
+                         ap->base);
+  });
 }
 
 nsfps_status nsfps_ball_query(const float *xyz, uint64_t n, const float *centers, uint64_t m,
                               float radius, uint32_t nsample, int32_t *out) {
-  nsfps_status rc = check_ball(radius, nsample);
-  if (rc) return rc;
-  if (m == 0) return NSFPS_OK;
-  if (!centers || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
-  rc = check_group(n, m, nsample);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  Arena *ap = nullptr;
-  rc = arena_for_device(&ap);
-  if (rc) return rc;
-  const size_t o_x = 0, o_c = o_x + up256(n * 12), o_o = o_c + up256(m * 12),
-               o_w = o_o + up256(m * (size_t)nsample * 4);
-  rc = arena_reserve(*ap, o_w + (bq_use_grid(n, m) ? bq_grid_bytes(n, m) : 0));
-  if (rc) return rc;
-  hipStream_t st = ap->stream;
-  char *b = ap->base;
-  if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
-  HIP_TRY(hipMemcpyAsync(b + o_c, centers, m * 12, hipMemcpyHostToDevice, st));
-  rc = ball_query_on(st, (const float *)(b + o_x), n, (const float *)(b + o_c), m, radius, nsample,
-                     (int32_t *)(b + o_o), b + o_w);
-  if (rc) return rc;
-  HIP_TRY(hipMemcpyAsync(out, b + o_o, m * (size_t)nsample * 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    nsfps_status rc = check_ball(radius, nsample);
+    if (rc) return rc;
+    if (m == 0) return NSFPS_OK;
+    if (!centers || !out || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    rc = check_group(n, m, nsample);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    rc = arena_for_device(&ap);
+    if (rc) return rc;
+    const size_t o_x = 0, o_c = o_x + up256(n * 12), o_o = o_c + up256(m * 12),
+                 o_w = o_o + up256(m * (size_t)nsample * 4);
+    rc = arena_reserve(*ap, o_w + (bq_use_grid(n, m) ? bq_grid_bytes(n, m) : 0));
+    if (rc) return rc;
+    hipStream_t st = ap->stream;
+    char *b = ap->base;
+    if (n) HIP_TRY(hipMemcpyAsync(b + o_x, xyz, n * 12, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(b + o_c, centers, m * 12, hipMemcpyHostToDevice, st));
+    rc = ball_query_on(st, (const float *)(b + o_x), n, (const float *)(b + o_c), m, radius, nsample,
+                       (int32_t *)(b + o_o), b + o_w);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(out, b + o_o, m * (size_t)nsample * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return NSFPS_OK;
+  });
 }
 
 nsfps_status nsfps_get_stats(nsfps_stats *stats) {
-  if (!stats) return fail(NSFPS_EINVAL, "null pointer");
-  *stats = g_stats;
-  return NSFPS_OK;
+  return guarded([&]() -> nsfps_status {
+    if (!stats) return fail(NSFPS_EINVAL, "null pointer");
+    *stats = g_stats;
+    return NSFPS_OK;
+  });
 }
 
 void nsfps_release_workspace(void) {
