@@ -209,3 +209,18 @@ def test_gpu_grouping_device_entry_points(lib):
     finally:
         for b in bufs:
             hip.free(b)
+
+
+@pytest.mark.gpu
+def test_gpu_grid_ball_query_at_full_size(yf, oracle):
+    """The uniform cube's 1,048,576 points (the FPS workload) around 512 of its
+    own points and 64 outside them: the grid path at its real size."""
+    from ns_fps_amd.workloads import make_workload
+    from oracle import ball_query
+    P = make_workload("uniform_cube")["clouds"][0]
+    rs = np.random.RandomState(33)
+    cen = np.concatenate([P[rs.randint(0, len(P), 512)],
+                          rs.uniform(-1.2, 1.2, (64, 3)).astype(np.float32)])
+    for radius, k in [(0.05, 32), (0.02, 8)]:
+        got = yf.ball_query(P, cen, radius, k)
+        assert np.array_equal(got, ball_query(oracle, P, cen, radius, k)), (radius, k)
