@@ -738,19 +738,46 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
 // windows nearly always resolve the threshold) until a round had to force it
 // and got a list under a quarter full; from the next batch on, every round
 // gets kRefinePasses passes.
+// The batches of rounds (size, refinement passes) the last call of a given
+// shape enqueued.  A call of the same shape enqueues them back to back with no
+// status read in between, then goes on batch by batch if it is not finished;
+// rounds enqueued after a cloud is done return at once.  The samples never
+// depend on how rounds are batched.  Guarded by g_mu.
+struct RoundSchedule {
+  uint64_t shape[5] = {0, 0, 0, 0, 0};
+  std::vector<std::pair<uint32_t, uint32_t>> batches;
+};
+RoundSchedule g_schedule;
+
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
                         uint64_t *rounds_out) {
   uint32_t max_nl1 = 1;
   for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
   const uint32_t nc = (uint32_t)plans.size();
+  const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
+  const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
+  std::vector<std::pair<uint32_t, uint32_t>> used;
   HIP_TRY(launch_runs_init(d_clouds, nc, st));
   std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0, passes = 0;
+  if (replay) {
+    for (size_t i = 0; i + 1 < g_schedule.batches.size(); ++i) {
+      const auto bp = g_schedule.batches[i];
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, bp.first, bp.second, profile, st));
+      enqueued += bp.first;
+      used.push_back(bp);
+    }
+    if (!g_schedule.batches.empty()) {
+      batch = g_schedule.batches.back().first;
+      passes = g_schedule.batches.back().second;
+    }
+  }
   while (true) {
     HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
     enqueued += batch;
+    used.emplace_back(batch, passes);
     HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
                            st));
     HIP_TRY(hipStreamSynchronize(st));
@@ -772,7 +799,11 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       rounds = std::max<uint64_t>(rounds, q.rs.rounds);
     }
     *rounds_out = rounds;
-    if (all) break;
+    if (all) {
+      std::copy(shape, shape + 5, g_schedule.shape);
+      g_schedule.batches = used;
+      break;
+    }
     // every round takes at least one sample of every unfinished cloud
     stalled = samples == last_samples ? stalled + 1 : 0;
     if (stalled >= 2) return fail(NSFPS_EDEVICE, "internal: sampling made no progress");

@@ -76,3 +76,20 @@ def test_gpu_matches_oracle_on_sweep(yf, oracle, seed):
     want = oracle.fps(p, m, rng)
     assert got.dtype == np.int32
     assert np.array_equal(got, want), f"first difference at {np.argmax(got[:len(want)] != want[:len(got)])}"
+
+
+@pytest.mark.gpu
+def test_gpu_round_schedule_of_one_cloud_on_others(yf, oracle):
+    """A call replays the round batches of the last call of the same shape;
+    clouds of one shape but different contents (and so different round
+    counts) still give the oracle's samples, in either order."""
+    rs = np.random.RandomState(77)
+    n, m, rng = 30000, 6000, (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 32, 32, 32)
+    c = rs.uniform(-0.9, 0.9, (5, 3))
+    clouds = [rs.uniform(-1, 1, (n, 3)), rs.randn(n, 3) * 0.3,
+              c[rs.randint(0, 5, n)] + rs.randn(n, 3) * 0.01, rs.uniform(-1, 1, (n, 3))]
+    clouds = [np.ascontiguousarray(x, dtype=np.float32) for x in clouds]
+    want = [oracle.fps(x, m, rng) for x in clouds]
+    for order in ([0, 1, 2, 3], [2, 0, 3, 1, 1, 2]):
+        for i in order:
+            assert np.array_equal(yf.fps(clouds[i], m, yf.make_range(*rng)), want[i]), (order, i)
