@@ -233,7 +233,35 @@ __global__ __launch_bounds__(256) void k_bq_query(const float4 *__restrict__ spt
   }
   uint64_t cells = __ballot(cb < ce);
   uint32_t cnt = 0, nruns = 0;
-  while (cells) {
+  // one cell's candidates, already read: its hits, in index order, form a run
+  const auto scan_cell = [&](const float4 &q, bool in) {
+    if (lane == 0) runs[nruns] = cnt;
+    ++nruns;
+    const bool hit = in && sqdist(q.x, q.y, q.z, cx, cy, cz) < r2;
+    const uint64_t mask = __ballot(hit);
+    const uint32_t pos = cnt + lanes_below(mask);
+    if (hit && pos < kBqCap) hits[pos] = __float_as_uint(q.w);
+    cnt += (uint32_t)__popcll(mask);
+  };
+  if (__ballot(ce - cb > 64u) == 0) {
+    // every cell fits one step: two cells a step, both reads in flight
+    while (cells) {
+      const uint32_t l1 = (uint32_t)__builtin_ctzll(cells);
+      cells &= cells - 1;
+      const bool two = cells != 0;
+      const uint32_t l2 = two ? (uint32_t)__builtin_ctzll(cells) : l1;
+      if (two) cells &= cells - 1;
+      const uint32_t b1 = rdlane(cb, l1), e1 = rdlane(ce, l1), b2 = rdlane(cb, l2),
+                     e2 = two ? rdlane(ce, l2) : b2;
+      const uint32_t i1 = b1 + lane, i2 = b2 + lane;
+      float4 q1 = make_float4(0.f, 0.f, 0.f, 0.f), q2 = q1;
+      if (i1 < e1) q1 = spts[i1];
+      if (i2 < e2) q2 = spts[i2];
+      scan_cell(q1, i1 < e1);
+      if (two) scan_cell(q2, i2 < e2);
+    }
+  }
+  while (cells) {  // some cell holds more than 64 points: one cell at a time
     const uint32_t l = (uint32_t)__builtin_ctzll(cells);
     cells &= cells - 1;
     const uint32_t b = rdlane(cb, l), e = rdlane(ce, l);
