@@ -739,13 +739,15 @@ double ms_between(hipEvent_t a, hipEvent_t b) {
 // and got a list under a quarter full; from the next batch on, every round
 // gets kRefinePasses passes.
 // The batches of rounds (size, refinement passes) the last call of a given
-// shape enqueued.  A call of the same shape enqueues them back to back with no
-// status read in between, then goes on batch by batch if it is not finished;
-// rounds enqueued after a cloud is done return at once.  The samples never
-// depend on how rounds are batched.  Guarded by g_mu.
+// shape enqueued, and the rounds it needed.  A call of the same shape enqueues
+// those batches back to back, cut at that many rounds, with no status read in
+// between, then goes on batch by batch if it is not finished; rounds enqueued
+// after a cloud is done return at once.  The samples never depend on how
+// rounds are batched.  Guarded by g_mu.
 struct RoundSchedule {
   uint64_t shape[5] = {0, 0, 0, 0, 0};
   std::vector<std::pair<uint32_t, uint32_t>> batches;
+  uint64_t rounds = 0;
 };
 RoundSchedule g_schedule;
 
@@ -762,22 +764,25 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0, passes = 0;
+  bool launched = false;  // rounds are in the queue and no status read has followed
   if (replay) {
-    for (size_t i = 0; i + 1 < g_schedule.batches.size(); ++i) {
-      const auto bp = g_schedule.batches[i];
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, bp.first, bp.second, profile, st));
-      enqueued += bp.first;
-      used.push_back(bp);
-    }
-    if (!g_schedule.batches.empty()) {
-      batch = g_schedule.batches.back().first;
-      passes = g_schedule.batches.back().second;
+    for (const auto &bp : g_schedule.batches) {
+      const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
+      if (take == 0) break;
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, st));
+      enqueued += take;
+      used.emplace_back(take, bp.second);
+      passes = bp.second;
+      launched = true;
     }
   }
   while (true) {
-    HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
-    enqueued += batch;
-    used.emplace_back(batch, passes);
+    if (!launched) {
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
+      enqueued += batch;
+      used.emplace_back(batch, passes);
+    }
+    launched = false;
     HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
                            st));
     HIP_TRY(hipStreamSynchronize(st));
@@ -802,6 +807,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     if (all) {
       std::copy(shape, shape + 5, g_schedule.shape);
       g_schedule.batches = used;
+      g_schedule.rounds = rounds;
       break;
     }
     // every round takes at least one sample of every unfinished cloud
