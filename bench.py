@@ -8,19 +8,25 @@ call on device-resident input: structure build (cell keys, radix sorts,
 leaves) + the whole sampling pass + the int32 indices written to device
 memory.
 
-Roofline: the sampling pass (speculative-run rounds: k_update, k_refine,
-k_gather, k_run) moves the reference's algorithmic bytes -- 16 B per
-candidate point and 8 B per candidate 16-point leaf of every iteration, the
-per-iteration census in tests/golden/census.npz -- in the hipEvent-timed
+Roofline: the sampling pass moves the reference's algorithmic bytes -- 16 B
+per candidate point and 8 B per candidate 16-point leaf of every iteration,
+the per-iteration census in tests/golden/census.npz -- in the hipEvent-timed
 sample_ms of the call.
 
-Prints ONE JSON line (rank 0).  With --all it first prints one extra line per
-workload (informational), the contract line always comes last.
+Besides the steady-state time of repeated calls (ms_per_step), the line
+reports the first call of a shape (first_call_ms: no replayed round
+schedule), the host-buffer call with its PCIe copies (e2e_ms) and the
+sampling of a prepared plan (plan_sample_ms).
 
-  python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--workload uniform_cube]
+Prints ONE JSON line (rank 0).  With --all it first prints one line per
+workload (the five seeded workloads, each with its roofline and reference
+CPU time); the contract line always comes last.
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload uniform_cube]
 """
 
 import argparse
+import hashlib
 import json
 import os
 import re
@@ -34,6 +40,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+HEADLINE_METRIC = "FPS ms/call & samples/s at 1M pts -> 65,536 samples; % of HBM roofline"
+ALL_WORKLOADS = ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]
+
+
+def metric_for(w):
+    if w["name"] == "uniform_cube":
+        return HEADLINE_METRIC
+    n, m = len(w["clouds"][0]), int(w["n_samples"])
+    per = f"{len(w['clouds'])} x " if len(w["clouds"]) > 1 else ""
+    return (f"FPS ms/call & samples/s at {per}{n:,} pts -> {m:,} samples ({w['name']}); "
+            "% of HBM roofline")
 
 
 def workload_config(w, extra=None):
@@ -53,6 +70,23 @@ def workload_config(w, extra=None):
     return cfg
 
 
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count()
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "cpus_available": avail}
+
+
 def load_census(wname):
     path = os.path.join(ROOT, "tests", "golden", "census.npz")
     if not os.path.exists(path):
@@ -60,8 +94,7 @@ def load_census(wname):
     z = np.load(path, allow_pickle=False)
     if f"{wname}__total" not in z.files:
         return None
-    return {"total": int(z[f"{wname}__total"][0]),
-            "cum": z[f"{wname}__cum4096"] if f"{wname}__cum4096" in z.files else None}
+    return {"total": int(z[f"{wname}__total"][0])}
 
 
 def golden_hashes(wname):
@@ -70,7 +103,7 @@ def golden_hashes(wname):
         return json.load(f).get(wname)
 
 
-def profile_traffic(kernel="sampling", wname="uniform_cube"):
+def profile_traffic(kernel, wname):
     """HBM bytes per call of the sampling pass from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE in KiB, calibrated by a copy kernel of
     known size); None when no summary was committed."""
@@ -83,13 +116,42 @@ def profile_traffic(kernel="sampling", wname="uniform_cube"):
     return float(m.group(1)) if m else None
 
 
+def sha_i32(a):
+    return hashlib.sha256(np.asarray(a, np.int32).tobytes()).hexdigest()
+
+
+def roofline_of(wname, sample_ms, engine):
+    census = load_census(wname)
+    if census is None or not sample_ms or sample_ms <= 0:
+        return None
+    alg = census["total"]  # every iteration, first pass included
+    achieved = alg / (sample_ms * 1e6)  # GB/s
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 6),
+            "traffic": profile_traffic("sampling", wname),
+            "kernel": "sampling pass (k_update+k_refine+k_gather+k_run rounds)"
+            if engine == "runs" else "sampling pass (k_wide_update+k_late_loop)",
+            "alg_bytes_per_launch": alg, "kernel_ms": round(sample_ms, 3)}
+
+
+# ------------------------------------------------------------------ GPU legs
+
 def run_single(lib, hip, w, steps, warmup):
-    import hashlib
+    """Device-resident input.  Returns the steady-state ms per call, per-call
+    statistics, the output and its digest, and the first call of the shape."""
     P = w["clouds"][0]
     m = int(w["n_samples"])
     d_xyz = hip.upload(P)
     d_out = hip.malloc(m * 4)
     try:
+        # a call of another shape first, so that the timed first call replays
+        # no round schedule
+        lib.fps_device(d_xyz, len(P), m - 1, w["range"], d_out)
+        hip.synchronize()
+        t = time.perf_counter()
+        lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
+        first_ms = (time.perf_counter() - t) * 1e3
+        first_stats = lib.stats()
         for _ in range(warmup):
             lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
         hip.synchronize()
@@ -104,12 +166,53 @@ def run_single(lib, hip, w, steps, warmup):
     finally:
         hip.free(d_xyz)
         hip.free(d_out)
-    digest = hashlib.sha256(out.astype(np.int32).tobytes()).hexdigest()
-    return (t1 - t0) * 1e3 / steps, stats, out, digest
+    return {"ms": (t1 - t0) * 1e3 / steps, "stats": stats, "out": out, "digest": sha_i32(out),
+            "first_ms": first_ms, "first_stats": first_stats}
+
+
+def run_host_buffers(lib, w, reps=3):
+    """nsfps_fps on host buffers: upload, build, sampling, download."""
+    P = w["clouds"][0]
+    m = int(w["n_samples"])
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        out = lib.fps(P, m, w["range"])
+        times.append((time.perf_counter() - t) * 1e3)
+    return statistics.median(times), sha_i32(out)
+
+
+def run_plan(lib, hip, w, steps):
+    """A plan created once on device-resident input, sampled `steps` times."""
+    if not hasattr(lib, "plan_create"):
+        return None
+    P = w["clouds"][0]
+    m = int(w["n_samples"])
+    d_xyz = hip.upload(P)
+    d_out = hip.malloc(m * 4)
+    plan = None
+    try:
+        t = time.perf_counter()
+        plan = lib.plan_create(d_xyz, len(P), w["range"], on_device=True)
+        create_ms = (time.perf_counter() - t) * 1e3
+        lib.plan_sample(plan, m, d_out)
+        hip.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            n = lib.plan_sample(plan, m, d_out)
+        hip.synchronize()
+        t1 = time.perf_counter()
+        out = hip.download(d_out, n, np.int32)
+    finally:
+        if plan is not None:
+            lib.plan_destroy(plan)
+        hip.free(d_xyz)
+        hip.free(d_out)
+    return {"plan_create_ms": round(create_ms, 3),
+            "plan_sample_ms": round((t1 - t0) * 1e3 / steps, 3), "digest": sha_i32(out)}
 
 
 def run_batched(yf, w, steps, warmup):
-    import hashlib
     P = np.stack(w["clouds"])
     for _ in range(warmup):
         yf.fps_batched(P, w["n_samples"], None, *w["blocks"])
@@ -119,64 +222,116 @@ def run_batched(yf, w, steps, warmup):
         idx, lens = yf.fps_batched(P, w["n_samples"], None, *w["blocks"])
         stats.append(yf.last_stats())
     t1 = time.perf_counter()
-    digests = [hashlib.sha256(idx[b, :lens[b]].astype(np.int32).tobytes()).hexdigest()
-               for b in range(len(lens))]
+    digests = [sha_i32(idx[b, :lens[b]]) for b in range(len(lens))]
     return (t1 - t0) * 1e3 / steps, stats, digests
 
 
+# ------------------------------------------------------------- CPU baseline
+
 def cpu_baseline(w, budget_s=30.0):
     """The reference compiled from its own sources with its setup.py flags
-    (oracle/_ref, kind "reference"), else the oracle ("port"); one core; the
-    whole first cloud of the workload when it fits the budget, else the first
-    iterations extrapolated linearly."""
+    (oracle/_ref, kind "reference"), else the oracle ("port"); one core.
+
+    A prefix of cloud 0's samples is timed first; when the whole workload (all
+    clouds, every sample), extrapolated linearly from it, fits budget_s, the
+    whole workload is timed, up to three times (median).  Otherwise the longest
+    power-of-two prefix of cloud 0's sample sequence that fits the budget is
+    timed once (a prefix costs more per sample than the whole call: early
+    samples have the largest cubes)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import REF_ASBUILT_SO, Oracle, Reference
-    P = w["clouds"][0]
+    clouds = w["clouds"]
     m = int(w["n_samples"])
     if os.path.exists(REF_ASBUILT_SO):
         runner, kind = Reference(REF_ASBUILT_SO), "reference"
     else:
         runner, kind = Oracle(), "port"
+    rng, blocks = w["range"], w["blocks"]
+    mp = min(m, max(64, m // 16))
     t = time.perf_counter()
-    runner.fps(P, m, w["range"], w["blocks"])
-    el = time.perf_counter() - t
-    base = {"value": round(m / el, 2), "unit": "samples/s", "cores": 1, "kind": kind,
-            "ms_per_call": round(el * 1e3, 2),
-            "sample": f"one full call on cloud 0 of {w['name']} ({len(P)} points -> {m} samples), "
-                      f"single thread, {os.path.basename(getattr(runner, 'path', 'liboracle.so'))}"}
-    o = Oracle()
-    # our C restatement on the same call, one core, against the reference
-    if kind == "reference":
-        try:
+    runner.fps(clouds[0], mp, rng, blocks)
+    t_p = time.perf_counter() - t
+    est = t_p * (m / mp) * len(clouds)
+    info = cpu_info()
+    if est <= budget_s:
+        reps = max(1, min(3, int(budget_s // max(est, 1e-3))))
+        times = []
+        for _ in range(reps):
             t = time.perf_counter()
-            o.fps(P, m, w["range"], w["blocks"])
+            for P in clouds:
+                runner.fps(P, m, rng, blocks)
+            times.append(time.perf_counter() - t)
+        el = statistics.median(times)
+        done = m * len(clouds)
+        what = (f"{'all ' + str(len(clouds)) + ' clouds' if len(clouds) > 1 else 'the whole call'} "
+                f"of {w['name']} ({len(clouds[0])} points -> {m} samples"
+                f"{' each' if len(clouds) > 1 else ''}), median of {reps}")
+        sample_m = m
+    else:
+        sample_m = mp
+        while sample_m * 2 <= m and t_p * (sample_m * 2 / mp) <= budget_s:
+            sample_m *= 2
+        t = time.perf_counter()
+        runner.fps(clouds[0], sample_m, rng, blocks)
+        el = time.perf_counter() - t
+        done = sample_m
+        what = (f"the first {sample_m} of {m} samples of cloud 0 of {w['name']} "
+                f"({len(clouds[0])} points; a prefix of the same sample sequence), one run")
+    base = {"value": round(done / el, 2), "unit": "samples/s", "cores": 1, "kind": kind,
+            "ms_per_call": round(el * 1e3, 2) if sample_m == m else None,
+            "ms_sample": round(el * 1e3, 2),
+            "sample": f"{what}; single thread, "
+                      f"{os.path.basename(getattr(runner, 'path', 'liboracle.so'))}",
+            **info}
+    if kind == "reference":
+        # our C restatement (the oracle) on the same sample, one core
+        try:
+            o = Oracle()
+            t = time.perf_counter()
+            if sample_m == m:
+                for P in clouds:
+                    o.fps(P, m, rng, blocks)
+            else:
+                o.fps(clouds[0], sample_m, rng, blocks)
             el_port = time.perf_counter() - t
-            base["port_ms_per_call"] = round(el_port * 1e3, 2)
+            base["port_ms_sample"] = round(el_port * 1e3, 2)
             base["port_over_reference"] = round(el_port / el, 3)
         except Exception as e:  # informational only
             base["port_error"] = str(e)
-    # naive O(N*M) FPS, first iterations extrapolated linearly (cost per
-    # iteration is constant): one thread, then every core of the host
+    return base
+
+
+def naive_baselines(w):
+    """Naive O(N*M) FPS on cloud 0, the first iterations extrapolated linearly
+    (cost per iteration is constant): one thread, then every core."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle
+    o = Oracle()
+    P = w["clouds"][0]
+    m = int(w["n_samples"])
+    out = {}
     try:
         k = max(16, min(m - 1, int(2e8 // max(len(P), 1))))
         t = time.perf_counter()
         o.fps_naive(P, m, tie="index", max_iters=k)
         el = time.perf_counter() - t
-        base["naive_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
-        base["naive_sample"] = f"first {k} of {m - 1} iterations, single thread, extrapolated"
+        out["naive_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
+        out["naive_sample"] = f"first {k} of {m - 1} iterations, single thread, extrapolated"
         nt = o.max_threads()
         k = max(16, min(m - 1, int(2e8 * nt // max(len(P), 1))))
         t = time.perf_counter()
         o.fps_naive_mt(P, m, max_iters=k, threads=nt)
         el = time.perf_counter() - t
-        base["naive_mt_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
-        base["naive_mt_threads"] = nt
-        base["naive_mt_sample"] = (f"first {k} of {m - 1} iterations, {nt} OpenMP threads, "
-                                   "extrapolated")
+        out["naive_mt_ms_extrapolated"] = round(el / k * (m - 1) * 1e3, 1)
+        out["naive_mt_threads"] = nt
+        out["naive_mt_sample"] = (f"first {k} of {m - 1} iterations, {nt} OpenMP threads, "
+                                  "extrapolated")
     except Exception as e:  # the naive timings are informational only
-        base["naive_error"] = str(e)
-    return base
+        out["naive_error"] = str(e)
+    return out
 
+
+# ---------------------------------------------------------------- grouping
 
 def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
     """The grouping step after FPS on the uniform cube: 65,536 FPS centers,
@@ -210,14 +365,64 @@ def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
             "exact": exact}
 
 
+# --------------------------------------------------------------------- lines
+
+def workload_line(lib, hip, yf, wname, budget_s, with_cpu=True):
+    """One informational line per workload: time per call, samples/s,
+    roofline of the sampling pass and the reference's CPU time."""
+    from ns_fps_amd.workloads import make_workload
+    w = make_workload(wname)
+    g = golden_hashes(wname)
+    if len(w["clouds"]) == 1:
+        steps = 1 if wname == "clustered" else 5
+        r = run_single(lib, hip, w, steps, 0 if wname == "clustered" else 1)
+        s = r["stats"][-1]
+        exact = g is not None and r["digest"] == g["output_sha256"][0]
+        line = {"workload": wname, "metric": metric_for(w), "ms_per_call": round(r["ms"], 3),
+                "first_call_ms": round(r["first_ms"], 3),
+                "device_ms": round(s["device_ms"], 3), "build_ms": round(s["build_ms"], 3),
+                "sample_ms": round(s["sample_ms"], 3), "rounds": int(s["rounds"]),
+                "samples_per_s": round(len(r["out"]) / (r["ms"] / 1e3), 1), "bit_exact": exact}
+        if wname != "clustered":
+            e2e, dg = run_host_buffers(lib, w)
+            line["e2e_ms"] = round(e2e, 3)
+            line["e2e_bit_exact"] = g is not None and dg == g["output_sha256"][0]
+        sample_ms = statistics.mean(x["sample_ms"] for x in r["stats"])
+        engine = "runs" if s["engine"] else "tree"
+    else:
+        ms, st, dgs = run_batched(yf, w, 3, 1)
+        s = st[-1]
+        exact = g is not None and dgs == g["output_sha256"]
+        line = {"workload": wname, "metric": metric_for(w), "ms_per_call": round(ms, 3),
+                "device_ms": round(s["device_ms"], 3), "build_ms": round(s["build_ms"], 3),
+                "sample_ms": round(s["sample_ms"], 3), "e2e_ms": round(s["e2e_ms"], 3),
+                "rounds": int(s["rounds"]),
+                "samples_per_s": round(s["samples"] / (ms / 1e3), 1), "bit_exact": exact,
+                "input": "host float32 (B,N,3); e2e includes the bounds on the host and the copies"}
+        sample_ms = statistics.mean(x["sample_ms"] for x in st)
+        engine = s["engine"]
+    line["roofline"] = roofline_of(wname, sample_ms, engine)
+    if with_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, budget_s)
+        cb = line["cpu_baseline"]
+        if cb.get("ms_per_call"):
+            line["speedup_vs_cpu_baseline"] = round(cb["ms_per_call"] / line["ms_per_call"], 1)
+    return line
+
+
 def main():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="uniform_cube")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=30.0,
+                    help="seconds of reference CPU work per workload (default 30)")
     ap.add_argument("--all", action="store_true", help="also print a line per workload")
+    ap.add_argument("--only", default="",
+                    help="with --all: comma-separated workloads instead of all five")
     ap.add_argument("--ball-query", action="store_true",
                     help="time only the grouping step after FPS (ball query) and print its line")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
@@ -232,7 +437,7 @@ def main():
 
     from ns_fps_amd.capi import Hip, Lib
     from ns_fps_amd.workloads import make_workload
-    import ns_fps_amd.yuezu_fps_module as yf
+    import yuezu_fps.yuezu_fps_module as yf
 
     lib = Lib()
     if lib.device_count() < 1:
@@ -252,75 +457,57 @@ def main():
         return
 
     if args.all:
-        for wname in ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]:
-            w = make_workload(wname)
-            g = golden_hashes(wname)
-            if len(w["clouds"]) == 1:
-                steps = 1 if wname == "clustered" else 3
-                ms, st, out, dg = run_single(lib, hip, w, steps, 1 if wname != "clustered" else 0)
-                exact = g is not None and dg == g["output_sha256"][0]
-                s = st[-1]
-                line = {"workload": wname, "ms_per_call": round(ms, 3),
-                        "device_ms": round(s["device_ms"], 3), "build_ms": round(s["build_ms"], 3),
-                        "late_ms": round(s["late_ms"], 3), "wide_ms": round(s["wide_ms"], 3),
-                        "samples_per_s": round(len(out) / (ms / 1e3), 1), "bit_exact": exact}
-            else:
-                ms, st, dgs = run_batched(yf, w, 3, 1)
-                exact = g is not None and dgs == g["output_sha256"]
-                s = st[-1]
-                line = {"workload": wname, "ms_per_call": round(ms, 3),
-                        "device_ms": round(s["device_ms"], 3), "e2e_ms": round(s["e2e_ms"], 3),
-                        "samples_per_s": round(s["samples"] / (ms / 1e3), 1), "bit_exact": exact}
-            census = load_census(wname)
-            if census:
-                line["alg_gb"] = round(census["total"] / 1e9, 3)
-                line["alg_gbs_over_device_time"] = round(census["total"] / (line["device_ms"] * 1e6), 1)
+        names = [n for n in args.only.split(",") if n] or ALL_WORKLOADS
+        for wname in names:
+            line = workload_line(lib, hip, yf, wname, args.cpu_budget,
+                                 with_cpu=not args.no_cpu_baseline)
             print(json.dumps(line), flush=True)
 
     w = make_workload(args.workload)
     if len(w["clouds"]) != 1:
         print(json.dumps({"error": "the contract line needs a single-cloud workload"}))
         sys.exit(2)
-    ms, stats, out, digest = run_single(lib, hip, w, args.steps, args.warmup)
-    m = int(w["n_samples"])
+    r = run_single(lib, hip, w, args.steps, args.warmup)
+    stats = r["stats"]
     g = golden_hashes(args.workload)
-    exact = g is not None and digest == g["output_sha256"][0] and len(out) == g["lengths"][0]
+    exact = g is not None and r["digest"] == g["output_sha256"][0] and len(r["out"]) == g["lengths"][0]
     sample_ms = statistics.mean(s["sample_ms"] for s in stats)
-    census = load_census(args.workload)
-    roofline = None
     engine = "runs" if stats[-1].get("engine", 0) else "tree"
-    if census is not None:
-        alg = census["total"]  # every iteration, first pass included
-        achieved = alg / (sample_ms * 1e6)  # GB/s
-        roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6),
-                    "traffic": profile_traffic("sampling", args.workload),
-                    "kernel": "sampling pass (k_update+k_refine+k_gather+k_run rounds)"
-                    if engine == "runs" else "k_wide_update+k_late_loop",
-                    "alg_bytes_per_launch": alg, "kernel_ms": round(sample_ms, 3)}
-    wide_iters = int(stats[-1]["wide_iters"])
+    e2e_ms, e2e_digest = run_host_buffers(lib, w)
+    plan = run_plan(lib, hip, w, max(3, args.steps // 2))
     line = {
-        "metric": "FPS ms/call & samples/s at 1M pts -> 65,536 samples; % of HBM roofline",
-        "value": round(len(out) / (ms / 1e3), 2),
+        "metric": metric_for(w),
+        "value": round(len(r["out"]) / (r["ms"] / 1e3), 2),
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 3),
+        "ms_per_step": round(r["ms"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded uniform cube, NumPy RandomState(2))",
-        "config": workload_config(w, {"engine": engine, "rounds": int(stats[-1].get("rounds", 0)),
-                                      "wide_iters": wide_iters,
-                                      "device_ms": round(statistics.mean(s["device_ms"] for s in stats), 3),
-                                      "build_ms": round(statistics.mean(s["build_ms"] for s in stats), 3),
-                                      "bit_exact_vs_reference": exact}),
-        "roofline": roofline,
+        "data": "synthetic (seeded, NumPy RandomState; the workload's generator in "
+                "ns_fps_amd/workloads.py)",
+        "config": workload_config(w, {
+            "engine": engine, "rounds": int(stats[-1].get("rounds", 0)),
+            "device_ms": round(statistics.mean(s["device_ms"] for s in stats), 3),
+            "build_ms": round(statistics.mean(s["build_ms"] for s in stats), 3),
+            "sample_ms": round(sample_ms, 3),
+            "bit_exact_vs_reference": exact}),
+        "first_call_ms": round(r["first_ms"], 3),
+        "e2e_ms": round(e2e_ms, 3),
+        "e2e_bit_exact": g is not None and e2e_digest == g["output_sha256"][0],
+        "roofline": roofline_of(args.workload, sample_ms, engine),
     }
+    if plan is not None:
+        line["plan_sample_ms"] = plan["plan_sample_ms"]
+        line["plan_create_ms"] = plan["plan_create_ms"]
+        line["plan_bit_exact"] = g is not None and plan["digest"] == g["output_sha256"][0]
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(w)
+        cb = cpu_baseline(w, args.cpu_budget)
+        cb.update(naive_baselines(w))
+        line["cpu_baseline"] = cb
     print(json.dumps(line), flush=True)
 
 

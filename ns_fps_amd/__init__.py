@@ -1,8 +1,9 @@
 """MI355X-native farthest point sampling with the NS-FPS (yuezu_fps) semantics.
 
-* ``ns_fps_amd.yuezu_fps_module`` -- drop-in Python module (SpaceRange,
-  make_range, make_uniform_range, fps, fps_with_bbox, constants, plus
-  fps_batched), built from csrc/ by ``python -m ns_fps_amd.build``.
+* ``yuezu_fps.yuezu_fps_module`` -- the drop-in Python module under the
+  reference's import path (SpaceRange, make_range, make_uniform_range, fps,
+  fps_with_bbox, constants, plus fps_batched and the grouping step), built
+  from csrc/ by ``python -m ns_fps_amd.build``.
 * ``ns_fps_amd.capi`` -- ctypes binding of the C ABI (include/nsfps.h).
 * ``ns_fps_amd.workloads`` -- seeded synthetic clouds of the benchmark.
 * ``ns_fps_amd.kitti`` -- KITTI scan files: reader, z filter, bounds range

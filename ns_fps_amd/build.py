@@ -1,29 +1,41 @@
 """Builds the native parts in-tree (no JIT cache, nothing installed).
 
-* ``libnsfps.so`` -- HIP kernels (gfx950) + C++ host library behind the C ABI
-  of include/nsfps.h, compiled by hipcc.
-* ``yuezu_fps_module*.so`` -- the pybind11 module, linked against libnsfps.so
-  with an $ORIGIN rpath.
+* ``ns_fps_amd/libnsfps.so`` -- HIP kernels (gfx950) + C++ host library
+  behind the C ABI of include/nsfps.h, compiled by hipcc.
+* ``yuezu_fps/yuezu_fps_module*.so`` -- the pybind11 module under the
+  reference's own import path (``import yuezu_fps.yuezu_fps_module as yf``),
+  linked against libnsfps.so with an $ORIGIN-relative rpath.
 
 Run ``python -m ns_fps_amd.build`` (or ``__graft_entry__.build()``).
 """
 
 import os
+import re
 import subprocess
 import sys
 import sysconfig
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
+MODULE_DIR = os.path.join(ROOT, "yuezu_fps")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("NSFPS_OFFLOAD_ARCH", "gfx950")
 
 LIB = os.path.join(HERE, "libnsfps.so")
+SOURCES = ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_group.hip",
+           "nsfps_host.cpp")
 
-# Exact fp32: no contraction, IEEE division/sqrt, denormals kept.  Packed fp32
-# instructions are disabled for all device code.
+# Exact fp32: no contraction, IEEE division/sqrt, denormals kept.
+# "-packed-fp32-ops" turns off the gfx950 packed fp32 instructions
+# (v_pk_add/mul/fma_f32) in the device pass.  The same -Xclang pair also
+# reaches hipcc's x86 host pass, which does not know the feature and prints
+# "not a recognized feature" once per translation unit; the driver cannot
+# forward an option with an argument to the device pass alone
+# (-Xarch_device refuses it), so that host-pass warning is filtered from the
+# build output and the device assembly is checked instead (check_no_packed_fp32).
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fno-fast-math",
@@ -32,37 +44,77 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result",
 ]
+HOST_PASS_WARNING = "'-packed-fp32-ops' is not a recognized feature for this target"
+PACKED_FP32 = re.compile(r"\bv_pk_(add|mul|fma)_f32\b")
 
 
-def _run(cmd):
+def _run(cmd, cwd=None):
     print("+", " ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    p = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    lines = p.stdout.splitlines()
+    kept = [ln for ln in lines if HOST_PASS_WARNING not in ln]
+    if kept:
+        print("\n".join(kept), flush=True)
+    if len(kept) != len(lines):
+        print(f"  ({len(lines) - len(kept)} host-pass notes about -packed-fp32-ops omitted; "
+              "the device pass applies the feature)", flush=True)
+    if p.returncode != 0:
+        raise subprocess.CalledProcessError(p.returncode, cmd)
+
+
+def check_no_packed_fp32(asm_dir):
+    """Fails when the gfx950 assembly of this build holds a packed fp32
+    add/mul/fma instruction."""
+    found = []
+    n_files = 0
+    for name in sorted(os.listdir(asm_dir)):
+        if not (name.endswith(".s") and f"amdgcn-amd-amdhsa-{ARCH}" in name):
+            continue
+        n_files += 1
+        with open(os.path.join(asm_dir, name)) as f:
+            for ln in f:
+                if PACKED_FP32.search(ln):
+                    found.append(f"{name}: {ln.strip()}")
+    if n_files == 0:
+        raise RuntimeError("no device assembly was written; cannot check for packed fp32")
+    if found:
+        raise RuntimeError("packed fp32 instructions in the device code:\n" + "\n".join(found[:20]))
+    print(f"  device assembly of {n_files} translation units: no v_pk_add/mul/fma_f32", flush=True)
 
 
 def module_path():
     suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
-    return os.path.join(HERE, "yuezu_fps_module" + suffix)
+    return os.path.join(MODULE_DIR, "yuezu_fps_module" + suffix)
 
 
 def build_lib():
-    srcs = [os.path.join(CSRC, f) for f in ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_group.hip",
-                                             "nsfps_host.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in SOURCES]
     tmp = LIB + ".tmp"
-    _run([HIPCC, *DEVICE_FLAGS, "-shared", "-I", INCLUDE, "-I", CSRC, *srcs, "-o", tmp])
+    with tempfile.TemporaryDirectory(prefix="nsfps_build_") as td:
+        # -save-temps keeps each translation unit's gfx950 assembly in td
+        _run([HIPCC, *DEVICE_FLAGS, "-save-temps", "-shared", "-I", INCLUDE, "-I", CSRC, *srcs,
+              "-o", tmp], cwd=td)
+        check_no_packed_fp32(td)
     os.replace(tmp, LIB)
     return LIB
 
 
 def build_module():
     import pybind11
+    os.makedirs(MODULE_DIR, exist_ok=True)
     out = module_path()
     tmp = out + ".tmp"
     pyinc = sysconfig.get_paths()["include"]
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
           "-I", INCLUDE, "-I", pybind11.get_include(), "-I", pyinc,
           os.path.join(CSRC, "yuezu_fps_pybind.cpp"),
-          "-L", HERE, "-lnsfps", "-Wl,-rpath,$ORIGIN", "-o", tmp])
+          "-L", HERE, "-lnsfps", "-Wl,-rpath,$ORIGIN/../ns_fps_amd", "-o", tmp])
     os.replace(tmp, out)
+    # an older build placed the module inside the package: remove it so that
+    # only one copy of the bindings exists
+    old = os.path.join(HERE, os.path.basename(out))
+    if os.path.exists(old):
+        os.remove(old)
     return out
 
 

@@ -77,7 +77,10 @@ nsfps_status check_range(const nsfps_range &r) {
   const uint32_t bl[3] = {r.x_blocks, r.y_blocks, r.z_blocks};
   for (uint32_t v : bl) {
     if (v == 0) return fail(NSFPS_EINVAL, "block counts must be >= 1");
-    if (v > 1024) return fail(NSFPS_EUNSUPPORTED, "block counts above 1024 per axis are not supported");
+    if (v > 1024)
+      return fail(NSFPS_EUNSUPPORTED,
+                  "block counts above 1024 per axis are not supported (a cell's coordinates are "
+                  "packed 10 bits per axis)");
   }
   return NSFPS_OK;
 }
@@ -317,6 +320,7 @@ struct CloudPlan {
   uint2 *d_cell_info = nullptr;
   uint32_t *d_bucket = nullptr, *d_fine = nullptr;  // per point: bucket, sub-cell code
   uint64_t cap = 0;                // slots per bucket in the padded layout
+  bool tree = false;               // sampled by the tree engine (its loop holds level 1 in LDS)
   std::vector<uint32_t> lut_host;  // source of an asynchronous copy: lives until the sync
 };
 
@@ -534,8 +538,13 @@ nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs) {
   if (c.nleaves > p.leaves_ub)
     return fail(NSFPS_EDEVICE, "internal: leaf count %u exceeds bound %u", c.nleaves, p.leaves_ub);
   c.nl1 = (c.nleaves + kFan - 1) / kFan;
-  if (c.nl1 > kMaxL1)
-    return fail(NSFPS_EUNSUPPORTED, "cloud needs %u level-1 nodes (max %u)", c.nl1, kMaxL1);
+  // the tree engine's single-workgroup loop keeps every level-1 node in LDS;
+  // the runs engine has no such limit (level-1 nodes are its grid size)
+  if (p.tree && c.nl1 > kMaxL1)
+    return fail(NSFPS_EUNSUPPORTED,
+                "cloud needs %u level-1 nodes, above the %u the tree engine (grids whose block "
+                "counts are not all powers of two) holds",
+                c.nl1, kMaxL1);
   return NSFPS_OK;
 }
 
@@ -861,6 +870,14 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
     plans[i].dev.rs = &d_status[i].rs;
   }
 
+  // the engine: speculative runs where every cloud's bucket <-> cell map is
+  // one-to-one, the tree loop otherwise (or when NSFPS_ENGINE=tree asks)
+  bool runs = true;
+  for (auto &p : plans) runs = runs && p.rng.dev.bijective;
+  const char *eng = getenv("NSFPS_ENGINE");
+  if (eng && strcmp(eng, "tree") == 0) runs = false;
+  for (auto &p : plans) p.tree = !runs;
+
   HIP_TRY(hipEventRecord(a.ev[0], st));
   uint64_t leaves = 0, points = 0, wide_total = 0;
   uint32_t lds_bytes = 0;
@@ -876,10 +893,6 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   std::vector<CloudDev> devs;
   for (auto &p : plans) devs.push_back(p.dev);
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
-  bool runs = true;
-  for (auto &p : plans) runs = runs && p.rng.dev.bijective;
-  const char *eng = getenv("NSFPS_ENGINE");
-  if (eng && strcmp(eng, "tree") == 0) runs = false;
   uint64_t rounds = 0;
   if (runs) {
     HIP_TRY(hipEventRecord(a.ev[3], st));

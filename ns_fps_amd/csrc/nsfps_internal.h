@@ -14,7 +14,8 @@ constexpr uint32_t kFan = 64;
 // Sub-cell Morton bits (3 per axis) used to order points physically inside a
 // cell so that leaf bounding boxes are tight; results do not depend on it.
 constexpr uint32_t kFineBits = 9;
-// Level-1 nodes the single-workgroup loop can hold (level 2 then fits one wave).
+// Level-1 nodes the tree engine's single-workgroup loop can hold (level 2 then
+// fits one wave); the runs engine has no such limit.
 constexpr uint32_t kMaxL1 = 4096;
 // Threads of the single-workgroup loop (one cube cell per thread per chunk):
 // 512 by default, 1024 selectable.

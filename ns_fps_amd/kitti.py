@@ -22,7 +22,7 @@ import warnings
 
 import numpy as np
 
-from . import yuezu_fps_module as yf
+import yuezu_fps.yuezu_fps_module as yf
 
 KITTI_BLOCKS = (128, 128, 2)
 KITTI_Z_MIN = -5.0

@@ -32,7 +32,7 @@ def oracle():
 
 @pytest.fixture(scope="session")
 def yf():
-    import ns_fps_amd.yuezu_fps_module as m
+    import yuezu_fps.yuezu_fps_module as m
     return m
 
 

@@ -248,6 +248,31 @@ def test_tie_heavy_clouds_match_oracle(yf, oracle, name, pts, m, rng):
     assert np.array_equal(got, want), name
 
 
+def test_many_level1_nodes_on_the_runs_engine(yf, oracle):
+    """1M uniform points on a 128^3 grid: about 825k occupied buckets, each
+    with at least one 64-point leaf, so some 12,900 level-1 nodes, above what
+    the tree engine's single-workgroup loop holds; the runs engine samples it."""
+    rs = np.random.RandomState(21)
+    pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)
+    rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 128, 128, 128)
+    got = yf.fps(pts, 3000, yf.make_range(*rng))
+    st = yf.last_stats()
+    assert st["engine"] == "runs" and st["n_leaves"] > 64 * 4096
+    assert np.array_equal(got, oracle.fps(pts, 3000, rng))
+
+
+def test_tree_engine_level1_limit_is_reported(yf):
+    """A non-power-of-two grid (tree engine) needing more than 4,096 level-1
+    nodes is refused with a message naming the limit, not sampled wrongly."""
+    rs = np.random.RandomState(22)
+    pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)
+    with pytest.raises(RuntimeError, match="level-1 nodes"):
+        yf.fps(pts, 100, yf.make_range(-1, 1, -1, 1, -1, 1, 100, 100, 100))
+    # the library stays usable after the refusal
+    case = {c.name: c for c in GOLDEN_CASES}["general_10x10x10"]
+    assert np.array_equal(run_module(yf, case), case.expected)
+
+
 def test_shared_buckets_visited_once(yf):
     """Grids whose block counts are not powers of two map several cells to one
     bucket; each bucket of a cube must be updated by one wave only (two waves

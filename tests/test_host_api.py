@@ -121,6 +121,30 @@ def test_capi_rejects_bad_arguments(capi):
     assert rc == 1
 
 
+@pytest.mark.parametrize("blocks", [(1025, 4, 4), (4, 2048, 4), (4, 4, 100000)])
+def test_more_than_1024_blocks_per_axis_is_unsupported(capi, yf, blocks):
+    """The reference accepts any block count (src/yuezu_fps.cpp:45-50, 136-161);
+    this build packs a cell's coordinates 10 bits per axis and refuses larger
+    grids with NSFPS_EUNSUPPORTED and a message naming the limit, before any
+    device work (so the check runs without a GPU)."""
+    capi.nsfps_last_error.restype = ctypes.c_char_p
+    pts = np.random.RandomState(1).rand(100, 3).astype(np.float32)
+    out = np.zeros(100, np.int32)
+    n = ctypes.c_uint64()
+    r = Range(0.0, 1.0, 0.0, 1.0, 0.0, 1.0, *blocks)
+    rc = capi.nsfps_fps(pts.ctypes.data_as(ctypes.c_void_p), ctypes.c_uint64(100),
+                        ctypes.c_uint64(10), ctypes.byref(r), out.ctypes.data_as(ctypes.c_void_p),
+                        ctypes.byref(n))
+    assert rc == 4  # NSFPS_EUNSUPPORTED
+    assert b"above 1024 per axis" in capi.nsfps_last_error()
+    # the module maps it to RuntimeError (not the input-error class)
+    with pytest.raises(RuntimeError, match="above 1024 per axis") as ei:
+        yf.fps(pts, 10, yf.make_range(0, 1, 0, 1, 0, 1, *blocks))
+    assert not isinstance(ei.value, ValueError)
+    # 1024 is still accepted (the trivial identity path needs no device)
+    assert list(yf.fps(pts[:3], 5, yf.make_range(0, 1, 0, 1, 0, 1, 1024, 1, 1))) == [0, 1, 2]
+
+
 def test_module_surface_mirrors_reference(yf):
     for name in ["SpaceRange", "make_range", "make_uniform_range", "fps", "fps_with_bbox",
                  "DEFAULT_X_BLOCKS", "DEFAULT_Y_BLOCKS", "DEFAULT_Z_BLOCKS",
