@@ -254,13 +254,15 @@ def cpu_baseline(w, budget_s=30.0):
     est = t_p * (m / mp) * len(clouds)
     info = cpu_info()
     if est <= budget_s:
-        reps = max(1, min(3, int(budget_s // max(est, 1e-3))))
         times = []
-        for _ in range(reps):
+        while True:
             t = time.perf_counter()
             for P in clouds:
                 runner.fps(P, m, rng, blocks)
             times.append(time.perf_counter() - t)
+            if len(times) == 3 or (len(times) + 1) * times[0] > budget_s:
+                break
+        reps = len(times)
         el = statistics.median(times)
         done = m * len(clouds)
         what = (f"{'all ' + str(len(clouds)) + ' clouds' if len(clouds) > 1 else 'the whole call'} "
@@ -365,6 +367,55 @@ def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
             "exact": exact}
 
 
+# ------------------------------------------------------------ phase clocks
+
+RUN_PHASES = ["load", "select", "gather", "phases", "apply", "tail", "big", "rank", "picks",
+              "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total"]
+
+
+def run_phases(lib, hip, w):
+    """One call with NSFPS_PROFILE=1: the run kernel's phase clocks summed over
+    rounds (s_memtime cycles of wave 0 between its barriers, and s_memrealtime
+    ticks of 10 ns for the load and the whole kernel), per round and per hot
+    set."""
+    os.environ["NSFPS_PROFILE"] = "1"
+    try:
+        P = w["clouds"][0]
+        m = int(w["n_samples"])
+        d_xyz = hip.upload(P)
+        d_out = hip.malloc(m * 4)
+        try:
+            lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
+            st = lib.stats()
+            words = lib.loop_profile()
+        finally:
+            hip.free(d_xyz)
+            hip.free(d_out)
+    finally:
+        del os.environ["NSFPS_PROFILE"]
+    v = dict(zip(RUN_PHASES, words[:16]))
+    rounds = max(1, v["rounds"])
+    hot = max(1, v["hot_sets"])
+    cycles = {k: v[k] for k in ["load", "select", "gather", "rank", "phases", "walk", "apply", "big",
+                                "publish", "tail"]}
+    cyc_total = sum(cycles.values())
+    rt_us = v["rt_total"] * 0.01
+    clock_ghz = cyc_total / (rt_us * 1e3) if rt_us else None
+    return {"workload": w["name"], "profile": "run kernel phase clocks (NSFPS_PROFILE=1)",
+            "rounds": v["rounds"], "hot_sets": v["hot_sets"], "picks": v["picks"],
+            "phases": v["phase_count"], "samples_per_hot_set": round(v["picks"] / hot, 2),
+            "phases_per_hot_set": round(v["phase_count"] / hot, 2),
+            "run_kernel_us_per_round": round(rt_us / rounds, 2),
+            "load_us_per_round": round(v["rt_load"] * 0.01 / rounds, 2),
+            "run_kernel_us_total": round(rt_us, 1),
+            "s_memtime_ghz": round(clock_ghz, 3) if clock_ghz else None,
+            "cycles_per_hot_set": {k: round(cycles[k] / hot, 1) for k in cycles
+                                   if k not in ("load", "tail")},
+            "cycles_per_round": {"load": round(cycles["load"] / rounds, 1),
+                                 "tail": round(cycles["tail"] / rounds, 1)},
+            "sample_ms": round(st["sample_ms"], 3), "device_ms": round(st["device_ms"], 3)}
+
+
 # --------------------------------------------------------------------- lines
 
 def workload_line(lib, hip, yf, wname, budget_s, with_cpu=True):
@@ -425,6 +476,8 @@ def main():
                     help="with --all: comma-separated workloads instead of all five")
     ap.add_argument("--ball-query", action="store_true",
                     help="time only the grouping step after FPS (ball query) and print its line")
+    ap.add_argument("--phases", action="store_true",
+                    help="print the run kernel's phase clocks of one profiled call and exit")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device (a copy kernel of known size for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -454,6 +507,9 @@ def main():
 
     if args.ball_query:
         print(json.dumps(run_ball_query(lib, hip, args.steps)), flush=True)
+        return
+    if args.phases:
+        print(json.dumps(run_phases(lib, hip, make_workload(args.workload))), flush=True)
         return
 
     if args.all:

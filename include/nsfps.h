@@ -50,6 +50,9 @@ typedef struct {
   uint32_t x_blocks, y_blocks, z_blocks;
 } nsfps_range;
 
+/* Number of cube half-width thresholds per axis in nsfps_range_info. */
+#define NSFPS_CUBE_THRESHOLDS 8
+
 /* Derived SpaceRange values (src/yuezu_fps.cpp:7-40, 136-161). */
 typedef struct {
   float inv_bs[3];     /* 1.0f / ((max - min) / (float)blocks) */
@@ -57,6 +60,13 @@ typedef struct {
   uint32_t bits[3];    /* ceil(log2(blocks)), at least 1 */
   uint32_t total_bits;
   uint64_t total_blocks;
+  /* cube_thr[a][k]: the smallest squared distance D >= 0 whose cube
+   * half-width on axis a, min((int)ceilf(sqrtf(D) / block_size[a]),
+   * blocks - 1) (get_morton_codes_in_range, src/yuezu_fps.cpp:564-570, cells
+   * beyond the grid being clipped), is at least k + 1; INFINITY when it never
+   * is.  The half-width is monotone in D, so it equals the number of
+   * thresholds <= D below the last one. */
+  float cube_thr[3][NSFPS_CUBE_THRESHOLDS];
 } nsfps_range_info;
 
 /* Per-call measurements of the last compute call on this thread. */

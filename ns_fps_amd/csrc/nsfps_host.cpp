@@ -85,6 +85,37 @@ nsfps_status check_range(const nsfps_range &r) {
   return NSFPS_OK;
 }
 
+// Cube half-width of get_morton_codes_in_range on one axis (src/yuezu_fps.cpp:
+// 564-570), (int)ceilf(sqrtf(D) / block_size), clipped to blocks - 1 (cells
+// beyond the grid are skipped, :583-589).  IEEE fp32 on the host, exactly as
+// the device's cube_half (correctly rounded sqrtf and division).
+uint32_t cube_half_host(float D, float bs, uint32_t blocks) {
+  const float rad = sqrtf(D < 0.0f ? 0.0f : D);
+  const float f = ceilf(rad / bs);
+  const uint32_t h = !(f < (float)blocks) ? blocks : (uint32_t)f;
+  return h < blocks - 1 ? h : blocks - 1;
+}
+
+// Smallest D >= 0 whose half-width is at least k1 (INFINITY when none is).
+// The half-width is monotone in D (sqrtf, division by a positive value and
+// ceilf are monotone), and non-negative floats order like their bit
+// patterns, so a binary search over the bits finds the first one.
+float cube_threshold(float bs, uint32_t blocks, uint32_t k1) {
+  if (k1 > blocks - 1) return INFINITY;
+  auto as_float = [](uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+  };
+  uint32_t lo = 0, hi = 0x7f800000u;  // +inf: half-width blocks - 1 >= k1
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (cube_half_host(as_float(mid), bs, blocks) >= k1) hi = mid;
+    else lo = mid + 1;
+  }
+  return as_float(lo);
+}
+
 // make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
 // _compute_bit_positions/_generate_morton_lut (:52-97).
 void derive(const nsfps_range &r, HostRange &h) {
@@ -137,6 +168,13 @@ void derive(const nsfps_range &r, HostRange &h) {
   d.lut_total = off;
   d.T = (uint32_t)h.info.total_blocks;
   d.bijective = bij ? 1u : 0u;
+  static_assert(kCubeThr == NSFPS_CUBE_THRESHOLDS, "threshold count");
+  for (int a = 0; a < 3; ++a)
+    for (uint32_t k = 0; k < kCubeThr; ++k) {
+      const float t = cube_threshold(h.info.block_size[a], bl[a], k + 1);
+      h.info.cube_thr[a][k] = t;
+      d.cube_thr[a][k] = t;
+    }
 }
 
 // compute_bbox (src/yuezu_fps.cpp:648-670) keeps, per axis, the running

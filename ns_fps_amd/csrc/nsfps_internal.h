@@ -33,6 +33,10 @@ constexpr uint32_t kHistBins = 4096;
 constexpr uint32_t kHists = 3;
 constexpr uint32_t kRefinePasses = 2;  // refinement passes when they are launched
 
+// Cube half-width thresholds kept per axis (half-widths up to this many are
+// found by comparisons; larger ones by the reference's arithmetic).
+constexpr uint32_t kCubeThr = 8;
+
 // Range values the kernels need, all derived on the host exactly as the
 // reference derives them (src/yuezu_fps.cpp:7-11, 136-161, 170-193).
 struct RangeDev {
@@ -45,6 +49,8 @@ struct RangeDev {
   uint32_t lut_total;
   uint32_t T;           // total blocks = number of buckets
   uint32_t bijective;   // 1 when bucket <-> cell is one-to-one
+  // cube half-width thresholds: half-width >= k + 1 exactly when D >= cube_thr[a][k]
+  float cube_thr[3][kCubeThr];
 };
 
 // Byte offsets inside the dynamic LDS of the single-workgroup loop; kNone

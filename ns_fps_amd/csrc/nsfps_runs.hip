@@ -547,8 +547,11 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // its distance down.  Every copy ranked above the first lowered one is a
 // sample, in rank order: all copies ranked above it are samples too, a copy
 // lowered by one of them started below it, and the rest of the list is below
-// H.  So a phase takes that whole prefix at once, applies its cubes to the
-// remaining copies, and ranks again, until no copy is >= max(H, B).  Then the
+// H.  The copies that are not lowered go on being samples past a lowered copy
+// j as long as they exceed K_j, j's key once every copy above it that is not
+// lowered has been applied (j's key can only be lower when their turn
+// comes).  So a phase takes those samples at once, applies their cubes to
+// the remaining copies, and ranks again, until no copy is >= max(H, B).  Then the
 // hot run's samples are applied to every list entry (a
 // sample with a small cube is applied by one quad walking its rows of the
 // cell index, one with a large cube by every thread to its own entries) and
@@ -574,7 +577,10 @@ static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 // rounds into the cloud's profile words) when PROF is set.
 enum : uint32_t {
   kRpLoad = 0, kRpSelect, kRpGather, kRpPhases, kRpApply, kRpTail, kRpBig, kRpRank,
-  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWalk, kRpPublish, kRpWords = 16
+  kRpPicks = 8, kRpRounds, kRpHotRounds, kRpPhaseCount, kRpWalk, kRpPublish,
+  kRpRtLoad = 14,  // s_memrealtime ticks (100 MHz) from the kernel's start to the end of the load
+  kRpRtTotal = 15, //   and to the kernel's end
+  kRpWords = 16
 };
 
 // Cell inside the cube of a sample at cell qc with packed half-widths h
@@ -615,14 +621,47 @@ __device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b
   hi_c = pack_cell(min(qcx + g0, b0 - 1), min(qcy + g1, b1 - 1), min(qcz + g2, b2 - 1));
 }
 
-// Cube half-widths of a sample with distance D (src/yuezu_fps.cpp:564-570),
-// packed 10 bits per axis; at or beyond the grid they select the same cells
-// as blocks - 1.
-__device__ __forceinline__ uint32_t packed_halves(const RangeDev &r, float D) {
-  return min((uint32_t)cube_half(D, r.bsize[0], r.blocks[0]), r.blocks[0] - 1) |
-         (min((uint32_t)cube_half(D, r.bsize[1], r.blocks[1]), r.blocks[1] - 1) << 10) |
-         (min((uint32_t)cube_half(D, r.bsize[2], r.blocks[2]), r.blocks[2] - 1) << 20);
+// Cube half-width of a sample with distance D on axis a (src/yuezu_fps.cpp:
+// 564-570), clipped to blocks - 1 (at or beyond the grid it selects the same
+// cells).  The half-width is monotone in D: below the last of the range's
+// thresholds it is the number of thresholds <= D (no square root or
+// division); above it, the reference's arithmetic (correctly rounded sqrtf
+// and division, as on the host that derived the thresholds).
+__device__ __forceinline__ uint32_t half_axis(const RangeDev &r, int a, float D) {
+  uint32_t h = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < kCubeThr; ++k) h += D >= r.cube_thr[a][k] ? 1u : 0u;
+  if (h == kCubeThr) h = min((uint32_t)cube_half(D, r.bsize[a], r.blocks[a]), r.blocks[a] - 1);
+  return h;
 }
+
+// The three half-widths packed 10 bits per axis.
+__device__ __forceinline__ uint32_t packed_halves(const RangeDev &r, float D) {
+  return half_axis(r, 0, D) | (half_axis(r, 1, D) << 10) | (half_axis(r, 2, D) << 20);
+}
+
+// The first three thresholds of every axis, in scalar registers.  Below the
+// third of every axis (half-widths of at most 2: the common case once cubes
+// are small) the packed half-widths take two comparisons per axis.
+struct SmallHalves {
+  float t[3][3];
+  __device__ __forceinline__ explicit SmallHalves(const RangeDev &r) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) t[a][k] = r.cube_thr[a][k];
+  }
+  __device__ __forceinline__ bool covers(float D) const {
+    return D < t[0][2] && D < t[1][2] && D < t[2][2];
+  }
+  __device__ __forceinline__ uint32_t packed(float D) const {
+    uint32_t h = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+      h |= ((D >= t[a][0] ? 1u : 0u) + (D >= t[a][1] ? 1u : 0u)) << (10 * a);
+    return h;
+  }
+};
 
 // LDS slot of hot copy i.  Lane q of a copy's group compares against copies
 // q * kCmp + u; the kCopyLanes copies read together for one u sit side by
@@ -679,6 +718,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
                                         //   distance bits}; key 0 once taken
   __shared__ __align__(16) uint32_t s_rank[kHot];  // rank of each hot copy in the phase
   __shared__ unsigned long long s_lowm[2];  // bit r: the copy ranked r is lowered
+  __shared__ unsigned long long s_lowc[2];  // bit j: hot copy j is lowered
+  __shared__ uint32_t s_stop[2];            // the first rank a lowered copy holds back
   __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
                                         //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
@@ -692,6 +733,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
   __shared__ uint32_t s_wr[2][kRunWaves][2];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
+  const uint64_t rt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
@@ -836,6 +878,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
   const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
   const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
   NSFPS_RMARK(kRpLoad);
+  if (PROF) pf[kRpRtLoad] = __builtin_amdgcn_s_memrealtime() - rt0;
   while (true) {
     uint64_t key[kOwnSlots];
     bool live[kOwnSlots];
@@ -927,12 +970,18 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       if (tid < 2) s_big[tid] = 0;
       if (tid == 0) {
         s_lowm[0] = 0;
+        s_lowc[0] = 0;
+        s_stop[0] = kHot;
         s_kmr = 0;
       }
       __syncthreads();
       if (wave == 0 && lane < min(s_nhot, kHot)) {
         const uint4 hx = s_hx[lane];
-        const uint32_t h = packed_halves(c.r, __uint_as_float(hx.z));
+        const float D = __uint_as_float(hx.z);
+        const SmallHalves sh(c.r);
+        uint32_t h;
+        if (sh.covers(D)) h = sh.packed(D);
+        else h = packed_halves(c.r, D);
         uint32_t lo_c, hi_c;
         cube_corners(hx.x, h, b0, b1, b2, lo_c, hi_c);
         s_hq[0][hot_slot(lane)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hx.y, hx.z);
@@ -974,9 +1023,8 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       uint32_t low = 0;
       if (cand) {  // rare: the exact distance decides
         const uint4 pj = s_hp[hj];
-        while (cand) {
-          const uint32_t u = (uint32_t)__builtin_ctz(cand);
-          cand &= cand - 1;
+        for (uint32_t cm = cand; cm; cm &= cm - 1) {
+          const uint32_t u = (uint32_t)__builtin_ctz(cm);
           const uint4 pi = s_hp[hq * kCmp + u];
           const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
                                   __uint_as_float(pj.z), __uint_as_float(pi.x),
@@ -990,18 +1038,24 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
       const bool ge = mkey >= hth;
       if (rep) s_rank[hj] = rank;
       if (hq == 0 && !remj) s_rank[hj] = kHot;  // never accepted
-      if (rep && lowered) atomicOr(&s_lowm[ph], 1ull << rank);
+      if (rep && lowered) {
+        atomicOr(&s_lowm[ph], 1ull << rank);
+        atomicOr(&s_lowc[ph], 1ull << hj);
+      }
       const uint32_t wge = (uint32_t)__popcll(__ballot(rep && ge));
       const uint32_t wnz = (uint32_t)__popcll(__ballot(rep && ge && me.w != 0u));
       if (lane == 0) {
         s_wr[ph][wave][0] = wge;
         s_wr[ph][wave][1] = wnz;
       }
-      if (tid == 0) s_lowm[ph ^ 1] = 0;
+      if (tid == 0) {
+        s_lowm[ph ^ 1] = 0;
+        s_lowc[ph ^ 1] = 0;
+        s_stop[ph ^ 1] = kHot;
+      }
       __syncthreads();
       NSFPS_RMARK(kRpRank);
-      // prefix length: first lowered rank, copies >= the hot threshold with
-      // distance > 0 (a rank prefix), samples left
+      // copies >= the hot threshold with distance > 0 are ranks 0 .. nnz - 1
       const unsigned long long lowm = s_lowm[ph];
       uint32_t nge = 0, nnz = 0;
 #pragma unroll
@@ -1009,18 +1063,55 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         nge += s_wr[ph][w][0];
         nnz += s_wr[ph][w][1];
       }
-      const uint32_t plow = lowm ? (uint32_t)__builtin_ctzll(lowm) : kHot;
-      const uint32_t P = min(min(plow, nnz), room - npk);
-      if (P == 0) {  // rank 0: below the hot threshold, or distance 0, or no room
+      // A lowered copy j bounds the samples of the phase by K_j, its key once
+      // every copy above it that is not lowered is a sample (more samples
+      // only lower it further): ranks at or below K_j wait for the next phase.
+      uint32_t sstop = kHot;
+      if (lowm) {
+        if (remj && lowered) {  // the whole group of a lowered copy
+          const uint32_t lowc = (uint32_t)(s_lowc[ph] >> (hq * kCmp));
+          uint32_t nk = me.w;
+          uint32_t nm = cand & ~lowc & ((1u << kCmp) - 1u);
+          if (nm) {
+            const uint4 pj = s_hp[hj];
+            for (; nm; nm &= nm - 1) {
+              const uint32_t u = (uint32_t)__builtin_ctz(nm);
+              const uint4 pi = s_hp[hq * kCmp + u];
+              const float dd = sqdist(__uint_as_float(pj.x), __uint_as_float(pj.y),
+                                      __uint_as_float(pj.z), __uint_as_float(pi.x),
+                                      __uint_as_float(pi.y), __uint_as_float(pi.z));
+              nk = min(nk, __float_as_uint(dd));  // non-negative floats order like their bits
+            }
+          }
+          const uint64_t K = ((uint64_t)group_min(nk) << 32) | me.z;
+          uint32_t above = 0;
+#pragma unroll
+          for (uint32_t u = 0; u < kCmp; ++u)
+            above += (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > K);
+          const uint32_t tj = group_sum(above);  // the first rank at or below K_j
+          if (hq == 0) atomicMin(&s_stop[ph], tj);
+        }
+        __syncthreads();
+        sstop = s_stop[ph];
+      }
+      // the samples: copies not lowered, ranked below min(stop, nnz), the
+      // first room - npk of them, in rank order
+      const uint32_t seff = min(sstop, nnz);
+      uint64_t accr = (seff >= 64 ? ~0ull : ((1ull << seff) - 1ull)) & ~lowm;  // by rank
+      uint32_t P = (uint32_t)__popcll(accr);
+      while (P > room - npk) {  // the last samples of the call
+        accr &= ~(1ull << (63 - __clzll(accr)));
+        --P;
+      }
+      if (P == 0) {  // rank 0: below the hot threshold, or distance 0
         stop = (nge == 0) ? 1u : 2u;
         break;
       }
-      // the prefix: samples npk .. npk + P - 1 in rank order
-      const bool acc = remj && rank < P;
+      const bool acc = remj && rank < kHot && ((accr >> rank) & 1u);
       if (acc) {
         my_acc = true;
         my_key = 0;
-        my_out = npk + rank;
+        my_out = npk + (uint32_t)__popcll(accr & ((1ull << rank) - 1ull));
         my_qc = mx.x;
         my_hh = mx.w;
       }
@@ -1053,7 +1144,9 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
         uint32_t cand2 = 0;
 #pragma unroll
         for (uint32_t u = 0; u < kCmp; ++u)
-          cand2 |= ((uint32_t)(rk[u] < P) & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
+          cand2 |= ((rk[u] < kHot ? (uint32_t)(accr >> rk[u]) & 1u : 0u) &
+                    in_box11(mx.y, mx.z, og[u].x, og[u].y))
+                   << u;
         if (cand2) {  // rare: the exact distances
           const uint4 pj = s_hp[hj];
           while (cand2) {
@@ -1221,6 +1314,7 @@ __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict_
     NSFPS_RMARK(kRpTail);
     pf[kRpPicks] = np;
     pf[kRpRounds] = 1;
+    pf[kRpRtTotal] = __builtin_amdgcn_s_memrealtime() - rt0;
     NSFPS_GLOBAL uint64_t *pw = gptr(c.prof);
     for (uint32_t i = 0; i < kRpWords; ++i) pw[i] += pf[i];
   }

@@ -25,7 +25,7 @@ class Range(ctypes.Structure):
 class RangeInfo(ctypes.Structure):
     _fields_ = [("inv_bs", ctypes.c_float * 3), ("block_size", ctypes.c_float * 3),
                 ("bits", ctypes.c_uint32 * 3), ("total_bits", ctypes.c_uint32),
-                ("total_blocks", ctypes.c_uint64)]
+                ("total_blocks", ctypes.c_uint64), ("cube_thr", (ctypes.c_float * 8) * 3)]
 
 
 def declared_symbols():
@@ -64,6 +64,54 @@ def test_capi_range_derive_matches_oracle(capi, oracle):
             assert list(luts[off:off + n]) == list(o["luts"][a])
             off += n
         assert info.total_blocks == rng[6] * rng[7] * rng[8]
+
+
+def numpy_half_width(D, bs, blocks):
+    """get_morton_codes_in_range's half-width (src/yuezu_fps.cpp:564-570) in
+    NumPy float32: ceil(sqrtf(D) / block_size), clipped to blocks - 1."""
+    D = np.asarray(D, np.float32)
+    f = np.ceil(np.sqrt(D) / np.float32(bs)).astype(np.float64)
+    return np.minimum(f, blocks - 1).astype(np.int64)
+
+
+@pytest.mark.parametrize("rng", [(-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 32, 32, 32),
+                                 (-80.0, 80.0, -80.0, 80.0, -4.0, 4.0, 32, 32, 8),
+                                 (-100.0, 100.0, -100.0, 100.0, -100.0, 100.0, 16, 16, 16),
+                                 (-600.0, 600.0, -600.0, 600.0, -600.0, 600.0, 64, 64, 64),
+                                 (-5.0, 7.0, 0.0, 1.0, -2.0, 2.0, 10, 3, 1),
+                                 (0.0, 1e-3, 0.0, 3.0, 0.0, 7.0, 1024, 5, 2)])
+def test_cube_thresholds_match_the_reference_half_width(capi, rng):
+    """The range's cube thresholds: half-width k + 1 starts exactly at
+    cube_thr[k] (the float below gives less), and below the last threshold
+    the half-width of any D is the number of thresholds <= D -- checked
+    against the reference's arithmetic restated in NumPy float32 on
+    thresholds, their neighbours and random distances over 40 binades."""
+    info = RangeInfo()
+    assert capi.nsfps_range_derive(ctypes.byref(Range(*rng)), ctypes.byref(info), None,
+                                   ctypes.c_uint64(0)) == 0
+    rs = np.random.RandomState(5)
+    for a in range(3):
+        b = rng[6 + a]
+        bs = np.float32(info.block_size[a])
+        thr = np.array(list(info.cube_thr[a]), np.float32)
+        for k, t in enumerate(thr):
+            if k + 1 > b - 1:
+                assert np.isinf(t)
+                continue
+            assert np.isfinite(t) and numpy_half_width(t, bs, b) >= k + 1
+            below = np.nextafter(t, np.float32(0)) if t > 0 else None
+            if below is not None:
+                assert numpy_half_width(below, bs, b) < k + 1
+        D = np.concatenate([thr[np.isfinite(thr)],
+                            np.nextafter(thr[np.isfinite(thr)], np.float32(0)),
+                            (np.float32(bs) ** 2 * np.float32(10.0) **
+                             rs.uniform(-6, 3, 20000)).astype(np.float32),
+                            np.array([0.0, 1e-45, 1e-38], np.float32)])
+        h = numpy_half_width(D, bs, b)
+        count = (D[:, None] >= thr[None, :]).sum(1)
+        low = D < thr[-1] if np.isfinite(thr[-1]) else np.ones(len(D), bool)
+        assert np.array_equal(count[low], h[low])
+        assert np.all(h[~low] >= 8)
 
 
 def _capi_bbox(capi, pts):
