@@ -19,6 +19,10 @@
  *   nsfps_fps_device     yuezu_fps() on device-resident input (cf. the
  *                        reference GPU driver's FpsGPU::sample,
  *                        eval/src_gpu/yuezu_fps_gpu.h:90-126)
+ *   nsfps_plan_create / _sample / _destroy
+ *                        the reference GPU driver's FpsGPU::initialize /
+ *                        sample and its teardown (eval/src_gpu/yuezu_fps_gpu.h:
+ *                        90-126): build once, sample many times
  *   nsfps_gather_points, nsfps_ball_query (and _device)
  *                        no counterpart: the grouping step the reference's
  *                        callers run on its output (see their declarations)
@@ -143,6 +147,25 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
 nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples,
                               const nsfps_range *range, int32_t *d_out,
                               uint64_t *out_len, void *stream);
+
+/* A cloud built once and sampled many times, the split of the reference GPU
+ * driver's FpsGPU::initialize / FpsGPU::sample (eval/src_gpu/yuezu_fps_gpu.h:
+ * 90-126).  nsfps_plan_create builds the structure of n points (xyz: host
+ * pointer, or a device pointer when on_device != 0; read during the call
+ * only) on the current device, in device memory the plan owns.
+ * nsfps_plan_sample restores the points' min-distances and keys and runs the
+ * sampling alone: the samples of nsfps_fps on the same points and range, for
+ * any n_samples, written to device memory d_out (n_samples int32) on stream
+ * (a hipStream_t, NULL = default stream); it returns after the stream work
+ * completes and must be called with the plan's device current.  Calls on one
+ * plan, or on several, are serialised by the library's lock.
+ * nsfps_plan_destroy frees the plan (NULL is ignored). */
+typedef struct nsfps_plan_s nsfps_plan;
+nsfps_status nsfps_plan_create(const float *xyz, uint64_t n, const nsfps_range *range,
+                               int on_device, nsfps_plan **plan);
+nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t n_samples, int32_t *d_out,
+                               uint64_t *out_len, void *stream);
+void nsfps_plan_destroy(nsfps_plan *plan);
 
 /* The step after sampling: set-abstraction grouping on the samples.  No
  * counterpart in the reference, which stops at the indices; the next step of

@@ -110,6 +110,31 @@ class Lib:
                                               ctypes.byref(n_out), _vp(stream)))
         return n_out.value
 
+    def plan_create(self, xyz, n, rng, on_device=False):
+        """nsfps_plan_create: xyz is a device pointer (int) when on_device,
+        else a host (N, 3) float32 array.  Returns the plan handle."""
+        plan = _vp()
+        if on_device:
+            ptr = _vp(xyz)
+        else:
+            arr = np.ascontiguousarray(xyz, dtype=np.float32)
+            n = len(arr)
+            ptr = arr.ctypes.data_as(_vp)
+        self._check(self.lib.nsfps_plan_create(ptr, _u64(n), ctypes.byref(Range.of(rng)),
+                                               ctypes.c_int(1 if on_device else 0),
+                                               ctypes.byref(plan)))
+        return plan.value
+
+    def plan_sample(self, plan, n_samples, d_out, stream=None):
+        n_out = _u64()
+        self._check(self.lib.nsfps_plan_sample(_vp(plan), _u64(int(n_samples)), _vp(d_out),
+                                               ctypes.byref(n_out), _vp(stream)))
+        return n_out.value
+
+    def plan_destroy(self, plan):
+        self.lib.nsfps_plan_destroy.restype = None
+        self.lib.nsfps_plan_destroy(_vp(plan))
+
     def gather_points(self, points, idx):
         p = np.ascontiguousarray(points, dtype=np.float32)
         ix = np.ascontiguousarray(idx, dtype=np.int32).ravel()

@@ -473,9 +473,24 @@ __global__ void k_init_state(CloudDev c, const uint32_t *__restrict__ phys0) {
   if (threadIdx.x == 0 && blockIdx.x == 0) init_state_of(c, phys0);
 }
 
+// Fills 32-bit words (clears flags, counters and tables with a kernel, not a
+// memset node, so that the call path holds no hipMemsetAsync).
+__global__ void k_fill_u32(uint32_t *__restrict__ p, uint32_t value, uint64_t words) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride)
+    p[i] = value;
+}
+
 // ---------------------------------------------------------------- launchers
 
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t st) {
+  if (words == 0) return hipSuccess;
+  const uint64_t blocks = (words + 255) / 256;
+  k_fill_u32<<<(uint32_t)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>((uint32_t *)p, value, words);
+  return hipGetLastError();
+}
 
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,

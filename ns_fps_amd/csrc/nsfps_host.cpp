@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -624,8 +625,8 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
   const uint32_t n = p.n, T = p.rng.dev.T;
   const float *xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
   if (c.padded) {
-    HIP_TRY(hipMemsetAsync(c.P4, 0, (size_t)c.nslots * sizeof(float4), st));
-    HIP_TRY(hipMemsetAsync(const_cast<uint2 *>(c.RO), 0, (size_t)c.nslots * sizeof(uint2), st));
+    HIP_TRY(launch_fill_u32(c.P4, 0u, (uint64_t)c.nslots * 4, st));
+    HIP_TRY(launch_fill_u32(const_cast<uint2 *>(c.RO), 0u, (uint64_t)c.nslots * 2, st));
   }
   HIP_TRY(launch_gather(prank, lorig, base, p.d_bucket, p.d_counts, xyz, n, c.padded,
                         (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), p.d_small + 2, st));
@@ -658,8 +659,8 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
         HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)p.n * 12, hipMemcpyHostToDevice,
                                st));
   }
-  HIP_TRY(hipMemsetAsync(cb.counts, 0, cb.counts_total * 4, st));
-  HIP_TRY(hipMemsetAsync(cb.small, 0, nc * 16, st));
+  HIP_TRY(launch_fill_u32(cb.counts, 0u, cb.counts_total, st));
+  HIP_TRY(launch_fill_u32(cb.small, 0u, nc * 4, st));
   // many clouds sorted together, of few buckets each: one launch per build
   // step for all of them
   uint32_t nmax = 0, tmax = 0;
@@ -867,135 +868,158 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   return NSFPS_OK;
 }
 
-// Builds every cloud, then samples: grid-wide steps for the first iterations
-// of a single cloud, then one single-workgroup loop launch for all clouds.
-nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, bool out_on_host,
-                        int32_t *h_out, uint64_t out_stride, uint64_t *out_lens) {
-  auto t0 = std::chrono::steady_clock::now();
-  Arena *ap = nullptr;
-  nsfps_status rc = arena_for_device(&ap);
-  if (rc) return rc;
-  Arena &a = *ap;
-  hipStream_t st = user_stream ? user_stream : a.stream;
+// Device memory and stream of one call: the cached per-device arena (grown on
+// demand), a plan's own allocation, or the allocation-free entry point's
+// static scratch array.  ev: five events timing the phases, or null.
+struct Ws {
+  char *base = nullptr;
+  size_t cap = 0;
+  hipStream_t st = nullptr;
+  const hipEvent_t *ev = nullptr;
+};
+
+// Where one call's buffers live: per cloud (layout_cloud), for the call
+// (layout_call), the sorts' scratch, and the per-cloud descriptors and status
+// words the sampling kernels read.
+struct CallLayout {
+  CallBuffers cb{};
+  Scratch sc{};
+  CloudDev *d_clouds = nullptr;
+  CloudStatus *d_status = nullptr;
+  uint32_t nsort = 0, tmax = 0;
+};
+
+// Lays the call out over bp (a null base measures it).
+void layout_all(Bump &bp, std::vector<CloudPlan> &plans, CallLayout &L) {
+  for (auto &p : plans) layout_cloud(bp, p);
+  layout_call(bp, plans, L.cb);
+  layout_scratch(bp, L.nsort, L.tmax, L.sc);
+  L.d_clouds = bp.take<CloudDev>(plans.size());
+  L.d_status = bp.take<CloudStatus>(plans.size());
+  if (bp.base)
+    for (size_t i = 0; i < plans.size(); ++i) {
+      plans[i].dev.done = &L.d_status[i].done;
+      plans[i].dev.iter = &L.d_status[i].iter;
+      plans[i].dev.rs = &L.d_status[i].rs;
+    }
+}
+
+// Bytes of layout_all for these clouds (and the sort sizes it uses).
+size_t measure_call(std::vector<CloudPlan> &plans, CallLayout &L) {
   uint32_t nmax = 0, tmax = 0;
   for (auto &p : plans) {
     nmax = std::max(nmax, p.n);
     tmax = std::max(tmax, p.rng.dev.T);
   }
   // sorts run over one cloud, or over all clouds of a call at once
-  const uint32_t nsort = std::max<uint64_t>(nmax, (uint64_t)nmax * plans.size()) <= 0x7fffffffu
-                             ? (uint32_t)std::max<uint64_t>(nmax, (uint64_t)nmax * plans.size())
-                             : nmax;
+  const uint64_t all = (uint64_t)nmax * plans.size();
+  L.nsort = all <= 0x7fffffffu ? (uint32_t)std::max<uint64_t>(nmax, all) : nmax;
+  L.tmax = tmax;
   Bump meas(nullptr);
-  for (auto &p : plans) layout_cloud(meas, p);
-  CallBuffers cb{};
-  layout_call(meas, plans, cb);
-  Scratch sc{};
-  layout_scratch(meas, nsort, tmax, sc);
-  meas.take<CloudDev>(plans.size());
-  meas.take<CloudStatus>(plans.size());
-  rc = arena_reserve(a, meas.off + 4096);
-  if (rc) return rc;
-  Bump bp(a.base);
-  for (auto &p : plans) layout_cloud(bp, p);
-  layout_call(bp, plans, cb);
-  layout_scratch(bp, nsort, tmax, sc);
-  CloudDev *d_clouds = bp.take<CloudDev>(plans.size());
-  CloudStatus *d_status = bp.take<CloudStatus>(plans.size());
-  for (size_t i = 0; i < plans.size(); ++i) {
-    plans[i].dev.done = &d_status[i].done;
-    plans[i].dev.iter = &d_status[i].iter;
-    plans[i].dev.rs = &d_status[i].rs;
-  }
+  layout_all(meas, plans, L);
+  return meas.off + 4096;
+}
 
-  // the engine: speculative runs where every cloud's bucket <-> cell map is
-  // one-to-one, the tree loop otherwise (or when NSFPS_ENGINE=tree asks)
+// The engine: speculative runs where every cloud's bucket <-> cell map is
+// one-to-one, the tree loop otherwise (or when NSFPS_ENGINE=tree asks).
+bool choose_runs(std::vector<CloudPlan> &plans) {
   bool runs = true;
   for (auto &p : plans) runs = runs && p.rng.dev.bijective;
   const char *eng = getenv("NSFPS_ENGINE");
   if (eng && strcmp(eng, "tree") == 0) runs = false;
   for (auto &p : plans) p.tree = !runs;
+  return runs;
+}
 
-  HIP_TRY(hipEventRecord(a.ev[0], st));
-  uint64_t leaves = 0, points = 0, wide_total = 0;
+// Samples the built clouds (descriptors in plans[i].dev): grid-wide steps for
+// the first iterations of a single cloud on the tree engine, then its loop;
+// or the speculative-run rounds.
+nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
+                           bool runs, uint64_t *rounds, uint64_t *wide_total) {
+  hipStream_t st = ws.st;
+  std::vector<CloudDev> devs;
   uint32_t lds_bytes = 0;
-  std::vector<BuildDev> bd_host;  // lives until the stream is synchronised below
-  rc = build_clouds(plans, cb, sc, bd_host, st);
-  if (rc) return rc;
   for (auto &p : plans) {
-    leaves += p.dev.nleaves;
-    points += p.n;
+    devs.push_back(p.dev);
     lds_bytes = std::max(lds_bytes, p.dev.lds.total);
   }
-  HIP_TRY(hipEventRecord(a.ev[1], st));
-  std::vector<CloudDev> devs;
-  for (auto &p : plans) devs.push_back(p.dev);
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
-  uint64_t rounds = 0;
+  *rounds = 0;
+  *wide_total = 0;
   if (runs) {
-    HIP_TRY(hipEventRecord(a.ev[3], st));
-    HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
+    if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[3], st));
+    HIP_TRY(hipMemcpyAsync(L.d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                            hipMemcpyHostToDevice, st));
-    HIP_TRY(hipEventRecord(a.ev[4], st));
-    if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
-    rc = run_rounds(plans, d_clouds, d_status, st, profile, &rounds);
-    if (rc) return rc;
-  } else {
-    if (plans.size() == 1) {
-      uint32_t e = wide_iters_for(plans[0]);
-      wide_total = e;
-      if (e)
-        HIP_TRY(launch_wide_steps(plans[0].dev, e, std::max<uint32_t>(1, plans[0].dev.nl1), st));
-    }
-    HIP_TRY(hipEventRecord(a.ev[3], st));
-    HIP_TRY(hipMemcpyAsync(d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
-                           hipMemcpyHostToDevice, st));
-    HIP_TRY(hipEventRecord(a.ev[4], st));
-    if (profile) HIP_TRY(hipMemsetAsync(plans[0].dev.prof, 0, kProfWords * 8, st));
-    const char *lt = getenv("NSFPS_LATE_THREADS");
-    const uint32_t late_threads = (lt && atoi(lt) == 1024) ? 1024u : kLateThreads;
-    HIP_TRY(launch_late_loop(d_clouds, (uint32_t)plans.size(), lds_bytes, profile, late_threads,
-                             st));
+    if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
+    if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
+    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds);
   }
-  HIP_TRY(hipEventRecord(a.ev[2], st));
+  if (plans.size() == 1) {
+    uint32_t e = wide_iters_for(plans[0]);
+    *wide_total = e;
+    if (e) HIP_TRY(launch_wide_steps(plans[0].dev, e, std::max<uint32_t>(1, plans[0].dev.nl1), st));
+  }
+  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[3], st));
+  HIP_TRY(hipMemcpyAsync(L.d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
+                         hipMemcpyHostToDevice, st));
+  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
+  if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
+  const char *lt = getenv("NSFPS_LATE_THREADS");
+  const uint32_t late_threads = (lt && atoi(lt) == 1024) ? 1024u : kLateThreads;
+  HIP_TRY(launch_late_loop(L.d_clouds, (uint32_t)plans.size(), lds_bytes, profile, late_threads,
+                           st));
+  return NSFPS_OK;
+}
+
+// After sampling: lengths, the samples to the host (out_on_host) and the
+// statistics of the call (t0: host time at its start).
+nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
+                         bool runs, uint64_t rounds, uint64_t wide_total, bool out_on_host,
+                         int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
+                         std::chrono::steady_clock::time_point t0) {
+  hipStream_t st = ws.st;
+  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[2], st));
   std::vector<CloudStatus> fin(plans.size());
-  HIP_TRY(hipMemcpyAsync(fin.data(), d_status, fin.size() * sizeof(CloudStatus),
+  HIP_TRY(hipMemcpyAsync(fin.data(), L.d_status, fin.size() * sizeof(CloudStatus),
                          hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
-  std::vector<uint32_t> lens(plans.size());
-  for (size_t i = 0; i < plans.size(); ++i) lens[i] = fin[i].iter;
-  uint64_t samples = 0;
-  uint32_t maxlen = 0;
+  uint64_t samples = 0, leaves = 0, points = 0;
+  uint32_t maxlen = 0, lds_bytes = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
-    out_lens[i] = lens[i];
-    samples += lens[i];
-    maxlen = std::max(maxlen, lens[i]);
+    out_lens[i] = fin[i].iter;
+    samples += fin[i].iter;
+    maxlen = std::max(maxlen, fin[i].iter);
+    leaves += plans[i].dev.nleaves;
+    points += plans[i].n;
+    lds_bytes = std::max(lds_bytes, plans[i].dev.lds.total);
   }
   if (out_on_host && maxlen) {
     if (plans.size() > 1 && out_stride == plans[0].m) {
       // rows of m entries on both sides: one copy (entries past a cloud's
       // length are left unspecified, as the interface says)
-      HIP_TRY(hipMemcpyAsync(h_out, cb.out, plans.size() * (size_t)out_stride * 4,
+      HIP_TRY(hipMemcpyAsync(h_out, L.cb.out, plans.size() * (size_t)out_stride * 4,
                              hipMemcpyDeviceToHost, st));
     } else {
       for (size_t i = 0; i < plans.size(); ++i)
-        if (lens[i])
-          HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out, (size_t)lens[i] * 4,
-                                 hipMemcpyDeviceToHost, st));
+        if (fin[i].iter)
+          HIP_TRY(hipMemcpyAsync(h_out + i * out_stride, plans[i].dev.out,
+                                 (size_t)fin[i].iter * 4, hipMemcpyDeviceToHost, st));
     }
   }
-  if (profile)
+  if (getenv("NSFPS_PROFILE"))
     HIP_TRY(hipMemcpyAsync(g_prof, plans[0].dev.prof, sizeof(g_prof), hipMemcpyDeviceToHost, st));
   else
     memset(g_prof, 0, sizeof(g_prof));
   HIP_TRY(hipStreamSynchronize(st));
   auto t1 = std::chrono::steady_clock::now();
   nsfps_stats &S = g_stats;
-  S.build_ms = ms_between(a.ev[0], a.ev[1]);
-  S.sample_ms = ms_between(a.ev[1], a.ev[2]);
-  S.wide_ms = ms_between(a.ev[1], a.ev[3]);
-  S.late_ms = ms_between(a.ev[4], a.ev[2]);
-  S.device_ms = S.build_ms + S.sample_ms;
+  if (ws.ev) {
+    S.build_ms = ms_between(ws.ev[0], ws.ev[1]);
+    S.sample_ms = ms_between(ws.ev[1], ws.ev[2]);
+    S.wide_ms = ms_between(ws.ev[1], ws.ev[3]);
+    S.late_ms = ms_between(ws.ev[4], ws.ev[2]);
+    S.device_ms = S.build_ms + S.sample_ms;
+  }
   S.e2e_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   S.n_points = points;
   S.n_clouds = plans.size();
@@ -1007,6 +1031,44 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, hipStream_t user_stream, 
   S.rounds = rounds;
   S.engine = runs ? 1u : 0u;
   return NSFPS_OK;
+}
+
+// One call from start to end over workspace ws: layout, build, sampling,
+// results.  ws.base == null takes the calling thread's device arena.
+nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, int32_t *h_out,
+                        uint64_t out_stride, uint64_t *out_lens) {
+  auto t0 = std::chrono::steady_clock::now();
+  CallLayout L;
+  const size_t need = measure_call(plans, L);
+  if (!ws.base) {
+    Arena *ap = nullptr;
+    nsfps_status rc = arena_for_device(&ap);
+    if (rc) return rc;
+    rc = arena_reserve(*ap, need);
+    if (rc) return rc;
+    ws.base = ap->base;
+    ws.cap = ap->cap;
+    if (!ws.st) ws.st = ap->stream;
+    ws.ev = ap->ev;
+  } else if (need > ws.cap) {
+    return fail(NSFPS_EUNSUPPORTED,
+                "the call needs %zu bytes of device workspace, more than the %zu available",
+                need, ws.cap);
+  }
+  Bump bp(ws.base);
+  layout_all(bp, plans, L);
+  const bool runs = choose_runs(plans);
+  hipStream_t st = ws.st;
+  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[0], st));
+  std::vector<BuildDev> bd_host;  // lives until the stream is synchronised below
+  nsfps_status rc = build_clouds(plans, L.cb, L.sc, bd_host, st);
+  if (rc) return rc;
+  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[1], st));
+  uint64_t rounds = 0, wide_total = 0;
+  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total);
+  if (rc) return rc;
+  return finish_call(plans, L, ws, runs, rounds, wide_total, out_on_host, h_out, out_stride,
+                     out_lens, t0);
 }
 
 // Guards of yuezu_fps (src/yuezu_fps.cpp:678-688) that need no device.
@@ -1030,8 +1092,44 @@ bool trivial(uint64_t n, uint64_t m, int32_t *out, uint64_t *len) {
 
 void reset_stats() { memset(&g_stats, 0, sizeof(g_stats)); }
 
+// A cloud built once and sampled many times (nsfps_plan_*): its own device
+// memory holds the call layout and a copy of the arrays sampling changes
+// (the points' min-distances, the leaf keys and winners), taken after the
+// build; each sampling restores them, re-derives the level-1 nodes and the
+// sampling state, and runs the sampling pass alone.
+struct PlanImpl {
+  int device = -1;
+  std::vector<CloudPlan> plans;  // one cloud
+  CallLayout L;
+  char *mem = nullptr;
+  size_t cap = 0;
+  float4 *p4_0 = nullptr;
+  uint64_t *lk_0 = nullptr;
+  float4 *lp_0 = nullptr;
+  hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  bool runs = true;
+  PlanImpl() = default;
+  PlanImpl(const PlanImpl &) = delete;
+  PlanImpl &operator=(const PlanImpl &) = delete;
+  // Frees the plan's device memory and events on its device (the caller
+  // holds g_mu).
+  ~PlanImpl() {
+    int cur = -1;
+    const bool other = hipGetDevice(&cur) == hipSuccess && device >= 0 && cur != device;
+    if (other) (void)hipSetDevice(device);
+    for (auto &e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (mem) (void)hipFree(mem);
+    if (other) (void)hipSetDevice(cur);
+  }
+};
+
 }  // namespace
 }  // namespace nsfps
+
+struct nsfps_plan_s {
+  nsfps::PlanImpl impl;
+};
 
 using namespace nsfps;
 
@@ -1118,7 +1216,7 @@ static nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m,
   p.m = (uint32_t)m;
   derive(r, p.rng);
   p.h_xyz = xyz;
-  return run_clouds(plans, nullptr, true, out, 0, out_len);
+  return run_clouds(plans, Ws{}, true, out, 0, out_len);
 }
 
 nsfps_status nsfps_fps(const float *xyz, uint64_t n, uint64_t n_samples, const nsfps_range *range,
@@ -1191,7 +1289,7 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n, uin
       derive(rs[b], plans[b].rng);
       plans[b].h_xyz = xyz + b * n * 3;
     }
-    return run_clouds(plans, nullptr, true, out, m, out_lens);
+    return run_clouds(plans, Ws{}, true, out, m, out_lens);
   });
 }
 
@@ -1221,12 +1319,148 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const 
     p.m = (uint32_t)m;
     derive(*range, p.rng);
     p.d_xyz_in = d_xyz;
-    rc = run_clouds(plans, st, false, nullptr, 0, out_len);
+    Ws ws;
+    ws.st = st;
+    rc = run_clouds(plans, ws, false, nullptr, 0, out_len);
     if (rc) return rc;
     HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));
     return NSFPS_OK;
   });
+}
+
+nsfps_status nsfps_plan_create(const float *xyz, uint64_t n, const nsfps_range *range,
+                               int on_device, nsfps_plan **out) {
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (!out || !range || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    *out = nullptr;
+    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+    nsfps_status rc = check_range(*range);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+      return fail(NSFPS_EDEVICE, "no HIP device available (nsfps has no CPU path)");
+    auto plan = std::make_unique<nsfps_plan_s>();
+    PlanImpl &P = plan->impl;
+    HIP_TRY(hipGetDevice(&P.device));
+    P.plans.resize(1);
+    CloudPlan &p = P.plans[0];
+    p.n = (uint32_t)n;
+    p.m = 0;  // the sample count is given to each sampling
+    derive(*range, p.rng);
+    if (on_device) p.d_xyz_in = xyz;
+    else p.h_xyz = xyz;
+    // a cloud of at most one point needs no device structure
+    if (n <= 1) {
+      *out = plan.release();
+      return NSFPS_OK;
+    }
+    const size_t need = measure_call(P.plans, P.L);
+    Bump snap(nullptr);
+    snap.off = need;
+    const CloudPlan &pb = P.plans[0];
+    snap.take<float4>(pb.slots_ub);
+    snap.take<uint64_t>(pb.leaves_ub);
+    snap.take<float4>(pb.leaves_ub);
+    const size_t total = snap.off + 256;
+    hipError_t e = hipMalloc(&P.mem, total);
+    if (e != hipSuccess) {
+      P.mem = nullptr;
+      return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", total, hipGetErrorString(e));
+    }
+    P.cap = total;
+    for (auto &ev : P.ev) HIP_TRY(hipEventCreate(&ev));
+    Bump bp(P.mem);
+    layout_all(bp, P.plans, P.L);
+    bp.off = need;
+    P.p4_0 = bp.take<float4>(pb.slots_ub);
+    P.lk_0 = bp.take<uint64_t>(pb.leaves_ub);
+    P.lp_0 = bp.take<float4>(pb.leaves_ub);
+    P.runs = choose_runs(P.plans);
+    hipStream_t st = nullptr;
+    std::vector<BuildDev> bd_host;
+    rc = build_clouds(P.plans, P.L.cb, P.L.sc, bd_host, st);
+    if (rc) return rc;
+    const CloudDev &c = P.plans[0].dev;
+    HIP_TRY(hipMemcpyAsync(P.p4_0, c.P4, (size_t)c.nslots * sizeof(float4),
+                           hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipMemcpyAsync(P.lk_0, c.leaf_key, (size_t)c.nleaves * 8, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipMemcpyAsync(P.lp_0, c.leaf_pos, (size_t)c.nleaves * sizeof(float4),
+                           hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    // the input is not read again
+    P.plans[0].h_xyz = nullptr;
+    P.plans[0].d_xyz_in = nullptr;
+    *out = plan.release();
+    return NSFPS_OK;
+  });
+}
+
+nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uint64_t *out_len,
+                               void *stream) {
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (!plan || !out_len || (m && !d_out)) return fail(NSFPS_EINVAL, "null pointer");
+    PlanImpl &P = plan->impl;
+    std::lock_guard<std::mutex> lk(g_mu);
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != P.device)
+      return fail(NSFPS_EINVAL, "the plan was created on device %d, the current device is %d",
+                  P.device, dev);
+    hipStream_t st = (hipStream_t)stream;
+    CloudPlan &p = P.plans[0];
+    const uint64_t n = p.n;
+    if (n == 0 || m == 0 || m >= n || m == 1) {
+      int32_t first[1] = {0};
+      std::vector<int32_t> tmp;
+      const int32_t *src = first;
+      if (m >= n) {
+        tmp.resize((size_t)n);
+        trivial(n, m, tmp.data(), out_len);
+        src = tmp.data();
+      } else {
+        trivial(n, m, first, out_len);
+      }
+      if (*out_len) {
+        HIP_TRY(hipMemcpyAsync(d_out, src, *out_len * 4, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipStreamSynchronize(st));
+      }
+      return NSFPS_OK;
+    }
+    if (m > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 samples");
+    auto t0 = std::chrono::steady_clock::now();
+    p.m = (uint32_t)m;
+    p.dev.m = (uint32_t)m;
+    p.dev.out = d_out;
+    Ws ws;
+    ws.base = P.mem;
+    ws.cap = P.cap;
+    ws.st = st;
+    ws.ev = P.ev;
+    CloudDev &c = p.dev;
+    HIP_TRY(hipEventRecord(P.ev[0], st));
+    HIP_TRY(hipMemcpyAsync(c.P4, P.p4_0, (size_t)c.nslots * sizeof(float4),
+                           hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipMemcpyAsync(c.leaf_key, P.lk_0, (size_t)c.nleaves * 8, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipMemcpyAsync(c.leaf_pos, P.lp_0, (size_t)c.nleaves * sizeof(float4),
+                           hipMemcpyDeviceToDevice, st));
+    HIP_TRY(launch_init_state(c, p.d_small + 2, st));
+    HIP_TRY(hipEventRecord(P.ev[1], st));
+    uint64_t rounds = 0, wide_total = 0;
+    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total);
+    if (rc) return rc;
+    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, false, nullptr, 0, out_len,
+                       t0);
+  });
+}
+
+void nsfps_plan_destroy(nsfps_plan *plan) {
+  if (!plan) return;
+  std::lock_guard<std::mutex> lk(g_mu);
+  delete plan;
 }
 
 nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords) {

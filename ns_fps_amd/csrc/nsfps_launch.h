@@ -10,6 +10,9 @@
 
 namespace nsfps {
 
+// words 32-bit words at p set to value
+hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t st);
+
 // build
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
