@@ -26,6 +26,9 @@
  *   nsfps_gather_points, nsfps_ball_query (and _device)
  *                        no counterpart: the grouping step the reference's
  *                        callers run on its output (see their declarations)
+ *   nsfps_fps_device_noalloc
+ *                        no counterpart: nsfps_fps_device for callers that
+ *                        cannot allocate device memory (see its declaration)
  */
 #ifndef NSFPS_H
 #define NSFPS_H
@@ -147,6 +150,25 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
 nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples,
                               const nsfps_range *range, int32_t *d_out,
                               uint64_t *out_len, void *stream);
+
+/* nsfps_fps_device without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The call's whole workspace (cell keys, sorts, slots, leaves,
+ * tree and sampling state) lives in a static device array of
+ * nsfps_noalloc_scratch_bytes() bytes (64 MiB) per device, held until the
+ * process ends; a cloud whose layout needs more (about 400,000 points on
+ * grids of up to 2^16 blocks) fails with NSFPS_EUNSUPPORTED and a message
+ * giving both sizes.  Same arguments, samples and guards as nsfps_fps_device;
+ * no hipMalloc, hipFree, stream or event creation, and no memset nodes (fill
+ * kernels clear what must start at zero).  The array keeps the last call's
+ * contents; calls are serialised by the library's lock, and a call on one
+ * device must not overlap another use of that device's array (the library
+ * makes none).  Statistics report e2e_ms only (no device events). */
+nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t n_samples,
+                                      const nsfps_range *range, int32_t *d_out,
+                                      uint64_t *out_len, void *stream);
+uint64_t nsfps_noalloc_scratch_bytes(void);
 
 /* A cloud built once and sampled many times, the split of the reference GPU
  * driver's FpsGPU::initialize / FpsGPU::sample (eval/src_gpu/yuezu_fps_gpu.h:

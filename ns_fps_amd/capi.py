@@ -110,6 +110,19 @@ class Lib:
                                               ctypes.byref(n_out), _vp(stream)))
         return n_out.value
 
+    def fps_device_noalloc(self, d_xyz, n, n_samples, rng, d_out, stream=None):
+        """nsfps_fps_device_noalloc: nsfps_fps_device with its workspace in the
+        library's static device array (no device allocation)."""
+        n_out = _u64()
+        self._check(self.lib.nsfps_fps_device_noalloc(_vp(d_xyz), _u64(n), _u64(int(n_samples)),
+                                                      ctypes.byref(Range.of(rng)), _vp(d_out),
+                                                      ctypes.byref(n_out), _vp(stream)))
+        return n_out.value
+
+    def noalloc_scratch_bytes(self):
+        self.lib.nsfps_noalloc_scratch_bytes.restype = ctypes.c_uint64
+        return int(self.lib.nsfps_noalloc_scratch_bytes())
+
     def plan_create(self, xyz, n, rng, on_device=False):
         """nsfps_plan_create: xyz is a device pointer (int) when on_device,
         else a host (N, 3) float32 array.  Returns the plan handle."""

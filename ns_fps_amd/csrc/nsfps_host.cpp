@@ -1124,6 +1124,27 @@ struct PlanImpl {
   }
 };
 
+// The allocation-free entry point's workspace: one array per device, of
+// kScratchBytes, held until the process ends.  Host code uses only the
+// address hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = 64ull << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+void *g_scratch_ptr[16];
+
+nsfps_status scratch_for_device(void **out) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 16) return fail(NSFPS_EDEVICE, "device ordinal %d out of range", dev);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(NSFPS_EDEVICE, "no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSFPS_OK;
+}
+
 }  // namespace
 }  // namespace nsfps
 
@@ -1328,6 +1349,61 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const 
     return NSFPS_OK;
   });
 }
+
+nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t m,
+                                      const nsfps_range *range, int32_t *d_out,
+                                      uint64_t *out_len, void *stream) {
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (!range || !out_len || (m && !d_out) || (n && !d_xyz))
+      return fail(NSFPS_EINVAL, "null pointer");
+    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+    nsfps_status rc = check_range(*range);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+      return fail(NSFPS_EDEVICE, "no HIP device available (nsfps has no CPU path)");
+    hipStream_t st = (hipStream_t)stream;
+    void *ws_base = nullptr;
+    rc = scratch_for_device(&ws_base);
+    if (rc) return rc;
+    if (n == 0 || m == 0 || m >= n || m == 1) {
+      int32_t first[1] = {0};
+      std::vector<int32_t> tmp;
+      const int32_t *src = first;
+      if (m >= n) {
+        tmp.resize((size_t)n);
+        trivial(n, m, tmp.data(), out_len);
+        src = tmp.data();
+      } else {
+        trivial(n, m, first, out_len);
+      }
+      if (*out_len) {
+        HIP_TRY(hipMemcpyAsync(d_out, src, *out_len * 4, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipStreamSynchronize(st));
+      }
+      return NSFPS_OK;
+    }
+    std::vector<CloudPlan> plans(1);
+    CloudPlan &p = plans[0];
+    p.n = (uint32_t)n;
+    p.m = (uint32_t)m;
+    derive(*range, p.rng);
+    p.d_xyz_in = d_xyz;
+    Ws ws;
+    ws.base = (char *)ws_base;
+    ws.cap = kScratchBytes;
+    ws.st = st;
+    rc = run_clouds(plans, ws, false, nullptr, 0, out_len);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return NSFPS_OK;
+  });
+}
+
+uint64_t nsfps_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 nsfps_status nsfps_plan_create(const float *xyz, uint64_t n, const nsfps_range *range,
                                int on_device, nsfps_plan **out) {
