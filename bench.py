@@ -370,7 +370,8 @@ def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
 # ------------------------------------------------------------ phase clocks
 
 RUN_PHASES = ["load", "select", "gather", "phases", "apply", "tail", "big", "rank", "picks",
-              "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total"]
+              "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total",
+              "help_tail", "help_tail_n", "help_step", "help_steps", "help_count"]
 
 
 def run_phases(lib, hip, w):
@@ -393,7 +394,7 @@ def run_phases(lib, hip, w):
             hip.free(d_out)
     finally:
         del os.environ["NSFPS_PROFILE"]
-    v = dict(zip(RUN_PHASES, words[:16]))
+    v = dict(zip(RUN_PHASES, words[:21]))
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
     cycles = {k: v[k] for k in ["load", "select", "gather", "rank", "phases", "walk", "apply", "big",
@@ -413,7 +414,12 @@ def run_phases(lib, hip, w):
                                    if k not in ("load", "tail")},
             "cycles_per_round": {"load": round(cycles["load"] / rounds, 1),
                                  "tail": round(cycles["tail"] / rounds, 1)},
-            "sample_ms": round(st["sample_ms"], 3), "device_ms": round(st["device_ms"], 3)}
+            "sample_ms": round(st["sample_ms"], 3), "device_ms": round(st["device_ms"], 3),
+            "helpers": {"tail_us_per_round": round(v["help_tail"] * 0.01 / max(1, v["help_tail_n"]), 2),
+                        "rounds_measured": v["help_tail_n"],
+                        "step_us": round(v["help_step"] * 0.01 / max(1, v["help_steps"]), 2),
+                        "steps": v["help_steps"],
+                        "first_count_us_total": round(v["help_count"] * 0.01, 1)}}
 
 
 # --------------------------------------------------------------------- lines

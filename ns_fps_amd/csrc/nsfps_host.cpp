@@ -13,6 +13,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -378,6 +379,16 @@ int key_bits_for(uint32_t T) {
 // slots: cell -> leaf becomes arithmetic, no table lookup per iteration.
 uint64_t padded_slot_limit(uint32_t n) { return std::max<uint64_t>(4ull * n, 65536ull); }
 
+// How long a helper of a fused round waits for the run before giving up, in
+// s_memrealtime ticks (100 MHz): NSFPS_HELP_WAIT_US microseconds, 20 ms by
+// default (a run takes well under 1 ms; only a run that never started, or
+// a test asking for it, reaches the bound).
+uint32_t help_wait_ticks() {
+  const char *e = getenv("NSFPS_HELP_WAIT_US");
+  uint64_t us = e ? strtoull(e, nullptr, 10) : 20000ull;
+  return (uint32_t)std::min<uint64_t>(us * 100ull, 0xffffffffull);
+}
+
 // Lays out the persistent buffers of one cloud (upper bounds: the padded /
 // dense decision is made on the device data during the build).
 void layout_cloud(Bump &bp, CloudPlan &p) {
@@ -407,7 +418,8 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.root_pos = bp.take<float4>(1);
   c.counter = bp.take<uint32_t>(1);
   c.prof = bp.take<uint64_t>(kProfWords);
-  c.hist = bp.take<uint32_t>((size_t)kHists * kHistBins);
+  c.hist = bp.take<uint32_t>((size_t)2 * kHists * kHistBins);
+  c.rec = bp.take<uint64_t>((size_t)kListCap * kRecWords);
   c.pick_p = bp.take<float4>(kListCap);
   c.pick_c = bp.take<uint2>(kListCap);
   c.list_p = bp.take<float4>(kListCap);
@@ -417,6 +429,7 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.n = n;
   c.m = p.m;
   c.r = p.rng.dev;
+  c.help_wait = help_wait_ticks();
 }
 
 void layout_scratch(Bump &bp, uint32_t n, uint32_t tmax, Scratch &s) {
@@ -799,16 +812,49 @@ struct RoundSchedule {
 };
 RoundSchedule g_schedule;
 
+// Helper workgroups of a fused round for a single cloud of nl1 level-1
+// nodes: one per node when that many fit beside the run on the device at
+// once and there are at least kFusedMinNodes of them, else 0 (classic
+// rounds).  Measured on the MI355X: a helper owning several nodes steps
+// slower than the run publishes (1M-point uniform cube, 512 nodes over 255
+// helpers: a 20 us tail per round against the 14 us update pass it
+// replaces), and on a small cloud the update pass is shorter than the
+// helpers' tail (10,000 points, 3 nodes: 1.64 against 1.38 ms per call);
+// the 120,000-point scan (93 nodes) gains 0.45 ms.  NSFPS_FUSED=1 uses them
+// whenever they fit (up to fused_max_nodes_per_helper() nodes per helper),
+// NSFPS_NO_FUSED=1 never.  Several clouds take classic rounds.
+constexpr uint32_t kFusedMinNodes = 64;
+
+uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
+  if (nclouds != 1 || getenv("NSFPS_NO_FUSED")) return 0;
+  const char *force = getenv("NSFPS_FUSED");
+  const bool forced = force && atoi(force) == 1;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      fused_blocks_per_cu(&per_cu) != hipSuccess || per_cu < 1 || cus < 2)
+    return 0;
+  const uint32_t cap = (uint32_t)(cus * per_cu - 1);
+  if (!forced) return nl1 <= cap && nl1 >= kFusedMinNodes ? nl1 : 0u;
+  const uint32_t h = std::min<uint32_t>(nl1, cap);
+  if (h == 0 || (nl1 + h - 1) / h > fused_max_nodes_per_helper()) return 0;
+  return h;
+}
+
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
-                        uint64_t *rounds_out) {
+                        uint64_t *rounds_out, uint32_t *repairs_out) {
   uint32_t max_nl1 = 1;
   for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
   const uint32_t nc = (uint32_t)plans.size();
+  const uint32_t helpers = fused_helpers(nc, max_nl1);
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
   std::vector<std::pair<uint32_t, uint32_t>> used;
+  uint32_t repairs = 0, seq = 0;
   HIP_TRY(launch_runs_init(d_clouds, nc, st));
+  // fused rounds: the first pick (row 0, the whole grid) by one update pass
+  if (helpers) HIP_TRY(launch_update_pass(d_clouds, nc, max_nl1, st));
   std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0, passes = 0;
@@ -817,7 +863,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     for (const auto &bp : g_schedule.batches) {
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, helpers, &seq, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -826,7 +872,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   }
   while (true) {
     if (!launched) {
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, helpers, &seq, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }
@@ -834,6 +880,21 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
                            st));
     HIP_TRY(hipStreamSynchronize(st));
+    // a helper that gave up waiting left its round's update undone, and every
+    // launch after it in the batch did nothing: redo that update (every pick
+    // of the run on every point; points already updated stay as they are)
+    // into a cleared histogram set, then go on
+    bool repaired = false;
+    for (uint32_t i = 0; i < nc; ++i) {
+      if (!pr[i].rs.hold || pr[i].done) continue;
+      const CloudDev &c = plans[i].dev;
+      HIP_TRY(launch_fill_u32(c.hist + (size_t)pr[i].rs.hsel * kHists * kHistBins, 0u,
+                              (uint64_t)kHists * kHistBins, st));
+      HIP_TRY(launch_update_pass(d_clouds + i, 1, std::max<uint32_t>(c.nl1, 1), st));
+      HIP_TRY(launch_fill_u32((char *)c.rs + offsetof(RunState, hold), 0u, 1, st));
+      repaired = true;
+      ++repairs;
+    }
     bool all = true;
     uint64_t samples = 0, rounds = 0;
     for (auto &q : pr) {
@@ -852,6 +913,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       rounds = std::max<uint64_t>(rounds, q.rs.rounds);
     }
     *rounds_out = rounds;
+    *repairs_out = repairs;
     if (all) {
       std::copy(shape, shape + 5, g_schedule.shape);
       g_schedule.batches = used;
@@ -859,7 +921,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       break;
     }
     // every round takes at least one sample of every unfinished cloud
-    stalled = samples == last_samples ? stalled + 1 : 0;
+    stalled = samples == last_samples && !repaired ? stalled + 1 : 0;
     if (stalled >= 2) return fail(NSFPS_EDEVICE, "internal: sampling made no progress");
     last_samples = samples;
     batch = std::min<uint32_t>(batch * 2, 64);
@@ -935,7 +997,8 @@ bool choose_runs(std::vector<CloudPlan> &plans) {
 // the first iterations of a single cloud on the tree engine, then its loop;
 // or the speculative-run rounds.
 nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
-                           bool runs, uint64_t *rounds, uint64_t *wide_total) {
+                           bool runs, uint64_t *rounds, uint64_t *wide_total,
+                           uint32_t *repairs) {
   hipStream_t st = ws.st;
   std::vector<CloudDev> devs;
   uint32_t lds_bytes = 0;
@@ -946,13 +1009,14 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
   *rounds = 0;
   *wide_total = 0;
+  *repairs = 0;
   if (runs) {
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[3], st));
     HIP_TRY(hipMemcpyAsync(L.d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                            hipMemcpyHostToDevice, st));
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
     if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
-    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds);
+    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, repairs);
   }
   if (plans.size() == 1) {
     uint32_t e = wide_iters_for(plans[0]);
@@ -974,7 +1038,8 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
 // After sampling: lengths, the samples to the host (out_on_host) and the
 // statistics of the call (t0: host time at its start).
 nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
-                         bool runs, uint64_t rounds, uint64_t wide_total, bool out_on_host,
+                         bool runs, uint64_t rounds, uint64_t wide_total, uint32_t repairs,
+                         bool out_on_host,
                          int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
                          std::chrono::steady_clock::time_point t0) {
   hipStream_t st = ws.st;
@@ -1030,6 +1095,7 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
   S.lds_bytes = runs ? 0 : lds_bytes;
   S.rounds = rounds;
   S.engine = runs ? 1u : 0u;
+  S.repairs = repairs;
   return NSFPS_OK;
 }
 
@@ -1065,10 +1131,11 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, 
   if (rc) return rc;
   if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[1], st));
   uint64_t rounds = 0, wide_total = 0;
-  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total);
+  uint32_t repairs = 0;
+  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &repairs);
   if (rc) return rc;
-  return finish_call(plans, L, ws, runs, rounds, wide_total, out_on_host, h_out, out_stride,
-                     out_lens, t0);
+  return finish_call(plans, L, ws, runs, rounds, wide_total, repairs, out_on_host, h_out,
+                     out_stride, out_lens, t0);
 }
 
 // Guards of yuezu_fps (src/yuezu_fps.cpp:678-688) that need no device.
@@ -1526,10 +1593,11 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
     HIP_TRY(launch_init_state(c, p.d_small + 2, st));
     HIP_TRY(hipEventRecord(P.ev[1], st));
     uint64_t rounds = 0, wide_total = 0;
-    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total);
+    uint32_t repairs = 0;
+    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &repairs);
     if (rc) return rc;
-    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, false, nullptr, 0, out_len,
-                       t0);
+    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, repairs, false, nullptr, 0,
+                       out_len, t0);
   });
 }
 

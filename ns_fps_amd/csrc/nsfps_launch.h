@@ -82,8 +82,18 @@ constexpr uint32_t kProfWords = 24;
 
 // speculative-run engine
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);
+// helpers == 0: rounds of update pass, refinements, gather pass and run; else
+// fused rounds of one cloud (refinements, gather pass, then the run with
+// `helpers` helper workgroups applying its picks), after one update pass
+// (launch_update_pass) for the first pick.
+// *seq counts the call's fused launches (each gets the next number).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, uint32_t passes, bool profile, hipStream_t st);
+                         uint32_t rounds, uint32_t passes, bool profile, uint32_t helpers,
+                         uint32_t *seq, hipStream_t st);
+hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
+                              hipStream_t st);
+uint32_t fused_max_nodes_per_helper();
+hipError_t fused_blocks_per_cu(int *blocks);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

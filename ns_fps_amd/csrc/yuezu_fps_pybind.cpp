@@ -275,6 +275,7 @@ py::dict last_stats_py() {
   d["samples"] = s.samples;
   d["rounds"] = s.rounds;
   d["engine"] = s.engine ? "runs" : "tree";
+  d["repairs"] = s.repairs;
   return d;
 }
 
