@@ -19,8 +19,9 @@ schedule), the host-buffer call with its PCIe copies (e2e_ms) and the
 sampling of a prepared plan (plan_sample_ms).
 
 Prints ONE JSON line (rank 0).  With --all it first prints one line per
-workload (the five seeded workloads, each with its roofline and reference
-CPU time); the contract line always comes last.
+workload (the five seeded benchmark workloads and the uniform cube on a 30^3
+grid, which takes the general bucket path; each with its roofline and
+reference CPU time); the contract line always comes last.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload uniform_cube]
 """
@@ -41,7 +42,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 HEADLINE_METRIC = "FPS ms/call & samples/s at 1M pts -> 65,536 samples; % of HBM roofline"
-ALL_WORKLOADS = ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]
+ALL_WORKLOADS = ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan", "batched_shapes",
+                 "clustered"]
 
 
 def metric_for(w):
@@ -372,6 +374,7 @@ def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
 RUN_PHASES = ["load", "select", "gather", "phases", "apply", "tail", "big", "rank", "picks",
               "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total",
               "help_tail", "help_tail_n", "help_step", "help_steps", "help_count"]
+PASS_COUNTERS = ["update_leaves", "update_points", "gather_leaves", "gather_points"]
 
 
 def run_phases(lib, hip, w):
@@ -395,6 +398,7 @@ def run_phases(lib, hip, w):
     finally:
         del os.environ["NSFPS_PROFILE"]
     v = dict(zip(RUN_PHASES, words[:21]))
+    ctr = dict(zip(PASS_COUNTERS, words[24:28]))
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
     cycles = {k: v[k] for k in ["load", "select", "gather", "rank", "phases", "walk", "apply", "big",
@@ -419,7 +423,26 @@ def run_phases(lib, hip, w):
                         "rounds_measured": v["help_tail_n"],
                         "step_us": round(v["help_step"] * 0.01 / max(1, v["help_steps"]), 2),
                         "steps": v["help_steps"],
-                        "first_count_us_total": round(v["help_count"] * 0.01, 1)}}
+                        "first_count_us_total": round(v["help_count"] * 0.01, 1)},
+            "passes": pass_counts(w["name"], ctr, rounds)}
+
+
+def pass_counts(wname, ctr, rounds):
+    """The grid-wide passes' device-counted reads against the census: leaves
+    (64-point) and points whose data the update and gather passes read, per
+    round and in total, and their bytes at the census's own prices (16 B per
+    point, 8 B per leaf) beside the census's total (16 B per candidate point,
+    8 B per candidate 16-point leaf of the reference's iterations)."""
+    out = {k: int(ctr[k]) for k in PASS_COUNTERS}
+    out.update({k + "_per_round": round(ctr[k] / rounds, 1) for k in PASS_COUNTERS})
+    census = load_census(wname)
+    dev = 16 * (ctr["update_points"] + ctr["gather_points"]) + \
+        8 * (ctr["update_leaves"] + ctr["gather_leaves"])
+    out["device_bytes_at_census_prices"] = int(dev)
+    if census is not None:
+        out["census_alg_bytes"] = census["total"]
+        out["device_over_census"] = round(dev / census["total"], 4)
+    return out
 
 
 # --------------------------------------------------------------------- lines
@@ -479,7 +502,7 @@ def main():
                     help="seconds of reference CPU work per workload (default 30)")
     ap.add_argument("--all", action="store_true", help="also print a line per workload")
     ap.add_argument("--only", default="",
-                    help="with --all: comma-separated workloads instead of all five")
+                    help="with --all: comma-separated workloads instead of all six")
     ap.add_argument("--ball-query", action="store_true",
                     help="time only the grouping step after FPS (ball query) and print its line")
     ap.add_argument("--phases", action="store_true",

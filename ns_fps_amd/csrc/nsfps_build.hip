@@ -317,14 +317,16 @@ __global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__r
             padded, cap, P4, RO, phys0);
 }
 
-// Leaf descriptors (first slot, point count, cell) of every leaf of bucket b.
+// Leaf descriptors (first slot, point count, cell) of every leaf of bucket b,
+// and the cells of the bucket (r.na per leaf).
 __device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restrict__ cell_start,
                                              const uint32_t *__restrict__ cell_leaf, uint32_t T,
                                              uint32_t padded, uint32_t cap, uint32_t lpc,
                                              const RangeDev &r, const float4 *__restrict__ P4,
                                              float4 *__restrict__ leaf_lo,
                                              float4 *__restrict__ leaf_hi,
-                                             uint32_t *__restrict__ leaf_cell) {
+                                             uint32_t *__restrict__ leaf_cell,
+                                             uint32_t *__restrict__ leaf_al) {
   if (b >= T) return;
   uint32_t s = cell_start[b], e = cell_start[b + 1];
   uint32_t cntb = e - s;
@@ -336,12 +338,15 @@ __device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restr
     float4 p = P4[first];
     packed = cell_axis(r, 0, p.x) | (cell_axis(r, 1, p.y) << 10) | (cell_axis(r, 2, p.z) << 20);
   }
+  uint32_t al[kMaxAlias];
+  if (nl) bucket_cells(r, b, al);
   for (uint32_t k = 0; k < nl; ++k, ++l) {
     uint32_t off = k * kLeaf;
     uint32_t cnt = cntb > off ? (cntb - off < kLeaf ? cntb - off : kLeaf) : 0u;
     leaf_lo[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(first + off));
     leaf_hi[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(cnt));
     leaf_cell[l] = packed;
+    for (uint32_t a = 0; a < r.na; ++a) leaf_al[(size_t)l * r.na + a] = al[a];
   }
 }
 
@@ -349,9 +354,9 @@ __global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
                             const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
                             uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
                             float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
-                            uint32_t *__restrict__ leaf_cell) {
+                            uint32_t *__restrict__ leaf_cell, uint32_t *__restrict__ leaf_al) {
   leaf_desc_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, padded, cap, lpc,
-               r, P4, leaf_lo, leaf_hi, leaf_cell);
+               r, P4, leaf_lo, leaf_hi, leaf_cell, leaf_al);
 }
 
 // Leaf bounding boxes and initial keys (FLT_MAX with the smallest rank of the
@@ -410,21 +415,43 @@ __global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float
                leaf_pos);
 }
 
-// Level-1 nodes from the initial leaves: max key, its position, and the union
-// of the leaf boxes.  One wave per node.
+// Level-1 nodes from the initial leaves: max key, its position, the union
+// of the leaf boxes, and the corners of the cells of the leaves' buckets
+// (leaves with points only; x = kNone when there are none).  One wave per
+// node.
 __device__ __forceinline__ void l1_init_at(uint32_t g, uint32_t nleaves, uint32_t nl1,
                                            const uint64_t *__restrict__ leaf_key,
                                            const float4 *__restrict__ leaf_pos,
                                            const float4 *__restrict__ leaf_lo,
                                            const float4 *__restrict__ leaf_hi,
+                                           const uint32_t *__restrict__ leaf_al, uint32_t na,
                                            uint64_t *__restrict__ l1_key,
                                            float4 *__restrict__ l1_pos,
                                            float4 *__restrict__ l1_lo,
-                                           float4 *__restrict__ l1_hi) {
+                                           float4 *__restrict__ l1_hi,
+                                           uint2 *__restrict__ l1_cbox) {
   uint32_t lane = lane_id();
   if (g >= nl1) return;
   uint32_t j = g * kFan + lane;
   bool v = j < nleaves;
+  uint32_t cmin[3] = {kNone, kNone, kNone}, cmax[3] = {0u, 0u, 0u};
+  if (v && __float_as_uint(leaf_hi[j].w) != 0u) {
+    for (uint32_t a = 0; a < na; ++a) {
+      const uint32_t cl = leaf_al[(size_t)j * na + a];
+      if (cl == kNoCell) continue;
+      const uint32_t cx[3] = {cl & 1023u, (cl >> 10) & 1023u, cl >> 20};
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        cmin[d] = cx[d] < cmin[d] ? cx[d] : cmin[d];
+        cmax[d] = cx[d] > cmax[d] ? cx[d] : cmax[d];
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    cmin[d] = wave_min_u32(cmin[d]);
+    cmax[d] = wave_max_u32(cmax[d]);
+  }
   uint64_t k = v ? leaf_key[j] : 0ull;
   float4 lo = v ? leaf_lo[j] : make_float4(INFINITY, INFINITY, INFINITY, 0.f);
   float4 hi = v ? leaf_hi[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, 0.f);
@@ -445,6 +472,10 @@ __device__ __forceinline__ void l1_init_at(uint32_t g, uint32_t nleaves, uint32_
     l1_pos[g] = leaf_pos[g * kFan + wl];
     l1_lo[g] = make_float4(mnx, mny, mnz, 0.f);
     l1_hi[g] = make_float4(mxx, mxy, mxz, 0.f);
+    l1_cbox[g] = cmin[0] == kNone
+                     ? make_uint2(kNone, 0u)
+                     : make_uint2(cmin[0] | (cmin[1] << 10) | (cmin[2] << 20),
+                                  cmax[0] | (cmax[1] << 10) | (cmax[2] << 20));
   }
 }
 
@@ -455,10 +486,13 @@ __global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
                                                  const float4 *__restrict__ leaf_hi,
                                                  uint64_t *__restrict__ l1_key,
                                                  float4 *__restrict__ l1_pos,
+                                                 const uint32_t *__restrict__ leaf_al,
+                                                 uint32_t na,
                                                  float4 *__restrict__ l1_lo,
-                                                 float4 *__restrict__ l1_hi) {
+                                                 float4 *__restrict__ l1_hi,
+                                                 uint2 *__restrict__ l1_cbox) {
   l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, nl1, leaf_key, leaf_pos, leaf_lo,
-             leaf_hi, l1_key, l1_pos, l1_lo, l1_hi);
+             leaf_hi, leaf_al, na, l1_key, l1_pos, l1_lo, l1_hi, l1_cbox);
 }
 
 __device__ __forceinline__ void init_state_of(const CloudDev &c, const uint32_t *phys0) {
@@ -582,9 +616,10 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
                              uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
                              const RangeDev &r, const float4 *P4, const uint2 *RO,
                              float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
-                             uint64_t *leaf_key, float4 *leaf_pos, hipStream_t st) {
+                             uint32_t *leaf_al, uint64_t *leaf_key, float4 *leaf_pos,
+                             hipStream_t st) {
   k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
-                                            leaf_lo, leaf_hi, leaf_cell);
+                                            leaf_lo, leaf_hi, leaf_cell, leaf_al);
   if (nleaves)
     k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
                                                   leaf_pos);
@@ -594,9 +629,10 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st) {
   if (c.nl1)
     k_l1_init<<<cdiv(c.nl1, 4), 256, 0, st>>>(c.nleaves, c.nl1, c.leaf_key, c.leaf_pos, c.leaf_lo,
-                                              c.leaf_hi, c.l1_key, c.l1_pos,
+                                              c.leaf_hi, c.l1_key, c.l1_pos, c.leaf_al, c.r.na,
                                               const_cast<float4 *>(c.l1_lo),
-                                              const_cast<float4 *>(c.l1_hi));
+                                              const_cast<float4 *>(c.l1_hi),
+                                              const_cast<uint2 *>(c.l1_cbox));
   k_init_state<<<1, 64, 0, st>>>(c, d_phys0);
   return hipGetLastError();
 }
@@ -643,7 +679,7 @@ __global__ void kb_cells(const BuildDev *__restrict__ bd) {
   cell_info_at(i, b.counts, b.lc, b.T, const_cast<uint2 *>(b.c.cell_info));
   leaf_desc_at(i, b.counts, b.lc, b.T, b.c.padded, b.cap, b.c.lpc, b.c.r, b.c.P4,
                const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
-               const_cast<uint32_t *>(b.c.leaf_cell));
+               const_cast<uint32_t *>(b.c.leaf_cell), const_cast<uint32_t *>(b.c.leaf_al));
 }
 
 __global__ __launch_bounds__(256) void kb_leaf_bbox(const BuildDev *__restrict__ bd) {
@@ -657,8 +693,9 @@ __global__ __launch_bounds__(256) void kb_l1_init(const BuildDev *__restrict__ b
   const BuildDev &b = bd[blockIdx.y];
   const CloudDev &c = b.c;
   l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), c.nleaves, c.nl1, c.leaf_key, c.leaf_pos,
-             c.leaf_lo, c.leaf_hi, c.l1_key, c.l1_pos, const_cast<float4 *>(c.l1_lo),
-             const_cast<float4 *>(c.l1_hi));
+             c.leaf_lo, c.leaf_hi, c.leaf_al, c.r.na, c.l1_key, c.l1_pos,
+             const_cast<float4 *>(c.l1_lo), const_cast<float4 *>(c.l1_hi),
+             const_cast<uint2 *>(c.l1_cbox));
 }
 
 __global__ void kb_init_state(const BuildDev *__restrict__ bd) {

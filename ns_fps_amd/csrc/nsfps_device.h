@@ -86,6 +86,29 @@ __device__ __forceinline__ uint32_t bucket_of(const RangeDev &r, const uint32_t 
   return r.bijective ? code : code % r.T;
 }
 
+// The bits of v at the set positions of mask, packed from bit 0 up.
+__device__ __forceinline__ uint32_t extract_bits(uint32_t v, uint32_t mask) {
+  uint32_t r = 0, k = 0;
+  for (uint32_t m = mask; m; m &= m - 1, ++k) r |= ((v >> __builtin_ctz(m)) & 1u) << k;
+  return r;
+}
+
+// The cells of bucket b, packed 10 bits per axis, kNoCell-padded to r.na
+// entries: every code b + jT below 2^cbits whose axis values lie inside the
+// grid (src/yuezu_fps.cpp:413, 592: a cell's bucket is its LUT Morton code
+// modulo the block count).
+__device__ __forceinline__ void bucket_cells(const RangeDev &r, uint32_t b, uint32_t *out) {
+  uint32_t k = 0;
+  const uint64_t codes = 1ull << r.cbits;
+  for (uint64_t code = b; code < codes && k < r.na; code += r.T) {
+    const uint32_t x = extract_bits((uint32_t)code, r.cmask[0]);
+    const uint32_t y = extract_bits((uint32_t)code, r.cmask[1]);
+    const uint32_t z = extract_bits((uint32_t)code, r.cmask[2]);
+    if (x < r.blocks[0] && y < r.blocks[1] && z < r.blocks[2]) out[k++] = x | (y << 10) | (z << 20);
+  }
+  for (; k < r.na; ++k) out[k] = kNoCell;
+}
+
 // Morton code of a cell from the concatenated LUTs.
 __device__ __forceinline__ uint32_t cell_code(const RangeDev &r, const uint32_t *lut, uint32_t ix,
                                               uint32_t iy, uint32_t iz) {

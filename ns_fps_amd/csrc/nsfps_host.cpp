@@ -170,6 +170,29 @@ void derive(const nsfps_range &r, HostRange &h) {
   d.lut_total = off;
   d.T = (uint32_t)h.info.total_blocks;
   d.bijective = bij ? 1u : 0u;
+  // cells per bucket: codes b + jT below 2^cbits, so at most ceil(2^cbits / T)
+  // (< 8: each axis has fewer than twice its blocks in codes, or exactly twice
+  // for one block); counted exactly over the cells when there are few
+  d.cbits = tb;
+  for (int a = 0; a < 3; ++a) d.cmask[a] = h.lut[a].back();
+  if (bij) {
+    d.na = 1;
+  } else {
+    const uint64_t codes = 1ull << tb, T = h.info.total_blocks;
+    uint32_t na = (uint32_t)std::min<uint64_t>((codes + T - 1) / T, kMaxAlias);
+    if (T <= 65536) {
+      std::vector<uint8_t> cnt(T, 0);
+      uint32_t mx = 1;
+      for (uint32_t z = 0; z < bl[2]; ++z)
+        for (uint32_t y = 0; y < bl[1]; ++y)
+          for (uint32_t x = 0; x < bl[0]; ++x) {
+            const uint32_t code = h.lut[0][x] | h.lut[1][y] | h.lut[2][z];
+            mx = std::max<uint32_t>(mx, ++cnt[code % T]);
+          }
+      na = std::min(na, mx);
+    }
+    d.na = na;
+  }
   static_assert(kCubeThr == NSFPS_CUBE_THRESHOLDS, "threshold count");
   for (int a = 0; a < 3; ++a)
     for (uint32_t k = 0; k < kCubeThr; ++k) {
@@ -408,12 +431,14 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.leaf_lo = bp.take<float4>(leaves);
   c.leaf_hi = bp.take<float4>(leaves);
   c.leaf_cell = bp.take<uint32_t>(leaves);
+  c.leaf_al = bp.take<uint32_t>(leaves * p.rng.dev.na);
   c.leaf_key = bp.take<uint64_t>(leaves);
   c.leaf_pos = bp.take<float4>(leaves);
   c.l1_key = bp.take<uint64_t>(p.l1_ub);
   c.l1_pos = bp.take<float4>(p.l1_ub);
   c.l1_lo = bp.take<float4>(p.l1_ub);
   c.l1_hi = bp.take<float4>(p.l1_ub);
+  c.l1_cbox = bp.take<uint2>(p.l1_ub);
   c.root_key = bp.take<uint64_t>(1);
   c.root_pos = bp.take<float4>(1);
   c.counter = bp.take<uint32_t>(1);
@@ -425,6 +450,7 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.list_p = bp.take<float4>(kListCap);
   c.list_r = bp.take<uint2>(kListCap);
   c.list_c = bp.take<uint32_t>(kListCap);
+  c.list_al = bp.take<uint32_t>((size_t)kListCap * p.rng.dev.na);
   c.lut = p.d_lut;
   c.n = n;
   c.m = p.m;
@@ -647,7 +673,7 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
   HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.nleaves,
                             p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
                             const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
-                            c.leaf_key, c.leaf_pos, st));
+                            const_cast<uint32_t *>(c.leaf_al), c.leaf_key, c.leaf_pos, st));
   HIP_TRY(launch_init_state(c, p.d_small + 2, st));
   c.lds = plan_lds(c);
   return NSFPS_OK;
@@ -845,9 +871,13 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
                         uint64_t *rounds_out, uint32_t *repairs_out) {
   uint32_t max_nl1 = 1;
-  for (auto &p : plans) max_nl1 = std::max(max_nl1, p.dev.nl1);
+  bool alias = false;  // some cloud's cells share buckets
+  for (auto &p : plans) {
+    max_nl1 = std::max(max_nl1, p.dev.nl1);
+    alias = alias || !p.rng.dev.bijective;
+  }
   const uint32_t nc = (uint32_t)plans.size();
-  const uint32_t helpers = fused_helpers(nc, max_nl1);
+  const uint32_t helpers = alias ? 0u : fused_helpers(nc, max_nl1);
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
   std::vector<std::pair<uint32_t, uint32_t>> used;
@@ -863,7 +893,8 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     for (const auto &bp : g_schedule.batches) {
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, helpers, &seq, st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, helpers, &seq,
+                            st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -872,7 +903,8 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   }
   while (true) {
     if (!launched) {
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, helpers, &seq, st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, helpers, &seq,
+                            st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }
@@ -982,11 +1014,11 @@ size_t measure_call(std::vector<CloudPlan> &plans, CallLayout &L) {
   return meas.off + 4096;
 }
 
-// The engine: speculative runs where every cloud's bucket <-> cell map is
-// one-to-one, the tree loop otherwise (or when NSFPS_ENGINE=tree asks).
+// The engine: speculative runs (for every grid; where cells share buckets its
+// kernels test every cell of a bucket), or the tree loop when
+// NSFPS_ENGINE=tree asks.
 bool choose_runs(std::vector<CloudPlan> &plans) {
   bool runs = true;
-  for (auto &p : plans) runs = runs && p.rng.dev.bijective;
   const char *eng = getenv("NSFPS_ENGINE");
   if (eng && strcmp(eng, "tree") == 0) runs = false;
   for (auto &p : plans) p.tree = !runs;

@@ -33,6 +33,12 @@ constexpr uint32_t kHistBins = 4096;
 constexpr uint32_t kHists = 3;
 constexpr uint32_t kRefinePasses = 2;  // refinement passes when they are launched
 
+// Cells one bucket can hold: codes run below 2^(bits x + bits y + bits z) < 8T.
+constexpr uint32_t kMaxAlias = 8;
+// Cell that lies outside every cube clipped to a grid whose cells share
+// buckets (such a grid has an axis of at most 1023 blocks): pads alias lists.
+constexpr uint32_t kNoCell = 0x3fffffffu;
+
 // Cube half-width thresholds kept per axis (half-widths up to this many are
 // found by comparisons; larger ones by the reference's arithmetic).
 constexpr uint32_t kCubeThr = 8;
@@ -49,6 +55,12 @@ struct RangeDev {
   uint32_t lut_total;
   uint32_t T;           // total blocks = number of buckets
   uint32_t bijective;   // 1 when bucket <-> cell is one-to-one
+  // Cells of one bucket: the valid cells among the codes b, b + T, b + 2T, ...
+  // below 2^cbits.  na bounds their number (1 when one-to-one, at most
+  // kMaxAlias); cmask[a] holds axis a's bits of a code.
+  uint32_t na;
+  uint32_t cbits;
+  uint32_t cmask[3];
   // cube half-width thresholds: half-width >= k + 1 exactly when D >= cube_thr[a][k]
   float cube_thr[3][kCubeThr];
 };
@@ -118,12 +130,15 @@ struct CloudDev {
   const float4 *leaf_lo;      // bbox min xyz, w = first slot (bits)
   const float4 *leaf_hi;      // bbox max xyz, w = point count (bits)
   const uint32_t *leaf_cell;  // ix | iy << 10 | iz << 20
+  const uint32_t *leaf_al;    // r.na per leaf: the cells of its bucket, kNoCell-padded
   uint64_t *leaf_key;         // max key of the leaf
   float4 *leaf_pos;           // x, y, z, input row (bits) of that key
   uint64_t *l1_key;
   float4 *l1_pos;
   const float4 *l1_lo;        // level-1 bounding boxes
   const float4 *l1_hi;
+  const uint2 *l1_cbox;       // level-1 nodes: lo / hi corners over the cells of their
+                              // leaves' buckets (lo > hi on some axis: no points)
   uint64_t *root_key;         // 1 entry
   float4 *root_pos;           // 1 entry
   uint32_t *iter;             // samples emitted so far (1 entry)
@@ -139,6 +154,7 @@ struct CloudDev {
   float4 *list_p;             // kListCap: x, y, z, min distance
   uint2 *list_r;              // kListCap: logical rank, input row
   uint32_t *list_c;           // kListCap: cell (10 bits per axis)
+  uint32_t *list_al;          // kListCap x r.na: the cells of each entry's bucket
   uint64_t *rec;              // kListCap x kRecWords: the run's picks as tagged records
   uint32_t help_wait;         // fused rounds: s_memrealtime ticks a helper waits before giving up
   uint32_t pad2;

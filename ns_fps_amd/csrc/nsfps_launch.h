@@ -47,7 +47,8 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
                              uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
                              const RangeDev &r, const float4 *P4, const uint2 *RO,
                              float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
-                             uint64_t *leaf_key, float4 *leaf_pos, hipStream_t st);
+                             uint32_t *leaf_al, uint64_t *leaf_key, float4 *leaf_pos,
+                             hipStream_t st);
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st);
 
 // The build of many clouds, each step one launch for all of them (grid y =
@@ -78,7 +79,7 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
 hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t lds_bytes,
                             bool profile, uint32_t threads, hipStream_t st);
-constexpr uint32_t kProfWords = 24;
+constexpr uint32_t kProfWords = 32;
 
 // speculative-run engine
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);
@@ -86,10 +87,11 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 // fused rounds of one cloud (refinements, gather pass, then the run with
 // `helpers` helper workgroups applying its picks), after one update pass
 // (launch_update_pass) for the first pick.
-// *seq counts the call's fused launches (each gets the next number).
+// *seq counts the call's fused launches (each gets the next number).  alias:
+// some cloud's cells share buckets (classic rounds only).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, uint32_t passes, bool profile, uint32_t helpers,
-                         uint32_t *seq, hipStream_t st);
+                         uint32_t rounds, uint32_t passes, bool profile, bool alias,
+                         uint32_t helpers, uint32_t *seq, hipStream_t st);
 hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                               hipStream_t st);
 uint32_t fused_max_nodes_per_helper();

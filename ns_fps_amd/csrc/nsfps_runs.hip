@@ -39,6 +39,11 @@ constexpr uint32_t kSparseGroups = 128;  // workgroups per cloud of the refineme
 constexpr uint32_t kGatherNodes = 16;    // nodes per list-range claim of the gather pass
 constexpr uint32_t kGatherHold = 4;      // hot leaves per wave whose points stay in registers
 
+// Work counters of the grid-wide passes (profile words, summed over rounds):
+// leaves whose points the update pass reads and those points, and the same
+// for the gather pass.
+enum : uint32_t { kCtUpLeaves = 24, kCtUpPoints, kCtGaLeaves, kCtGaPoints };
+
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
   return x | (y << 10) | (z << 20);
 }
@@ -192,7 +197,12 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // is searched only otherwise.  Reads that do not depend on each other are
 // issued together: the wave's leaf records with the run state and the node's
 // record, a pick's cube with its position, and the points of every leaf of
-// the wave that needs reading.
+// the wave that needs reading.  PROF: counts the leaves and points it reads.
+// ALIAS: cells share buckets, and a pick touches a leaf when its cube holds
+// any cell of the leaf's bucket (src/yuezu_fps.cpp:573-597 updates every point
+// of every bucket of the cube's cells); nodes are screened by the corners of
+// those cells.
+template <bool PROF, bool ALIAS>
 __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
@@ -224,15 +234,28 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t hsel = rs.hsel;
   const uint32_t gn = g < c.nl1 ? g : 0u;  // read unconditionally, used only if g < nl1
   const uint64_t nkey = gptr(c.l1_key)[gn];
-  const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
-  // the run state and the node's record are read together, ahead of the exit
-  pin_sgpr(done, npicks, kref, S, hsel, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
-  if (g >= c.nl1 || done || nlo.x > nhi.x) return;  // finished, or no points
+  uint32_t clo, chi;
+  // the cells of this wave's leaves' buckets: lane i < kLeavesPerWave * na
+  // holds word i of the wave's stretch of leaf_al
+  const uint32_t na = ALIAS ? c.r.na : 1u;
+  uint32_t mal = kNoCell;
+  if (ALIAS) {
+    const uint2 cb = gptr(c.l1_cbox)[gn];
+    if (lane < kLeavesPerWave * na && leaf0 + lane / na < c.nleaves)
+      mal = gptr(c.leaf_al)[(size_t)leaf0 * na + lane];
+    pin_sgpr(done, npicks, kref, S, hsel, nkey, cb.x, cb.y);
+    if (g >= c.nl1 || done || cb.x == kNone) return;  // finished, or no points
+    clo = cb.x;
+    chi = cb.y;
+  } else {
+    const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
+    // the run state and the node's record are read together, ahead of the exit
+    pin_sgpr(done, npicks, kref, S, hsel, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
+    if (g >= c.nl1 || done || nlo.x > nhi.x) return;  // finished, or no points
+    clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y), cell_axis(c.r, 2, nlo.z));
+    chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y), cell_axis(c.r, 2, nhi.z));
+  }
   const uint64_t wlo = window_lo(kref, S);
-  const uint32_t clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y),
-                                 cell_axis(c.r, 2, nlo.z));
-  const uint32_t chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y),
-                                 cell_axis(c.r, 2, nhi.z));
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   if (tid == 0) s_np = 0;
   __syncthreads();
@@ -256,18 +279,38 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   uint32_t cell[kLeavesPerWave], st[kLeavesPerWave], cnt[kLeavesPerWave];
   uint64_t okey[kLeavesPerWave], hm[kLeavesPerWave];
   bool hit[kLeavesPerWave], need[kLeavesPerWave];
+  // pick i's cube holds (a cell of the bucket of) leaf k
+  const auto touches = [&](uint32_t k, uint32_t i) -> bool {
+    const uint2 cube = s_pc[i];
+    if (!ALIAS) return cell_in(cell[k], cube);
+    bool in = false;
+    for (uint32_t a = 0; a < na; ++a) in |= cell_in(rdlane(mal, k * na + a), cube);
+    return in;
+  };
 #pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
     cell[k] = rdlane(mcell, k);
     st[k] = rdlane(mst, k);
     cnt[k] = rdlane(mcnt, k);
     okey[k] = ((uint64_t)rdlane((uint32_t)(mkey >> 32), k) << 32) | rdlane((uint32_t)mkey, k);
-    hm[k] = __ballot(lane < nsel && cell_in(cell[k], s_pc[lane]));
+    hm[k] = __ballot(lane < nsel && touches(k, lane));
     bool h = hm[k] != 0;
     for (uint32_t cb = 64; cb < nsel && !h; cb += 64)
-      h = __ballot(cb + lane < nsel && cell_in(cell[k], s_pc[cb + lane])) != 0;
+      h = __ballot(cb + lane < nsel && touches(k, cb + lane)) != 0;
     hit[k] = h;
     need[k] = leaf0 + k < c.nleaves && (h || okey[k] >= wlo);
+  }
+  if (PROF && lane == 0) {
+    uint32_t nl = 0, npt = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+      nl += need[k] ? 1u : 0u;
+      npt += need[k] ? cnt[k] : 0u;
+    }
+    if (nl) {
+      atomicAdd((unsigned long long *)gptr(c.prof) + kCtUpLeaves, (unsigned long long)nl);
+      atomicAdd((unsigned long long *)gptr(c.prof) + kCtUpPoints, (unsigned long long)npt);
+    }
   }
   float4 p[kLeavesPerWave];
   uint2 ro[kLeavesPerWave];
@@ -298,8 +341,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
         float d = p[k].w;
         if (hit[k]) {
           for (uint32_t cb = 0; cb < nsel; cb += 64) {
-            uint64_t m =
-                cb == 0 ? hm[k] : __ballot(cb + lane < nsel && cell_in(cell[k], s_pc[cb + lane]));
+            uint64_t m = cb == 0 ? hm[k] : __ballot(cb + lane < nsel && touches(k, cb + lane));
             while (m) {
               const uint32_t j = (uint32_t)__ffsll((long long)m) - 1;
               m &= m - 1;
@@ -404,7 +446,11 @@ __device__ __forceinline__ uint32_t bit_length(uint64_t v) { return v ? 64u - __
 // is >= it to the list.  When no threshold below the maximum fits the list
 // (more than kListCap keys inside the finest bin), the threshold is the
 // maximum key itself: a run of one sample.  Few workgroups, each striding over
-// the level-1 nodes; most nodes hold no key above the threshold.
+// the level-1 nodes; most nodes hold no key above the threshold.  PROF: counts
+// the hot leaves whose points it reads and those points.  ALIAS (cells share
+// buckets): an entry's cell is its point's own (where its cube is centred
+// when it becomes a sample), and it carries the cells of its bucket.
+template <bool PROF, bool ALIAS>
 __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restrict__ clouds,
                                                          uint32_t passes) {
   __shared__ uint32_t s_sc[kPassWaves + 2];
@@ -462,15 +508,26 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     }
     if (tid == 0) s_cnt = 0;
     uint64_t rest = __ballot(hot);
+    if (PROF) {
+      const uint64_t hp = __ballot(hot);
+      const uint32_t pts = rdlane(wave_incl_scan(hot ? lcnt : 0u), 63);
+      if (lane == 0 && hp) {
+        atomicAdd((unsigned long long *)gptr(c.prof) + kCtGaLeaves,
+                  (unsigned long long)__popcll(hp));
+        atomicAdd((unsigned long long *)gptr(c.prof) + kCtGaPoints, (unsigned long long)pts);
+      }
+    }
     float4 hp[kGatherHold];
     uint2 hr[kGatherHold];
-    uint32_t hcell[kGatherHold], hn[kGatherHold];
+    uint32_t hcell[kGatherHold], hn[kGatherHold], hal[kGatherHold];
     uint64_t htk[kGatherHold];
+    const uint32_t na = ALIAS ? c.r.na : 1u;
 #pragma unroll
     for (uint32_t u = 0; u < kGatherHold; ++u) {
       hp[u] = make_float4(0.f, 0.f, 0.f, 0.f);
       hr[u] = make_uint2(0u, 0u);
       hcell[u] = 0;
+      hal[u] = kNoCell;  // lane a < na: cell a of the held leaf's bucket
       hn[u] = 0;  // points of the held leaf (none: no leaf)
       if (rest) {
         const uint32_t j = (uint32_t)__builtin_ctzll(rest);
@@ -482,6 +539,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
           hp[u] = gptr(c.P4)[st + lane];
           hr[u] = gptr(c.RO)[st + lane];
         }
+        if (ALIAS && lane < na) hal[u] = gptr(c.leaf_al)[(size_t)rdlane(lf, j) * na + lane];
       }
     }
     uint32_t mine = 0;
@@ -510,13 +568,20 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     if (tid == 0) s_base = s_cnt ? atomicAdd(&rs.nlist, s_cnt) : 0u;
     __syncthreads();
     base = s_base + rdlane(base, 0);
-    const auto put = [&](const float4 &p, const uint2 &ro, uint32_t cell, uint64_t m) {
+    const auto put = [&](const float4 &p, const uint2 &ro, uint32_t cell, uint32_t al,
+                         uint64_t m) {
       if ((m >> lane) & 1u) {
         const uint32_t i = base + lanes_below(m);
         if (i < kListCap) {
           gptr(c.list_p)[i] = p;
           gptr(c.list_r)[i] = ro;
-          gptr(c.list_c)[i] = cell;
+          if (ALIAS) {
+            gptr(c.list_c)[i] =
+                pack_cell(cell_axis(c.r, 0, p.x), cell_axis(c.r, 1, p.y), cell_axis(c.r, 2, p.z));
+            for (uint32_t a = 0; a < na; ++a) gptr(c.list_al)[(size_t)i * na + a] = rdlane(al, a);
+          } else {
+            gptr(c.list_c)[i] = cell;
+          }
         } else {
           rs.err = 1;
         }
@@ -524,7 +589,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       base += (uint32_t)__popcll(m);
     };
 #pragma unroll
-    for (uint32_t u = 0; u < kGatherHold; ++u) put(hp[u], hr[u], hcell[u], htk[u]);
+    for (uint32_t u = 0; u < kGatherHold; ++u) put(hp[u], hr[u], hcell[u], hal[u], htk[u]);
     rest = later;
     while (rest) {
       const uint32_t j = (uint32_t)__builtin_ctzll(rest);
@@ -532,12 +597,14 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       const uint32_t st = rdlane(lst, j), cnt = rdlane(lcnt, j);
       float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
       uint2 ro = make_uint2(0u, 0u);
+      uint32_t al = kNoCell;
       if (lane < cnt) {
         p = gptr(c.P4)[st + lane];
         ro = gptr(c.RO)[st + lane];
       }
+      if (ALIAS && lane < na) al = gptr(c.leaf_al)[(size_t)rdlane(lf, j) * na + lane];
       const bool take = lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
-      put(p, ro, rdlane(lcell, j), __ballot(take));
+      put(p, ro, rdlane(lcell, j), al, __ballot(take));
     }
     __syncthreads();  // s_base is read before the next chunk's claim
   }
@@ -742,9 +809,15 @@ __device__ __forceinline__ void put_record(NSFPS_GLOBAL uint64_t *r, uint32_t ta
 // fused round, which also publishes every hot set's samples as tagged
 // records for the round's helpers, names its pick count at the end
 // (RunState::fin) and hands the histogram set the helpers counted into to
-// the next selection.
-template <bool PROF, bool FUSED>
+// the next selection.  ALIAS: cells share buckets.  A sample then updates
+// every entry whose bucket has a cell inside its cube (src/yuezu_fps.cpp:
+// 573-597).  The walk finds entries by their own cell; the entries whose
+// bucket has further cells are few and listed apart, and after each walk
+// every one of them is tested against every sample of the hot set; the
+// phases test every cell of a hot copy's bucket.
+template <bool PROF, bool FUSED, bool ALIAS>
 __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
+  static_assert(!(FUSED && ALIAS), "fused rounds need one cell per bucket");
   __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, fine cell}
   __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
   __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
@@ -768,6 +841,16 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
   __shared__ uint32_t s_wr[2][kRunWaves][2];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
+  // ALIAS: the cells of each entry's bucket (pack11, kNoCell-padded, at the
+  // entry's sorted position), the sorted positions of the entries whose
+  // bucket has several cells, the hot copies' positions, and the hot set's
+  // samples by output order: cube corners (pack11; hi with guards) and x, y, z
+  __shared__ uint32_t s_al[ALIAS ? kListCap * kMaxAlias : 1];
+  __shared__ uint32_t s_alist[ALIAS ? kListCap : 1];
+  __shared__ uint32_t s_nal;
+  __shared__ uint32_t s_hpos[kHot];
+  __shared__ uint2 s_sbox[ALIAS ? kHot : 1];
+  __shared__ float4 s_spos[ALIAS ? kHot : 1];
   const uint64_t rt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
@@ -793,12 +876,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   float4 P[kOwnSlots];
   uint2 R[kOwnSlots];
   uint32_t C[kOwnSlots];
+  const uint32_t na = ALIAS ? c.r.na : 1u;
+  uint32_t AL[ALIAS ? kOwnSlots : 1][kMaxAlias];
 #pragma unroll
   for (uint32_t s = 0; s < kOwnSlots; ++s) {
     const uint32_t i = s * kRunThreads + tid;
     P[s] = gptr(c.list_p)[i];
     R[s] = gptr(c.list_r)[i];
     C[s] = gptr(c.list_c)[i];
+    if (ALIAS) {
+#pragma unroll
+      for (uint32_t a = 0; a < kMaxAlias; ++a)
+        AL[s][a] = a < na && i < nlist ? gptr(c.list_al)[(size_t)i * na + a] : kNoCell;
+    }
   }
   uint64_t pf[kRpWords] = {}, tl = 0;
   if (PROF) tl = __builtin_amdgcn_s_memtime();
@@ -830,6 +920,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   if (tid < kHot) s_hq[0][tid] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
   if (tid == 0) {
     s_nhot = 0;
+    if (ALIAS) s_nal = 0;
     s_geo[0] = sx | (sy << 8) | (sz << 16);
     s_geo[1] = ncx;
     s_geo[2] = ncy;
@@ -880,6 +971,12 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                                __float_as_uint(P[s].z), C[s]);
         s_dd[pos] = __float_as_uint(P[s].w);
         s_rk[pos] = make_uint2(~R[s].x, R[s].y);
+        if (ALIAS) {
+#pragma unroll
+          for (uint32_t a = 0; a < kMaxAlias; ++a) s_al[pos * kMaxAlias + a] = pack11(AL[s][a]);
+          // the bucket's cells come first: a second one means further cells
+          if (AL[s][1] != kNoCell) s_alist[atomicAdd(&s_nal, 1u)] = pos;
+        }
       }
     }
     __syncthreads();
@@ -1009,6 +1106,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
             s_hx[hi] = make_uint4(cc[s], lo[s], __float_as_uint(d[s]), 0u);
             s_hp[hi] = make_uint4(__float_as_uint(x[s]), __float_as_uint(y[s]),
                                   __float_as_uint(z[s]), row[s]);
+            if (ALIAS) s_hpos[hi] = s * kRunThreads + tid;
           } else {  // cannot happen (at most kHot keys are >= the hot threshold)
             *err = 2;
           }
@@ -1048,6 +1146,25 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     bool my_acc = false;
     uint64_t my_key = 0;  // the copy's key at the last phase (0: none, or accepted)
     uint32_t my_out = 0, my_qc = 0, my_hh = 0;
+    // ALIAS: the cells of copy j's bucket (pack11; kNoCell's packing never
+    // lies in a clipped box).  Unused slots read some entry's cells: they
+    // have key 0 and are never compared.
+    uint32_t ja[kMaxAlias];
+    if (ALIAS) {
+      const uint32_t pj = s_hpos[hj] & (kListCap - 1u);
+#pragma unroll
+      for (uint32_t a = 0; a < kMaxAlias; ++a) ja[a] = s_al[pj * kMaxAlias + a];
+    }
+    // 1 when (a cell of the bucket of) copy j lies in the box of pack11
+    // corners lo, hig
+    const auto j_in = [&](uint32_t cg, uint32_t c11, uint32_t lo, uint32_t hig) -> uint32_t {
+      if (!ALIAS) return in_box11(cg, c11, lo, hig);
+      uint32_t r = 0;
+#pragma unroll
+      for (uint32_t a = 0; a < kMaxAlias; ++a)
+        if (a < na) r |= in_box11(ja[a] | kGuards, ja[a], lo, hig);
+      return r;
+    };
     while (true) {
       const uint4 me = s_hq[ph][hot_slot(hj)];
       const uint4 mx = s_hx[hj];
@@ -1065,7 +1182,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       for (uint32_t u = 0; u < kCmp; ++u) {
         const uint32_t gt = (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > mkey);
         cnt += gt;
-        cand |= (gt & in_box11(mx.y, mx.z, og[u].x, og[u].y)) << u;
+        cand |= (gt & j_in(mx.y, mx.z, og[u].x, og[u].y)) << u;
       }
       uint32_t low = 0;
       if (cand) {  // rare: the exact distance decides
@@ -1192,7 +1309,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
 #pragma unroll
         for (uint32_t u = 0; u < kCmp; ++u)
           cand2 |= ((rk[u] < kHot ? (uint32_t)(accr >> rk[u]) & 1u : 0u) &
-                    in_box11(mx.y, mx.z, og[u].x, og[u].y))
+                    j_in(mx.y, mx.z, og[u].x, og[u].y))
                    << u;
         if (cand2) {  // rare: the exact distances
           const uint4 pj = s_hp[hj];
@@ -1254,6 +1371,11 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
           pick_c[np + my_out] = make_uint2(lo_c, hi_c);
           s_rp[hj] = rp;
           s_rc[hj] = make_uint4(lo_c, hi_c, qc, hh);
+          if (ALIAS) {
+            s_sbox[my_out] = make_uint2(pack11(lo_c), pack11(hi_c) | kGuards);
+            s_spos[my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
+                                         __uint_as_float(rp.z), 0.f);
+          }
           if (FUSED) put_record(gptr(c.rec) + (size_t)(np + my_out) * kRecWords, tag, rp, lo_c, hi_c);
         }
         const uint32_t x0 = (lo_c & 1023u) >> gsx, x1 = (hi_c & 1023u) >> gsx;
@@ -1303,6 +1425,34 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       if (FUSED && tid == 0)  // the hot set's records are written (or on their way)
         __hip_atomic_store(&rs.pub, ((uint64_t)tag << 32) | (np + npk), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+      if (ALIAS) {
+        // the entries whose bucket has several cells, against every sample
+        // of the hot set (one thread per entry; the walk is done)
+        const uint32_t nal = s_nal;
+        for (uint32_t ia = tid; ia < nal; ia += kRunThreads) {
+          const uint32_t pe = s_alist[ia];
+          const uint4 pp = s_pc[pe];
+          uint32_t ea[kMaxAlias];
+#pragma unroll
+          for (uint32_t a = 0; a < kMaxAlias; ++a) ea[a] = s_al[pe * kMaxAlias + a];
+          uint32_t dm = s_dd[pe];
+          for (uint32_t k = 0; k < npk; ++k) {
+            const uint2 bx = s_sbox[k];
+            uint32_t in = 0;
+#pragma unroll
+            for (uint32_t a = 0; a < kMaxAlias; ++a)
+              if (a < na) in |= in_box11(ea[a] | kGuards, ea[a], bx.x, bx.y);
+            if (in) {
+              const float4 q = s_spos[k];
+              const float dd = sqdist(__uint_as_float(pp.x), __uint_as_float(pp.y),
+                                      __uint_as_float(pp.z), q.x, q.y, q.z);
+              dm = min(dm, __float_as_uint(dd));  // non-negative floats order like their bits
+            }
+          }
+          s_dd[pe] = dm;
+        }
+        __syncthreads();
+      }
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s)
         if (s * kRunThreads + tid < nlist) d[s] = __uint_as_float(s_dd[s * kRunThreads + tid]);
@@ -1380,9 +1530,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
 #undef NSFPS_RMARK
 }
 
-template <bool PROF>
+template <bool PROF, bool ALIAS>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  run_list<PROF, false>(clouds[blockIdx.x], 0u);
+  run_list<PROF, false, ALIAS>(clouds[blockIdx.x], 0u);
 }
 
 
@@ -1725,7 +1875,7 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
 template <bool PROF>
 __global__ __launch_bounds__(kRunThreads) void k_round(const CloudDev *__restrict__ clouds,
                                                        uint32_t seq) {
-  if (blockIdx.x == 0) run_list<PROF, true>(clouds[0], seq);
+  if (blockIdx.x == 0) run_list<PROF, true, false>(clouds[0], seq);
   else help_list<PROF>(clouds[0], blockIdx.x - 1, gridDim.x - 1, seq);
 }
 
@@ -1774,7 +1924,7 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 
 hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                               hipStream_t st) {
-  k_update<<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
+  k_update<false, false><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
   return hipGetLastError();
 }
 
@@ -1790,16 +1940,31 @@ hipError_t fused_blocks_per_cu(int *blocks) {
   return hipSuccess;
 }
 
+// The classic round's update, gather and run kernels of one variant.
+template <bool PROF, bool ALIAS>
+void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
+                    uint32_t passes, hipStream_t st) {
+  k_update<PROF, ALIAS><<<grid, kPassThreads, 0, st>>>(d_clouds);
+  for (uint32_t p = 1; p <= passes; ++p)
+    k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
+  k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
+  k_run<PROF, ALIAS><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+}
+
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                         uint32_t rounds, uint32_t passes, bool profile, uint32_t helpers,
-                         uint32_t *seq, hipStream_t st) {
+                         uint32_t rounds, uint32_t passes, bool profile, bool alias,
+                         uint32_t helpers, uint32_t *seq, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
-  if (helpers) {  // fused rounds of one cloud
+  if (helpers) {  // fused rounds of one cloud (one cell per bucket)
+    if (alias) return hipErrorInvalidValue;
     for (uint32_t r = 0; r < rounds; ++r) {
       for (uint32_t p = 1; p <= passes; ++p)
         k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
-      k_gather<<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
+      if (profile)
+        k_gather<true, false><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
+      else
+        k_gather<false, false><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
       const uint32_t q = ++*seq;
       if (profile)
         k_round<true><<<1 + helpers, kRunThreads, 0, st>>>(d_clouds, q);
@@ -1809,14 +1974,10 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
     return hipGetLastError();
   }
   for (uint32_t r = 0; r < rounds; ++r) {
-    k_update<<<grid, kPassThreads, 0, st>>>(d_clouds);
-    for (uint32_t p = 1; p <= passes; ++p)
-      k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
-    k_gather<<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
-    if (profile)
-      k_run<true><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
-    else
-      k_run<false><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    if (profile && alias) launch_classic<true, true>(d_clouds, nclouds, grid, sparse, passes, st);
+    else if (profile) launch_classic<true, false>(d_clouds, nclouds, grid, sparse, passes, st);
+    else if (alias) launch_classic<false, true>(d_clouds, nclouds, grid, sparse, passes, st);
+    else launch_classic<false, false>(d_clouds, nclouds, grid, sparse, passes, st);
   }
   return hipGetLastError();
 }

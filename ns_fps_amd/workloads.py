@@ -1,4 +1,5 @@
-"""Seeded synthetic point clouds for the five FPS workloads.
+"""Seeded synthetic point clouds for the FPS workloads: the five benchmark
+configurations and the uniform cube on a 30^3 grid (the general bucket path).
 
 Every generator uses the legacy ``numpy.random.RandomState`` stream (frozen by
 NEP 19, so the same seed gives the same cloud on every machine), draws in
@@ -15,8 +16,8 @@ given block counts.
 
 import numpy as np
 
-__all__ = ["WORKLOADS", "make_workload", "quickstart", "uniform_cube", "lidar_scan",
-           "batched_shapes", "clustered"]
+__all__ = ["WORKLOADS", "make_workload", "quickstart", "uniform_cube", "uniform_cube_30",
+           "lidar_scan", "batched_shapes", "clustered"]
 
 
 def quickstart(n=10000, n_samples=1000):
@@ -38,6 +39,17 @@ def uniform_cube(n=1048576, n_samples=65536):
             "n_samples": n_samples,
             "range": (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 32, 32, 32),
             "blocks": (32, 32, 32)}
+
+
+def uniform_cube_30(n=1048576, n_samples=65536):
+    """The uniform cube's points (seed 2) on a 30^3 grid: block counts that are
+    not powers of two, so Morton codes (src/yuezu_fps.cpp:136-161) taken modulo
+    the block count share buckets (src/yuezu_fps.cpp:413, 592) and the sampling
+    takes the general bucket path."""
+    w = uniform_cube(n, n_samples)
+    w.update(name="uniform_cube_30", range=(-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 30, 30, 30),
+             blocks=(30, 30, 30))
+    return w
 
 
 def _box_surface(rs, centre_xy, sides, ground_z, count):
@@ -156,6 +168,7 @@ def clustered(n_clusters=256, per_cluster=32768, n_samples=524288):
 WORKLOADS = {
     "quickstart": quickstart,
     "uniform_cube": uniform_cube,
+    "uniform_cube_30": uniform_cube_30,
     "lidar_scan": lidar_scan,
     "batched_shapes": batched_shapes,
     "clustered": clustered,

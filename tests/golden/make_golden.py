@@ -6,11 +6,14 @@ script only runs in the container that holds the reference tree.  Outputs:
 
 * tests/golden/cases.npz -- small cases: inputs (points, sample count, range
   or the compute_bbox flag) and the reference's output indices;
-* tests/golden/configs.json -- for the five benchmark workloads: SHA-256 of
-  the generated input and of the reference's int32 output per cloud, output
-  length and the first indices.
+* tests/golden/configs.json -- for the workloads of ns_fps_amd/workloads.py:
+  SHA-256 of the generated input and of the reference's int32 output per
+  cloud, output length and the first indices;
+* tests/golden/census.npz -- per-iteration algorithmic bytes of the same
+  workloads.
 
-Usage: python tests/golden/make_golden.py [--skip-large]
+Usage: python tests/golden/make_golden.py [--skip-large] [--workloads a,b]
+(--workloads regenerates those workloads' entries only and keeps the others).
 """
 
 import argparse
@@ -146,7 +149,11 @@ def census(wnames):
     from the oracle, whose outputs the fixtures above pin to the reference.
     Stored: exact prefix sums for the first 4,096 iterations and the total."""
     o = Oracle()
+    path = os.path.join(HERE, "census.npz")
     out = {}
+    if os.path.exists(path):  # entries of workloads not regenerated are kept
+        with np.load(path, allow_pickle=False) as z:
+            out = {k: z[k] for k in z.files if k.split("__")[0] not in wnames}
     for wname in wnames:
         w = make_workload(wname)
         tot = 0
@@ -160,7 +167,7 @@ def census(wnames):
                 out[f"{wname}__iters"] = np.array([len(idx)], np.uint64)
         out[f"{wname}__total"] = np.array([tot], np.uint64)
         print(f"census {wname}: {tot / 1e9:.3f} GB", flush=True)
-    np.savez_compressed(os.path.join(HERE, "census.npz"), **out)
+    np.savez_compressed(path, **out)
 
 
 def main():
@@ -168,12 +175,22 @@ def main():
     ap.add_argument("--skip-large", action="store_true",
                     help="skip the 8,388,608-point workload (about 4 minutes)")
     ap.add_argument("--census-only", action="store_true")
+    ap.add_argument("--workloads", default="",
+                    help="comma-separated workloads: regenerate only their census and hashes")
     args = ap.parse_args()
-    wl = ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes"]
-    census(wl if args.skip_large else wl + ["clustered"])
+    wl = ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan", "batched_shapes"]
+    if not args.skip_large:
+        wl.append("clustered")
+    only = [n for n in args.workloads.split(",") if n]
+    if only:
+        wl = only
+    census(wl)
     if args.census_only:
         return
     ref = Reference()
+    if only:
+        configs_for(ref, wl)
+        return
     out = {}
     pool = {}  # identical point arrays are stored once: P<i>, referenced by <name>__pid
     for name, p, m, rng, blocks in small_cases():
@@ -195,15 +212,16 @@ def main():
         out[f"{name}__expected"] = e.astype(np.int32)
         print(f"{name:32s} n={len(p):6d} m={m:5d} -> {len(e)} samples", flush=True)
     np.savez_compressed(os.path.join(HERE, "cases.npz"), **out)
+    configs_for(ref, wl)
 
+
+def configs_for(ref, wnames):
     cfg_path = os.path.join(HERE, "configs.json")
     configs = {}
     if os.path.exists(cfg_path):
         with open(cfg_path) as f:
             configs = json.load(f)
-    for wname in ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes", "clustered"]:
-        if wname == "clustered" and args.skip_large:
-            continue
+    for wname in wnames:
         w = make_workload(wname)
         t = time.time()
         outs = [ref.fps(P, w["n_samples"], w["range"], w["blocks"]) for P in w["clouds"]]

@@ -58,7 +58,8 @@ def run_workload(yf, lib, wname):
     return w, g, outs
 
 
-@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes"])
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan",
+                                   "batched_shapes"])
 def test_workload_matches_reference_hash(yf, lib, wname):
     w, g, outs = run_workload(yf, lib, wname)
     assert [len(o) for o in outs] == g["lengths"]
@@ -197,17 +198,43 @@ def test_full_size_properties(yf):
 
 
 def test_engine_choice(yf, monkeypatch):
-    """Speculative runs on one-to-one bucket grids, the tree loop otherwise or
-    when asked for."""
+    """Speculative runs on every grid (cells sharing buckets included), the
+    tree loop when asked for."""
     by = {c.name: c for c in GOLDEN_CASES}
     run_module(yf, by["granularity_32x32x32"])
     st = yf.last_stats()
     assert st["engine"] == "runs" and st["rounds"] >= 1
     run_module(yf, by["general_10x10x10"])
-    assert yf.last_stats()["engine"] == "tree"
+    assert yf.last_stats()["engine"] == "runs"
     monkeypatch.setenv("NSFPS_ENGINE", "tree")
-    run_module(yf, by["granularity_32x32x32"])
-    assert yf.last_stats()["engine"] == "tree"
+    for name in ["granularity_32x32x32", "general_10x10x10"]:
+        assert np.array_equal(run_module(yf, by[name]), by[name].expected)
+        assert yf.last_stats()["engine"] == "tree"
+
+
+# Grids whose cells share buckets (Morton code modulo the block count): up to
+# seven cells per bucket (17^3: codes run to 2^15 over 4,913 buckets), a
+# single block, one axis of 1,000 blocks beside powers of two, an axis of
+# 1,024 blocks, and the 30^3 grid of the general-path benchmark.
+SHARED_GRIDS = [(17, 17, 17), (1, 1, 1), (3, 5, 7), (1000, 4, 2), (1024, 3, 8), (30, 30, 30),
+                (20, 12, 6), (1, 64, 33)]
+
+
+@pytest.mark.parametrize("blocks", SHARED_GRIDS, ids=lambda b: "x".join(map(str, b)))
+def test_shared_bucket_grids_match_oracle(yf, oracle, blocks, monkeypatch):
+    """The runs engine where cells share buckets (every cell of a bucket in a
+    sample's cube updates the bucket's points), against the oracle, and the
+    tree engine on the same input."""
+    rs = np.random.RandomState(sum(blocks))
+    pts = rs.uniform(-1.2, 1.2, (60000, 3)).astype(np.float32)  # some outside: clamped
+    pts[:500] = pts[500:1000]                                     # duplicates
+    rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks)
+    want = oracle.fps(pts, 6000, rng)
+    got = yf.fps(pts, 6000, yf.make_range(*rng))
+    assert yf.last_stats()["engine"] == "runs"
+    assert np.array_equal(got, want)
+    monkeypatch.setenv("NSFPS_ENGINE", "tree")
+    assert np.array_equal(yf.fps(pts, 6000, yf.make_range(*rng)), want)
 
 
 @pytest.mark.parametrize("wname", ["quickstart", "lidar_scan"])
@@ -261,24 +288,34 @@ def test_many_level1_nodes_on_the_runs_engine(yf, oracle):
     assert np.array_equal(got, oracle.fps(pts, 3000, rng))
 
 
-def test_tree_engine_level1_limit_is_reported(yf):
-    """A non-power-of-two grid (tree engine) needing more than 4,096 level-1
-    nodes is refused with a message naming the limit, not sampled wrongly."""
+def test_tree_engine_level1_limit_is_reported(yf, oracle, monkeypatch):
+    """The tree engine, asked for, refuses a cloud needing more than 4,096
+    level-1 nodes with a message naming the limit, not sampling it wrongly;
+    the runs engine (the default) samples the same cloud."""
     rs = np.random.RandomState(22)
     pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)
+    rng = (-1, 1, -1, 1, -1, 1, 100, 100, 100)
+    monkeypatch.setenv("NSFPS_ENGINE", "tree")
     with pytest.raises(RuntimeError, match="level-1 nodes"):
-        yf.fps(pts, 100, yf.make_range(-1, 1, -1, 1, -1, 1, 100, 100, 100))
+        yf.fps(pts, 100, yf.make_range(*rng))
     # the library stays usable after the refusal
     case = {c.name: c for c in GOLDEN_CASES}["general_10x10x10"]
     assert np.array_equal(run_module(yf, case), case.expected)
+    monkeypatch.delenv("NSFPS_ENGINE")
+    assert np.array_equal(yf.fps(pts, 1000, yf.make_range(*rng)), oracle.fps(pts, 1000, rng))
+    assert yf.last_stats()["engine"] == "runs"
 
 
-def test_shared_buckets_visited_once(yf):
+@pytest.mark.parametrize("engine", ["runs", "tree"])
+def test_shared_buckets_visited_once(yf, engine, monkeypatch):
     """Grids whose block counts are not powers of two map several cells to one
-    bucket; each bucket of a cube must be updated by one wave only (two waves
-    on one leaf could pair a new leaf key with an old winner).  Repeated after
-    a large call so that the workspace holds stale data."""
+    bucket; on the tree engine each bucket of a cube must be updated by one
+    wave only (two waves on one leaf could pair a new leaf key with an old
+    winner), and the runs engine must reach every cell of a bucket.  Repeated
+    after a large call so that the workspace holds stale data."""
     from ns_fps_amd.workloads import make_workload
+    if engine == "tree":
+        monkeypatch.setenv("NSFPS_ENGINE", "tree")
     w = make_workload("lidar_scan")
     yf.fps(w["clouds"][0], w["n_samples"], yf.make_range(*w["range"]))
     cases = [c for c in GOLDEN_CASES if c.name.startswith("general_")]
@@ -286,6 +323,7 @@ def test_shared_buckets_visited_once(yf):
     for rep in range(3):
         for case in cases:
             assert np.array_equal(run_module(yf, case), case.expected), (case.name, rep)
+            assert yf.last_stats()["engine"] == engine
 
 
 @pytest.mark.parametrize("name", ["manual_includes_all", "quickstart_full", "lattice_ties_16",

@@ -232,7 +232,8 @@ def test_testpy_distance_sequence_acceptance(oracle, name):
     assert np.max(np.abs(bfs[1:k] - seq[1:k])) < 1e-3
 
 
-@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes"])
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan",
+                                   "batched_shapes"])
 def test_oracle_matches_reference_on_workloads(oracle, wname):
     from ns_fps_amd.workloads import make_workload
     g = GOLDEN_CONFIGS[wname]

@@ -83,8 +83,8 @@ def test_two_plans_alive_at_once(lib, hip):
 @pytest.mark.parametrize("name", ["testpy_10k_1k", "general_10x10x10", "lattice_ties_16",
                                   "tie_bucket_order", "early_stop_duplicates"])
 def test_plan_on_golden_cases(lib, hip, name):
-    """Golden cases through a plan: both engines (general_10x10x10 takes the
-    tree engine), ties, and the trivial guards (m >= n, m = 0, m = 1)."""
+    """Golden cases through a plan: a grid whose cells share buckets
+    (general_10x10x10), ties, and the trivial guards (m >= n, m = 0, m = 1)."""
     case = next(c for c in GOLDEN_CASES if c.name == name)
     if case.range is None:
         pytest.skip("a plan takes an explicit range")

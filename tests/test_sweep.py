@@ -5,8 +5,8 @@ own sources (CPU, where oracle/_ref is built).
 Shapes: uniform box, Gaussian, tight clusters, a flat plane (one axis
 constant), a line, an integer lattice (many equal distances), and clouds
 reaching outside the range (clamped into the boundary cells).  Grids mix
-powers of two (runs engine) with other block counts (tree engine), from 1 to
-64 blocks per axis.
+powers of two (one cell per bucket) with other block counts (cells sharing
+buckets), from 1 to 64 blocks per axis.
 """
 
 import os
