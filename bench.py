@@ -399,10 +399,11 @@ def run_phases(lib, hip, w):
         del os.environ["NSFPS_PROFILE"]
     v = dict(zip(RUN_PHASES, words[:21]))
     ctr = dict(zip(PASS_COUNTERS, words[24:28]))
+    v["walk_wait"], v["alias"], v["alias_entries"] = words[28], words[29], words[30]
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
-    cycles = {k: v[k] for k in ["load", "select", "gather", "rank", "phases", "walk", "apply", "big",
-                                "publish", "tail"]}
+    cycles = {k: v[k] for k in ["load", "select", "gather", "rank", "phases", "walk", "walk_wait",
+                                "alias", "apply", "big", "publish", "tail"]}
     cyc_total = sum(cycles.values())
     rt_us = v["rt_total"] * 0.01
     clock_ghz = cyc_total / (rt_us * 1e3) if rt_us else None
@@ -410,6 +411,7 @@ def run_phases(lib, hip, w):
             "rounds": v["rounds"], "hot_sets": v["hot_sets"], "picks": v["picks"],
             "phases": v["phase_count"], "samples_per_hot_set": round(v["picks"] / hot, 2),
             "phases_per_hot_set": round(v["phase_count"] / hot, 2),
+            "multi_cell_entries_per_hot_set": round(v["alias_entries"] / hot, 1),
             "run_kernel_us_per_round": round(rt_us / rounds, 2),
             "load_us_per_round": round(v["rt_load"] * 0.01 / rounds, 2),
             "run_kernel_us_total": round(rt_us, 1),

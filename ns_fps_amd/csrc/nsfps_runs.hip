@@ -283,6 +283,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const auto touches = [&](uint32_t k, uint32_t i) -> bool {
     const uint2 cube = s_pc[i];
     if (!ALIAS) return cell_in(cell[k], cube);
+    if (na == 2) return cell_in(rdlane(mal, 2 * k), cube) | cell_in(rdlane(mal, 2 * k + 1), cube);
     bool in = false;
     for (uint32_t a = 0; a < na; ++a) in |= cell_in(rdlane(mal, k * na + a), cube);
     return in;
@@ -664,7 +665,12 @@ enum : uint32_t {
   // outlived the run (measured by the next launch's run), launches measured,
   // helper time in steps, helper steps, helper time in the first count, and
   // the latest helper end / the run's end of the launch (absolute; scratch)
-  kHpTail = 16, kHpTailN, kHpStep, kHpSteps, kHpCount, kHpEndMax, kHpRunEnd
+  kHpTail = 16, kHpTailN, kHpStep, kHpSteps, kHpCount, kHpEndMax, kHpRunEnd,
+  // words kept past the first kRpWords (local words 16.., profile words
+  // 28.., after the work counters of the passes): the wait at the barrier
+  // after the walk, the pass over entries whose bucket has several cells,
+  // and those entries summed over hot sets
+  kRpWalkWait = 16, kRpAlias = 17, kRpAliasN = 18, kRpLocal = 19, kRpExtraAt = 28
 };
 
 // Cell inside the cube of a sample at cell qc with packed half-widths h
@@ -846,6 +852,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   // bucket has several cells, the hot copies' positions, and the hot set's
   // samples by output order: cube corners (pack11; hi with guards) and x, y, z
   __shared__ uint32_t s_al[ALIAS ? kListCap * kMaxAlias : 1];
+  __shared__ uint32_t s_ao[ALIAS ? kListCap * kMaxAlias : 1];  // the bucket's other cells
   __shared__ uint32_t s_alist[ALIAS ? kListCap : 1];
   __shared__ uint32_t s_nal;
   __shared__ uint32_t s_hpos[kHot];
@@ -890,7 +897,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         AL[s][a] = a < na && i < nlist ? gptr(c.list_al)[(size_t)i * na + a] : kNoCell;
     }
   }
-  uint64_t pf[kRpWords] = {}, tl = 0;
+  uint64_t pf[kRpLocal] = {}, tl = 0;
   if (PROF) tl = __builtin_amdgcn_s_memtime();
 #define NSFPS_RMARK(ph)                                  \
   do {                                                   \
@@ -972,10 +979,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         s_dd[pos] = __float_as_uint(P[s].w);
         s_rk[pos] = make_uint2(~R[s].x, R[s].y);
         if (ALIAS) {
+          // the bucket's cells, and apart (for the pass after the walk, which
+          // finds the entry by its own cell) its other cells, both in pack11
+          // form; the valid cells come first
+          uint32_t no = 0;
 #pragma unroll
-          for (uint32_t a = 0; a < kMaxAlias; ++a) s_al[pos * kMaxAlias + a] = pack11(AL[s][a]);
-          // the bucket's cells come first: a second one means further cells
-          if (AL[s][1] != kNoCell) s_alist[atomicAdd(&s_nal, 1u)] = pos;
+          for (uint32_t a = 0; a < kMaxAlias; ++a) {
+            s_al[pos * kMaxAlias + a] = pack11(AL[s][a]);
+            if (AL[s][a] != kNoCell && AL[s][a] != C[s]) s_ao[pos * kMaxAlias + no++] = pack11(AL[s][a]);
+          }
+          if (no) {
+            for (uint32_t a = no; a < kMaxAlias; ++a) s_ao[pos * kMaxAlias + a] = pack11(kNoCell);
+            s_alist[atomicAdd(&s_nal, 1u)] = pos;
+          }
         }
       }
     }
@@ -1153,16 +1169,20 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     if (ALIAS) {
       const uint32_t pj = s_hpos[hj] & (kListCap - 1u);
 #pragma unroll
-      for (uint32_t a = 0; a < kMaxAlias; ++a) ja[a] = s_al[pj * kMaxAlias + a];
+      for (uint32_t a = 0; a < kMaxAlias; ++a)
+        ja[a] = a < na ? s_al[pj * kMaxAlias + a] : pack11(kNoCell);
     }
     // 1 when (a cell of the bucket of) copy j lies in the box of pack11
-    // corners lo, hig
+    // corners lo, hig; two cells per bucket (grids near powers of two) take
+    // two tests, more take all kMaxAlias (padding never lies in a box)
+    const bool na2 = na == 2;
     const auto j_in = [&](uint32_t cg, uint32_t c11, uint32_t lo, uint32_t hig) -> uint32_t {
       if (!ALIAS) return in_box11(cg, c11, lo, hig);
-      uint32_t r = 0;
+      uint32_t r = in_box11(ja[0] | kGuards, ja[0], lo, hig) | in_box11(ja[1] | kGuards, ja[1], lo, hig);
+      if (!na2) {
 #pragma unroll
-      for (uint32_t a = 0; a < kMaxAlias; ++a)
-        if (a < na) r |= in_box11(ja[a] | kGuards, ja[a], lo, hig);
+        for (uint32_t a = 2; a < kMaxAlias; ++a) r |= in_box11(ja[a] | kGuards, ja[a], lo, hig);
+      }
       return r;
     };
     while (true) {
@@ -1422,36 +1442,53 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       }
       NSFPS_RMARK(kRpWalk);
       __syncthreads();  // the walks' updates are in LDS
+      NSFPS_RMARK(kRpWalkWait);
       if (FUSED && tid == 0)  // the hot set's records are written (or on their way)
         __hip_atomic_store(&rs.pub, ((uint64_t)tag << 32) | (np + npk), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       if (ALIAS) {
-        // the entries whose bucket has several cells, against every sample
-        // of the hot set (one thread per entry; the walk is done)
-        const uint32_t nal = s_nal;
+        // the entries whose bucket has other cells than their own (the walk
+        // reached them by their own cell), against every sample of the hot
+        // set: a thread per entry; lane k of every wave holds sample k's cube
+        // corners, which the loop reads lane by lane (the walk is done, so
+        // the thread owns the entry's distance)
+        const uint32_t nal = uniform(s_nal), nk = uniform(npk);
+        const uint2 bx = s_sbox[lane < nk ? lane : 0u];
+        if (PROF) pf[kRpAliasN] += nal;
         for (uint32_t ia = tid; ia < nal; ia += kRunThreads) {
           const uint32_t pe = s_alist[ia];
           const uint4 pp = s_pc[pe];
-          uint32_t ea[kMaxAlias];
-#pragma unroll
-          for (uint32_t a = 0; a < kMaxAlias; ++a) ea[a] = s_al[pe * kMaxAlias + a];
           uint32_t dm = s_dd[pe];
-          for (uint32_t k = 0; k < npk; ++k) {
-            const uint2 bx = s_sbox[k];
-            uint32_t in = 0;
+          // sample k's cube holds another cell of the bucket (rare): its distance
+          const auto take = [&](uint32_t k) {
+            const float4 q = s_spos[k];
+            const float dd = sqdist(__uint_as_float(pp.x), __uint_as_float(pp.y),
+                                    __uint_as_float(pp.z), q.x, q.y, q.z);
+            dm = min(dm, __float_as_uint(dd));  // non-negative floats order like their bits
+          };
+          if (na == 2) {  // one other cell (grids near powers of two)
+            const uint32_t e0 = s_ao[pe * kMaxAlias];
+            const uint32_t e0g = e0 | kGuards;
+            for (uint32_t k = 0; k < nk; ++k)
+              if (in_box11(e0g, e0, rdlane(bx.x, k), rdlane(bx.y, k))) take(k);
+          } else {
+            uint32_t eo[kMaxAlias - 1];
 #pragma unroll
-            for (uint32_t a = 0; a < kMaxAlias; ++a)
-              if (a < na) in |= in_box11(ea[a] | kGuards, ea[a], bx.x, bx.y);
-            if (in) {
-              const float4 q = s_spos[k];
-              const float dd = sqdist(__uint_as_float(pp.x), __uint_as_float(pp.y),
-                                      __uint_as_float(pp.z), q.x, q.y, q.z);
-              dm = min(dm, __float_as_uint(dd));  // non-negative floats order like their bits
+            for (uint32_t a = 0; a + 1 < kMaxAlias; ++a)
+              eo[a] = a + 1 < na ? s_ao[pe * kMaxAlias + a] : pack11(kNoCell);
+            for (uint32_t k = 0; k < nk; ++k) {
+              const uint32_t lo = rdlane(bx.x, k), hig = rdlane(bx.y, k);
+              uint32_t in = 0;
+#pragma unroll
+              for (uint32_t a = 0; a + 1 < kMaxAlias; ++a)
+                in |= in_box11(eo[a] | kGuards, eo[a], lo, hig);
+              if (in) take(k);
             }
           }
           s_dd[pe] = dm;
         }
         __syncthreads();
+        NSFPS_RMARK(kRpAlias);
       }
 #pragma unroll
       for (uint32_t s = 0; s < kOwnSlots; ++s)
@@ -1525,6 +1562,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     pf[kRpRtTotal] = __builtin_amdgcn_s_memrealtime() - rt0;
     NSFPS_GLOBAL uint64_t *pw = gptr(c.prof);
     for (uint32_t i = 0; i < kRpWords; ++i) pw[i] += pf[i];
+    for (uint32_t i = kRpWords; i < kRpLocal; ++i) pw[kRpExtraAt + i - kRpWords] += pf[i];
     if (FUSED) pw[kHpRunEnd] = __builtin_amdgcn_s_memrealtime();
   }
 #undef NSFPS_RMARK
