@@ -289,7 +289,8 @@ __device__ __forceinline__ void gather_at(uint32_t p, const uint32_t *__restrict
                                           const uint32_t *__restrict__ cell_start,
                                           const float *__restrict__ xyz, uint32_t n,
                                           uint32_t padded, uint32_t cap, float4 *__restrict__ P4,
-                                          uint2 *__restrict__ RO, uint32_t *__restrict__ phys0) {
+                                          uint2 *__restrict__ RO, uint32_t *__restrict__ R,
+                                          uint32_t *__restrict__ phys0) {
   if (p >= n) return;
   // ranks and rows come from sorts that may hold other clouds: this cloud's
   // start in them is base
@@ -304,6 +305,7 @@ __device__ __forceinline__ void gather_at(uint32_t p, const uint32_t *__restrict
   P4[slot] = make_float4(xyz[3 * (size_t)o], xyz[3 * (size_t)o + 1], xyz[3 * (size_t)o + 2],
                          FLT_MAX);
   RO[slot] = make_uint2(rk, o);
+  R[slot] = rk;
   if (o == 0) *phys0 = slot;
 }
 
@@ -312,9 +314,9 @@ __global__ void k_gather(const uint32_t *__restrict__ prank, const uint32_t *__r
                          const uint32_t *__restrict__ cell_start,
                          const float *__restrict__ xyz, uint32_t n, uint32_t padded, uint32_t cap,
                          float4 *__restrict__ P4, uint2 *__restrict__ RO,
-                         uint32_t *__restrict__ phys0) {
+                         uint32_t *__restrict__ R, uint32_t *__restrict__ phys0) {
   gather_at(blockIdx.x * blockDim.x + threadIdx.x, prank, lorig, base, bucket, cell_start, xyz, n,
-            padded, cap, P4, RO, phys0);
+            padded, cap, P4, RO, R, phys0);
 }
 
 // Leaf descriptors (first slot, point count, cell) of every leaf of bucket b,
@@ -326,7 +328,8 @@ __device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restr
                                              float4 *__restrict__ leaf_lo,
                                              float4 *__restrict__ leaf_hi,
                                              uint32_t *__restrict__ leaf_cell,
-                                             uint32_t *__restrict__ leaf_al) {
+                                             uint32_t *__restrict__ leaf_al,
+                                             uint2 *__restrict__ leaf_sc) {
   if (b >= T) return;
   uint32_t s = cell_start[b], e = cell_start[b + 1];
   uint32_t cntb = e - s;
@@ -345,6 +348,7 @@ __device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restr
     uint32_t cnt = cntb > off ? (cntb - off < kLeaf ? cntb - off : kLeaf) : 0u;
     leaf_lo[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(first + off));
     leaf_hi[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(cnt));
+    leaf_sc[l] = make_uint2(first + off, cnt);
     leaf_cell[l] = packed;
     for (uint32_t a = 0; a < r.na; ++a) leaf_al[(size_t)l * r.na + a] = al[a];
   }
@@ -354,9 +358,10 @@ __global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
                             const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
                             uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
                             float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
-                            uint32_t *__restrict__ leaf_cell, uint32_t *__restrict__ leaf_al) {
+                            uint32_t *__restrict__ leaf_cell, uint32_t *__restrict__ leaf_al,
+                            uint2 *__restrict__ leaf_sc) {
   leaf_desc_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, padded, cap, lpc,
-               r, P4, leaf_lo, leaf_hi, leaf_cell, leaf_al);
+               r, P4, leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
 }
 
 // Leaf bounding boxes and initial keys (FLT_MAX with the smallest rank of the
@@ -606,9 +611,9 @@ hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_lea
 hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
                          const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
                          uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
-                         uint32_t *phys0, hipStream_t st) {
+                         uint32_t *R, uint32_t *phys0, hipStream_t st) {
   k_gather<<<cdiv(n, 256), 256, 0, st>>>(prank, lorig, base, bucket, cell_start, xyz, n, padded,
-                                         cap, P4, RO, phys0);
+                                         cap, P4, RO, R, phys0);
   return hipGetLastError();
 }
 
@@ -616,10 +621,10 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
                              uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
                              const RangeDev &r, const float4 *P4, const uint2 *RO,
                              float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
-                             uint32_t *leaf_al, uint64_t *leaf_key, float4 *leaf_pos,
-                             hipStream_t st) {
+                             uint32_t *leaf_al, uint2 *leaf_sc, uint64_t *leaf_key,
+                             float4 *leaf_pos, hipStream_t st) {
   k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
-                                            leaf_lo, leaf_hi, leaf_cell, leaf_al);
+                                            leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
   if (nleaves)
     k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
                                                   leaf_pos);
@@ -665,12 +670,14 @@ __global__ void kb_zero_slots(const BuildDev *__restrict__ bd) {
   if (!b.c.padded || i >= b.c.nslots) return;
   b.c.P4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   const_cast<uint2 *>(b.c.RO)[i] = make_uint2(0u, 0u);
+  const_cast<uint32_t *>(b.c.R)[i] = 0u;
 }
 
 __global__ void kb_gather(const BuildDev *__restrict__ bd) {
   const BuildDev &b = bd[blockIdx.y];
   gather_at(blockIdx.x * blockDim.x + threadIdx.x, b.prank, b.lorig, b.base, b.bucket, b.counts,
-            b.xyz, b.n, b.c.padded, b.cap, b.c.P4, const_cast<uint2 *>(b.c.RO), b.small + 2);
+            b.xyz, b.n, b.c.padded, b.cap, b.c.P4, const_cast<uint2 *>(b.c.RO),
+            const_cast<uint32_t *>(b.c.R), b.small + 2);
 }
 
 __global__ void kb_cells(const BuildDev *__restrict__ bd) {
@@ -679,7 +686,8 @@ __global__ void kb_cells(const BuildDev *__restrict__ bd) {
   cell_info_at(i, b.counts, b.lc, b.T, const_cast<uint2 *>(b.c.cell_info));
   leaf_desc_at(i, b.counts, b.lc, b.T, b.c.padded, b.cap, b.c.lpc, b.c.r, b.c.P4,
                const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
-               const_cast<uint32_t *>(b.c.leaf_cell), const_cast<uint32_t *>(b.c.leaf_al));
+               const_cast<uint32_t *>(b.c.leaf_cell), const_cast<uint32_t *>(b.c.leaf_al),
+               const_cast<uint2 *>(b.c.leaf_sc));
 }
 
 __global__ __launch_bounds__(256) void kb_leaf_bbox(const BuildDev *__restrict__ bd) {

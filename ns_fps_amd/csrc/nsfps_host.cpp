@@ -425,11 +425,13 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   p.d_lut = bp.take<uint32_t>(p.rng.dev.lut_total + 16);
   c.P4 = bp.take<float4>(slots);
   c.RO = bp.take<uint2>(slots);
+  c.R = bp.take<uint32_t>(slots);
   p.d_lc = bp.take<uint32_t>((size_t)T + 1);
   p.d_cell_info = bp.take<uint2>((size_t)T + 1);
   c.cell_info = p.d_cell_info;
   c.leaf_lo = bp.take<float4>(leaves);
   c.leaf_hi = bp.take<float4>(leaves);
+  c.leaf_sc = bp.take<uint2>(leaves);
   c.leaf_cell = bp.take<uint32_t>(leaves);
   c.leaf_al = bp.take<uint32_t>(leaves * p.rng.dev.na);
   c.leaf_key = bp.take<uint64_t>(leaves);
@@ -666,14 +668,17 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
   if (c.padded) {
     HIP_TRY(launch_fill_u32(c.P4, 0u, (uint64_t)c.nslots * 4, st));
     HIP_TRY(launch_fill_u32(const_cast<uint2 *>(c.RO), 0u, (uint64_t)c.nslots * 2, st));
+    HIP_TRY(launch_fill_u32(const_cast<uint32_t *>(c.R), 0u, (uint64_t)c.nslots, st));
   }
   HIP_TRY(launch_gather(prank, lorig, base, p.d_bucket, p.d_counts, xyz, n, c.padded,
-                        (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), p.d_small + 2, st));
+                        (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), const_cast<uint32_t *>(c.R),
+                        p.d_small + 2, st));
   HIP_TRY(launch_cell_info(p.d_counts, p.d_lc, T, p.d_cell_info, st));
   HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.nleaves,
                             p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
                             const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
-                            const_cast<uint32_t *>(c.leaf_al), c.leaf_key, c.leaf_pos, st));
+                            const_cast<uint32_t *>(c.leaf_al), const_cast<uint2 *>(c.leaf_sc),
+                            c.leaf_key, c.leaf_pos, st));
   HIP_TRY(launch_init_state(c, p.d_small + 2, st));
   c.lds = plan_lds(c);
   return NSFPS_OK;

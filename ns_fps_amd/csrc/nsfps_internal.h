@@ -126,9 +126,12 @@ struct CloudDev {
   const uint32_t *lut;
   float4 *P4;                 // x, y, z, min squared distance per slot
   const uint2 *RO;            // logical rank, input row per slot
+  const uint32_t *R;          // logical rank per slot (RO's x apart: the passes over many
+                              // points need the rank alone)
   const uint2 *cell_info;     // T + 1 entries: first slot, first leaf
   const float4 *leaf_lo;      // bbox min xyz, w = first slot (bits)
   const float4 *leaf_hi;      // bbox max xyz, w = point count (bits)
+  const uint2 *leaf_sc;       // first slot, point count (leaf_lo.w / leaf_hi.w packed)
   const uint32_t *leaf_cell;  // ix | iy << 10 | iz << 20
   const uint32_t *leaf_al;    // r.na per leaf: the cells of its bucket, kNoCell-padded
   uint64_t *leaf_key;         // max key of the leaf

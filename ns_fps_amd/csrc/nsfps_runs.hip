@@ -13,6 +13,8 @@
 // min() of exact fp32 distances commutes, so each point ends with the same
 // bits as after the reference's one-by-one updates.  The same pass rebuilds
 // the leaf and level-1 keys and histograms the keys for the next threshold.
+// Only the keys: the samples come from the list, so the winners' positions
+// (leaf_pos, l1_pos, which the tree engine keeps) are not maintained.
 //
 // One round, in stream order:
 //   k_update     picks -> points, leaf and level-1 keys, key histogram
@@ -209,7 +211,6 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   __shared__ float4 s_pp[kListCap];
   __shared__ uint2 s_pc[kListCap];
   __shared__ uint64_t s_lk[kFan];
-  __shared__ float4 s_lp[kFan];
   __shared__ uint32_t s_np;
   const CloudDev &c = clouds[blockIdx.y];
   const uint32_t g = blockIdx.x;
@@ -218,13 +219,12 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t leaf0 = g * kFan + wave * kLeavesPerWave;
   uint64_t mkey = 0;
   uint32_t mcell = 0, mst = 0, mcnt = 0;
-  float4 mpos = make_float4(0.f, 0.f, 0.f, 0.f);
   if (lane < kLeavesPerWave && leaf0 + lane < c.nleaves) {
     mkey = gptr(c.leaf_key)[leaf0 + lane];
-    mpos = gptr(c.leaf_pos)[leaf0 + lane];
     mcell = gptr(c.leaf_cell)[leaf0 + lane];
-    mst = __float_as_uint(gptr(c.leaf_lo)[leaf0 + lane].w);
-    mcnt = __float_as_uint(gptr(c.leaf_hi)[leaf0 + lane].w);
+    const uint2 sc = gptr(c.leaf_sc)[leaf0 + lane];
+    mst = sc.x;
+    mcnt = sc.y;
   }
   const NSFPS_GLOBAL RunState &rs = rstate(c);
   const uint32_t done = *gptr(c.done);
@@ -314,31 +314,26 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     }
   }
   float4 p[kLeavesPerWave];
-  uint2 ro[kLeavesPerWave];
+  uint32_t rk[kLeavesPerWave];  // logical ranks
 #pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
     p[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    ro[k] = make_uint2(0u, 0u);
+    rk[k] = 0;
     if (need[k] && lane < cnt[k]) {
       p[k] = gptr(c.P4)[st[k] + lane];
-      ro[k] = gptr(c.RO)[st[k] + lane];
+      rk[k] = gptr(c.R)[st[k] + lane];
     }
   }
 #pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
     const uint32_t li = wave * kLeavesPerWave + k;
     uint64_t key = 0;
-    float4 pos = make_float4(0.f, 0.f, 0.f, 0.f);
     if (leaf0 + k < c.nleaves) {
       // unchanged unless the point holding the key is lowered below
       key = okey[k];
-      pos = make_float4(__uint_as_float(rdlane(__float_as_uint(mpos.x), k)),
-                        __uint_as_float(rdlane(__float_as_uint(mpos.y), k)),
-                        __uint_as_float(rdlane(__float_as_uint(mpos.z), k)),
-                        __uint_as_float(rdlane(__float_as_uint(mpos.w), k)));
       if (need[k]) {
         const bool act = lane < cnt[k];
-        const uint32_t lo = ~ro[k].x;
+        const uint32_t lo = ~rk[k];
         float d = p[k].w;
         if (hit[k]) {
           for (uint32_t cb = 0; cb < nsel; cb += 64) {
@@ -358,14 +353,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
             uint32_t mh;
             const uint32_t wl = key_winner(hi, lo, act, mh);
             key = ((uint64_t)mh << 32) | rdlane(lo, wl);  // the leaf has points: wl < 64
-            pos = make_float4(__uint_as_float(rdlane(__float_as_uint(p[k].x), wl)),
-                              __uint_as_float(rdlane(__float_as_uint(p[k].y), wl)),
-                              __uint_as_float(rdlane(__float_as_uint(p[k].z), wl)),
-                              __uint_as_float(rdlane(ro[k].y, wl)));
-            if (lane == 0) {
-              gptr(c.leaf_key)[leaf0 + k] = key;
-              gptr(c.leaf_pos)[leaf0 + k] = pos;
-            }
+            if (lane == 0) gptr(c.leaf_key)[leaf0 + k] = key;
           }
         }
         if (act) {
@@ -375,20 +363,14 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
         }
       }
     }
-    if (lane == 0) {
-      s_lk[li] = key;
-      s_lp[li] = pos;
-    }
+    if (lane == 0) s_lk[li] = key;
   }
   __syncthreads();
   if (wave == 0) {
     const uint64_t k = s_lk[lane];
     uint32_t mh;
     const uint32_t wl = key_winner((uint32_t)(k >> 32), (uint32_t)k, true, mh);
-    if (lane == 0) {
-      gptr(c.l1_key)[g] = ((uint64_t)mh << 32) | (uint32_t)s_lk[wl];
-      gptr(c.l1_pos)[g] = s_lp[wl];
-    }
+    if (lane == 0) gptr(c.l1_key)[g] = ((uint64_t)mh << 32) | (uint32_t)s_lk[wl];
   }
   NSFPS_GLOBAL uint32_t *H = hist_set(c, hsel);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
@@ -421,11 +403,11 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
     for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
       const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
       if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < wlo) continue;
-      const uint32_t st = __float_as_uint(gptr(c.leaf_lo)[leaf].w);
-      const uint32_t cnt = __float_as_uint(gptr(c.leaf_hi)[leaf].w);
+      const uint2 sc = gptr(c.leaf_sc)[leaf];
+      const uint32_t st = sc.x, cnt = sc.y;
       if (lane < cnt) {
         const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
-        const uint32_t rank = gptr(c.RO)[st + lane].x;
+        const uint32_t rank = gptr(c.R)[st + lane];
         const uint32_t b = key_bin(((uint64_t)__float_as_uint(d) << 32) | ~rank, s.kref, s.S);
         if (b != kNone) atomicAdd(&s_hist[b], 1u);
       }
@@ -503,8 +485,9 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     uint32_t lst = 0, lcnt = 0, lcell = 0;
     if (gq < c.nl1 && lf < c.nleaves) {
       hot = gptr(c.leaf_key)[lf] >= bkey;
-      lst = __float_as_uint(gptr(c.leaf_lo)[lf].w);
-      lcnt = __float_as_uint(gptr(c.leaf_hi)[lf].w);
+      const uint2 sc = gptr(c.leaf_sc)[lf];
+      lst = sc.x;
+      lcnt = sc.y;
       lcell = gptr(c.leaf_cell)[lf];
     }
     if (tid == 0) s_cnt = 0;
@@ -558,7 +541,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       bool take = false;
       if (lane < cnt) {
         const float d = ((const NSFPS_GLOBAL float *)gptr(c.P4 + st + lane))[3];
-        take = (((uint64_t)__float_as_uint(d) << 32) | ~gptr(c.RO)[st + lane].x) >= bkey;
+        take = (((uint64_t)__float_as_uint(d) << 32) | ~gptr(c.R)[st + lane]) >= bkey;
       }
       mine += (uint32_t)__popcll(__ballot(take));
     }
@@ -1624,7 +1607,6 @@ template <bool PROF>
 __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_t H, uint32_t seq) {
   __shared__ uint32_t s_hh[kHistBins];           // my points' keys in the next window
   __shared__ uint64_t s_lk[kHelpLeaves];         // my leaves: keys,
-  __shared__ float4 s_lp[kHelpLeaves];           //   winners,
   __shared__ uint32_t s_lc[kHelpLeaves];         //   cells,
   __shared__ uint2 s_ls[kHelpLeaves];            //   first slot and point count
   __shared__ uint2 s_nb[kMaxHelpNodes];          // my nodes' cell ranges; x = kNone: no points
@@ -1648,23 +1630,19 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
   const uint64_t wlo = window_lo(kref, S);
   const uint32_t nlv = nmine * kFan;
   const NSFPS_GLOBAL float4 *const P4 = gptr(c.P4);
-  const NSFPS_GLOBAL uint2 *const RO = gptr(c.RO);
+  const NSFPS_GLOBAL uint32_t *const R = gptr(c.R);
   for (uint32_t j = tid; j < kHistBins; j += kRunThreads) s_hh[j] = 0;
   for (uint32_t i = tid; i < nlv; i += kRunThreads) {
     const uint32_t leaf = (h + (i / kFan) * H) * kFan + i % kFan;
     uint64_t k = 0;
-    float4 lp = make_float4(0.f, 0.f, 0.f, 0.f);
     uint32_t cl = 0;
     uint2 ls = make_uint2(0u, 0u);
     if (leaf < c.nleaves) {
       k = gptr(c.leaf_key)[leaf];
-      lp = gptr(c.leaf_pos)[leaf];
       cl = gptr(c.leaf_cell)[leaf];
-      ls = make_uint2(__float_as_uint(gptr(c.leaf_lo)[leaf].w),
-                      __float_as_uint(gptr(c.leaf_hi)[leaf].w));
+      ls = gptr(c.leaf_sc)[leaf];
     }
     s_lk[i] = k;
-    s_lp[i] = lp;
     s_lc[i] = cl;
     s_ls[i] = ls;
   }
@@ -1694,7 +1672,7 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
       rk[k] = 0;
       if (s_lk[lb + k] >= wlo && lane < ls.y) {
         p[k] = P4[ls.x + lane];
-        rk[k] = RO[ls.x + lane].x;
+        rk[k] = R[ls.x + lane];
       }
     }
 #pragma unroll
@@ -1804,16 +1782,16 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
         }
       }
       float4 p[kHelpChunk][kHelpLPW];
-      uint2 ro[kHelpChunk][kHelpLPW];
+      uint32_t rr[kHelpChunk][kHelpLPW];  // logical ranks
 #pragma unroll
       for (uint32_t kk = 0; kk < kHelpChunk; ++kk)
 #pragma unroll
         for (uint32_t j = 0; j < kHelpLPW; ++j) {
           p[kk][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-          ro[kk][j] = make_uint2(0u, 0u);
+          rr[kk][j] = 0;
           if (hit[kk][j] && lane < cnt[kk][j]) {
             p[kk][j] = P4[st[kk][j] + lane];
-            ro[kk][j] = RO[st[kk][j] + lane];
+            rr[kk][j] = R[st[kk][j] + lane];
           }
         }
 #pragma unroll
@@ -1827,7 +1805,7 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
         for (uint32_t j = 0; j < kHelpLPW; ++j) {
           if (!hit[kk][j]) continue;
           const bool act = lane < cnt[kk][j];
-          const uint32_t lo = ~ro[kk][j].x;
+          const uint32_t lo = ~rr[kk][j];
           float d = p[kk][j].w;
           for (uint32_t cb = 0; cb < nsel[kk]; cb += 64) {
             uint64_t m = cb == 0 ? hm[kk][j]
@@ -1854,15 +1832,9 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
             uint32_t mh;
             const uint32_t wl = key_winner(hi, lo, act, mh);
             const uint64_t key = ((uint64_t)mh << 32) | rdlane(lo, wl);
-            const float4 pos = make_float4(__uint_as_float(rdlane(__float_as_uint(p[kk][j].x), wl)),
-                                           __uint_as_float(rdlane(__float_as_uint(p[kk][j].y), wl)),
-                                           __uint_as_float(rdlane(__float_as_uint(p[kk][j].z), wl)),
-                                           __uint_as_float(rdlane(ro[kk][j].y, wl)));
             if (lane == 0) {
               s_lk[lb + j] = key;
-              s_lp[lb + j] = pos;
               gptr(c.leaf_key)[leaf0 + j] = key;
-              gptr(c.leaf_pos)[leaf0 + j] = pos;
             }
             changed = true;
           }
@@ -1878,11 +1850,7 @@ __device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_
       const uint64_t kk = s_lk[k * kFan + lane];
       uint32_t mh;
       const uint32_t wl = key_winner((uint32_t)(kk >> 32), (uint32_t)kk, true, mh);
-      if (lane == 0) {
-        const uint32_t g = h + k * H;
-        gptr(c.l1_key)[g] = ((uint64_t)mh << 32) | (uint32_t)s_lk[k * kFan + wl];
-        gptr(c.l1_pos)[g] = s_lp[k * kFan + wl];
-      }
+      if (lane == 0) gptr(c.l1_key)[h + k * H] = ((uint64_t)mh << 32) | (uint32_t)s_lk[k * kFan + wl];
     }
     applied += nb;
     stalled = nb == 0;
