@@ -399,6 +399,7 @@ def run_phases(lib, hip, w):
         del os.environ["NSFPS_PROFILE"]
     v = dict(zip(RUN_PHASES, words[:21]))
     ctr = dict(zip(PASS_COUNTERS, words[24:28]))
+    ctr.update(zip(["up_t_picks", "up_t_leaves", "up_t_flush", "up_groups"], words[32:36]))
     v["walk_wait"], v["alias"], v["alias_entries"] = words[28], words[29], words[30]
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
@@ -441,6 +442,13 @@ def pass_counts(wname, ctr, rounds):
     dev = 16 * (ctr["update_points"] + ctr["gather_points"]) + \
         8 * (ctr["update_leaves"] + ctr["gather_leaves"])
     out["device_bytes_at_census_prices"] = int(dev)
+    if ctr.get("up_groups"):
+        ng = ctr["up_groups"]
+        out["update_pass_us_per_workgroup"] = {
+            "state_node_picks": round(ctr["up_t_picks"] * 0.01 / ng, 2),
+            "leaves": round(ctr["up_t_leaves"] * 0.01 / ng, 2),
+            "node_key_flush": round(ctr["up_t_flush"] * 0.01 / ng, 2),
+            "workgroups_per_round": round(ng / rounds, 1)}
     if census is not None:
         out["census_alg_bytes"] = census["total"]
         out["device_over_census"] = round(dev / census["total"], 4)

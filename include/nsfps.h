@@ -44,7 +44,13 @@ typedef enum {
   NSFPS_EINVAL = 1,      /* invalid argument (shape, range, non-finite input) */
   NSFPS_EDEVICE = 2,     /* HIP runtime / device failure, or no device */
   NSFPS_ENOMEM = 3,      /* device allocation failed */
-  NSFPS_EUNSUPPORTED = 4 /* valid input outside what this build handles */
+  NSFPS_EUNSUPPORTED = 4 /* valid input outside what this build handles: more than
+                            1024 blocks on an axis (cells are packed 10 bits per
+                            axis), more than 2^31-1 points or samples, a cloud
+                            needing more than 4096 level-1 nodes when the tree
+                            engine is asked for (NSFPS_ENGINE=tree; the default
+                            engine has no such limit), or a layout beyond the
+                            allocation-free entry point's array */
 } nsfps_status;
 
 /* The nine primary SpaceRange fields (src/yuezu_fps.h:56-60).  Derived fields

@@ -66,6 +66,17 @@ __device__ __forceinline__ void pin_vgpr(T... v) {
   (pin_vgpr1(v), ...);
 }
 
+// p held in vector registers from here on: the compiler cannot load it again
+// from the kernel's arguments, a scalar load that after a vector store must
+// wait for the store to complete.
+template <typename T>
+__device__ __forceinline__ T *vgpr_ptr(T *p) {
+  const uint64_t u = (uint64_t)p;
+  uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 // The range values cell_axis reads, as arguments of pin_sgpr.
 #define NSFPS_CELL_RANGE(r)                                                                   \
   (r).mn[0], (r).mn[1], (r).mn[2], (r).hiclamp[0], (r).hiclamp[1], (r).hiclamp[2],           \
