@@ -847,7 +847,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                                         //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
   __shared__ uint4 s_rp[kHot];          // accepted hot copies at their slot: {x, y, z, row}
-  __shared__ uint4 s_rc[kHot];          //   {cube lo, cube hi (clipped), cell, half-widths}
+  __shared__ uint2 s_rc[kHot];          //   cube corners, pack11 (hi with guards)
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
   __shared__ uint32_t s_big[2];                         // samples with large cubes
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
@@ -1029,6 +1029,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     lo[s] = e1.x;
     row[s] = e1.y;
   }
+  // own cells in pack11 form, for the box tests of samples with large cubes
+  uint32_t c11[kOwnSlots];
+#pragma unroll
+  for (uint32_t s = 0; s < kOwnSlots; ++s) c11[s] = pack11(cc[s]);
   uint32_t it = *gptr(c.iter);
   const uint32_t m = c.m;
   NSFPS_GLOBAL int32_t *const out = gptr(c.out);
@@ -1399,7 +1403,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                                             __uint_as_float(rp.z), 0.f);
           pick_c[np + my_out] = make_uint2(lo_c, hi_c);
           s_rp[hj] = rp;
-          s_rc[hj] = make_uint4(lo_c, hi_c, qc, hh);
+          s_rc[hj] = make_uint2(pack11(lo_c), pack11(hi_c) | kGuards);
           if (ALIAS) {
             s_sbox[my_out] = make_uint2(pack11(lo_c), pack11(hi_c) | kGuards);
             s_spos[my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
@@ -1508,11 +1512,11 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         while (bigm) {
           const uint32_t kb = (uint32_t)__builtin_ctzll(bigm);
           bigm &= bigm - 1;
-          const uint4 a0 = s_rp[kb], rc = s_rc[kb];
-          const uint32_t qc = rc.z, hh = rc.w;
+          const uint4 a0 = s_rp[kb];
+          const uint2 bx = s_rc[kb];
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
-            if (in_cube_h(cc[s], qc, hh)) {
+            if (in_box11(c11[s] | kGuards, c11[s], bx.x, bx.y)) {
               const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
                                       __uint_as_float(a0.y), __uint_as_float(a0.z));
               d[s] = dd < d[s] ? dd : d[s];
