@@ -682,16 +682,6 @@ enum : uint32_t {
   kRpWalkWait = 16, kRpAlias = 17, kRpAliasN = 18, kRpLocal = 19, kRpExtraAt = 28
 };
 
-// Cell inside the cube of a sample at cell qc with packed half-widths h
-// (10 bits per axis): |cell - qc| <= h per axis, as (cell - qc + h) <= 2h in
-// unsigned arithmetic (bitwise, no branches).
-__device__ __forceinline__ bool in_cube_h(uint32_t cell, uint32_t qc, uint32_t h) {
-  const uint32_t h0 = h & 1023u, h1 = (h >> 10) & 1023u, h2 = h >> 20;
-  return ((cell & 1023u) - (qc & 1023u) + h0 <= 2 * h0) &
-         (((cell >> 10) & 1023u) - ((qc >> 10) & 1023u) + h1 <= 2 * h1) &
-         ((cell >> 20) - (qc >> 20) + h2 <= 2 * h2);
-}
-
 // Cells packed 11 bits per axis (x | y << 11 | z << 22): bits 10 and 21 stay
 // clear and act as guards, so lo <= c <= hi on all three axes takes two
 // subtractions.  cg = pack11(c) | kGuards, c11 = pack11(c), hig = pack11(hi) |
@@ -833,7 +823,7 @@ __device__ __forceinline__ void put_record(NSFPS_GLOBAL uint64_t *r, uint32_t ta
 template <bool PROF, bool FUSED, bool ALIAS>
 __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   static_assert(!(FUSED && ALIAS), "fused rounds need one cell per bucket");
-  __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, fine cell}
+  __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, pack11(cell)}
   __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
   __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
   __shared__ uint4 s_hq[2][kHot];       // hot copies at hot_slot(i), one buffer per phase parity:
@@ -984,7 +974,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       if (i < nlist) {
         const uint32_t pos = s_cell[G[s]] + K[s];
         s_pc[pos] = make_uint4(__float_as_uint(P[s].x), __float_as_uint(P[s].y),
-                               __float_as_uint(P[s].z), C[s]);
+                               __float_as_uint(P[s].z), pack11(C[s]));
         s_dd[pos] = __float_as_uint(P[s].w);
         s_rk[pos] = make_uint2(~R[s].x, R[s].y);
         if (ALIAS) {
@@ -1009,7 +999,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   // owned entries: sorted entry s * kRunThreads + tid; an empty slot has
   // distance 0 and key 0 and is never live
   float x[kOwnSlots], y[kOwnSlots], z[kOwnSlots], d[kOwnSlots];
-  uint32_t lo[kOwnSlots], row[kOwnSlots], cc[kOwnSlots];
+  // own cells in pack11 form (the box tests of samples with large cubes) and
+  // 10 bits per axis (a sample's cube centre)
+  uint32_t lo[kOwnSlots], row[kOwnSlots], cc[kOwnSlots], c11[kOwnSlots];
 #pragma unroll
   for (uint32_t s = 0; s < kOwnSlots; ++s) {
     const uint32_t i = s * kRunThreads + tid;
@@ -1024,15 +1016,12 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     x[s] = __uint_as_float(e0.x);
     y[s] = __uint_as_float(e0.y);
     z[s] = __uint_as_float(e0.z);
-    cc[s] = e0.w;
     d[s] = __uint_as_float(e2);
     lo[s] = e1.x;
     row[s] = e1.y;
+    c11[s] = e0.w;
+    cc[s] = (e0.w & 1023u) | (((e0.w >> 11) & 1023u) << 10) | ((e0.w >> 22) << 20);
   }
-  // own cells in pack11 form, for the box tests of samples with large cubes
-  uint32_t c11[kOwnSlots];
-#pragma unroll
-  for (uint32_t s = 0; s < kOwnSlots; ++s) c11[s] = pack11(cc[s]);
   uint32_t it = *gptr(c.iter);
   const uint32_t m = c.m;
   NSFPS_GLOBAL int32_t *const out = gptr(c.out);
@@ -1397,15 +1386,16 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         const uint32_t qc = my_qc, hh = my_hh;
         uint32_t lo_c, hi_c;
         cube_corners(qc, hh, b0, b1, b2, lo_c, hi_c);
+        const uint32_t lo11 = pack11(lo_c), hi11g = pack11(hi_c) | kGuards;
         if (q == 0) {
           out[it + my_out] = (int32_t)rp.w;
           pick_p[np + my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
                                             __uint_as_float(rp.z), 0.f);
           pick_c[np + my_out] = make_uint2(lo_c, hi_c);
           s_rp[hj] = rp;
-          s_rc[hj] = make_uint2(pack11(lo_c), pack11(hi_c) | kGuards);
+          s_rc[hj] = make_uint2(lo11, hi11g);
           if (ALIAS) {
-            s_sbox[my_out] = make_uint2(pack11(lo_c), pack11(hi_c) | kGuards);
+            s_sbox[my_out] = make_uint2(lo11, hi11g);
             s_spos[my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
                                          __uint_as_float(rp.z), 0.f);
           }
@@ -1446,8 +1436,8 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                   __float_as_uint(sqdist(__uint_as_float(pb.x), __uint_as_float(pb.y),
                                          __uint_as_float(pb.z), px, py, pz));
               // non-negative floats order like their bits
-              atomicMin(&s_dd[e], in_cube_h(pa.w, qc, hh) ? da : 0xffffffffu);
-              atomicMin(&s_dd[eb], in_cube_h(pb.w, qc, hh) ? db : 0xffffffffu);
+              atomicMin(&s_dd[e], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
+              atomicMin(&s_dd[eb], in_box11(pb.w | kGuards, pb.w, lo11, hi11g) ? db : 0xffffffffu);
             }
           }
         }
