@@ -851,7 +851,15 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   // bucket has several cells, the hot copies' positions, and the hot set's
   // samples by output order: cube corners (pack11; hi with guards) and x, y, z
   __shared__ uint32_t s_al[ALIAS ? kListCap * kMaxAlias : 1];
-  __shared__ uint32_t s_ao[ALIAS ? kListCap * kMaxAlias : 1];  // the bucket's other cells
+  // ALIAS: a second coarse cell index, of records {x, y, z, pack11(cell)} of
+  // the entries' other cells (the cells of their bucket besides their own)
+  // and the entry each belongs to, so that the walk reaches an entry through
+  // any cell of its bucket; entries whose records do not fit go to a pass
+  // over every sample of the hot set (s_alist)
+  __shared__ __align__(16) uint32_t s_xc[ALIAS ? kCells + 4 : 4];
+  __shared__ uint4 s_xp[ALIAS ? kListCap : 1];
+  __shared__ uint32_t s_xe[ALIAS ? kListCap : 1];
+  __shared__ uint32_t s_nx;
   __shared__ uint32_t s_alist[ALIAS ? kListCap : 1];
   __shared__ uint32_t s_nal;
   __shared__ uint32_t s_hpos[kHot];
@@ -918,7 +926,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     else ++sz;
   }
   const uint32_t ncx = ((b0 - 1) >> sx) + 1, ncy = ((b1 - 1) >> sy) + 1;
-  for (uint32_t j = tid; j < kCells + 4; j += kRunThreads) s_cell[j] = 0;
+  for (uint32_t j = tid; j < kCells + 4; j += kRunThreads) {
+    s_cell[j] = 0;
+    if (ALIAS) s_xc[j] = 0;
+  }
   if (tid < kSelBins) {
     s_sel[0][tid] = 0;
     s_sel[1][tid] = 0;
@@ -926,7 +937,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   if (tid < kHot) s_hq[0][tid] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
   if (tid == 0) {
     s_nhot = 0;
-    if (ALIAS) s_nal = 0;
+    if (ALIAS) {
+      s_nal = 0;
+      s_nx = 0;
+    }
     s_geo[0] = sx | (sy << 8) | (sz << 16);
     s_geo[1] = ncx;
     s_geo[2] = ncy;
@@ -936,14 +950,34 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
 
   // ---- list -> LDS in coarse-cell order (counting sort)
   {
+    const auto coarse = [&](uint32_t c10) {
+      return (((c10 >> 20) >> sz) * ncy + (((c10 >> 10) & 1023u) >> sy)) * ncx +
+             ((c10 & 1023u) >> sx);
+    };
     uint32_t G[kOwnSlots], K[kOwnSlots];
+    // ALIAS: per entry, its other cells' number and whether their records
+    // fit the second index, and each record's place among its coarse cell's
+    uint32_t NO[ALIAS ? kOwnSlots : 1] = {};
+    bool XI[ALIAS ? kOwnSlots : 1] = {};
+    uint32_t XK[ALIAS ? kOwnSlots : 1][kMaxAlias];
 #pragma unroll
     for (uint32_t s = 0; s < kOwnSlots; ++s) {
       const uint32_t i = s * kRunThreads + tid;
       if (i < nlist) {
-        G[s] = (((C[s] >> 20) >> sz) * ncy + (((C[s] >> 10) & 1023u) >> sy)) * ncx +
-               ((C[s] & 1023u) >> sx);
+        G[s] = coarse(C[s]);
         K[s] = atomicAdd(&s_cell[G[s]], 1u);
+        if (ALIAS) {
+          uint32_t no = 0;
+#pragma unroll
+          for (uint32_t a = 0; a < kMaxAlias; ++a) no += AL[s][a] != kNoCell && AL[s][a] != C[s];
+          NO[s] = no;
+          if (no && atomicAdd(&s_nx, no) + no <= kListCap) {
+            XI[s] = true;
+#pragma unroll
+            for (uint32_t a = 0; a < kMaxAlias; ++a)
+              if (AL[s][a] != kNoCell && AL[s][a] != C[s]) XK[s][a] = atomicAdd(&s_xc[coarse(AL[s][a])], 1u);
+          }
+        }
       }
     }
     __syncthreads();
@@ -966,6 +1000,24 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         reinterpret_cast<uint4 *>(s_cell)[kV * tid + j] = o;
       }
       if (tid == 0) s_cell[kCells] = tot;
+      if (ALIAS) {  // the second index's counts, the same way (its own wave sums)
+        uint32_t sum2 = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kV; ++j) {
+          v[j] = reinterpret_cast<const uint4 *>(s_xc)[kV * tid + j];
+          sum2 += v[j].x + v[j].y + v[j].z + v[j].w;
+        }
+        uint32_t tot2;
+        uint32_t pre2 = block_excl_scan<kRunWaves>(sum2, s_wn + kRunWaves, &tot2);
+#pragma unroll
+        for (uint32_t j = 0; j < kV; ++j) {
+          const uint4 o = make_uint4(pre2, pre2 + v[j].x, pre2 + v[j].x + v[j].y,
+                                     pre2 + v[j].x + v[j].y + v[j].z);
+          pre2 += v[j].x + v[j].y + v[j].z + v[j].w;
+          reinterpret_cast<uint4 *>(s_xc)[kV * tid + j] = o;
+        }
+        if (tid == 0) s_xc[kCells] = tot2;
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -978,19 +1030,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         s_dd[pos] = __float_as_uint(P[s].w);
         s_rk[pos] = make_uint2(~R[s].x, R[s].y);
         if (ALIAS) {
-          // the bucket's cells, and apart (for the pass after the walk, which
-          // finds the entry by its own cell) its other cells, both in pack11
-          // form; the valid cells come first
-          uint32_t no = 0;
+          // the bucket's cells (pack11), and the records of the other cells
+          // in the second index, or the entry in the pass's list
 #pragma unroll
           for (uint32_t a = 0; a < kMaxAlias; ++a) {
             s_al[pos * kMaxAlias + a] = pack11(AL[s][a]);
-            if (AL[s][a] != kNoCell && AL[s][a] != C[s]) s_ao[pos * kMaxAlias + no++] = pack11(AL[s][a]);
+            if (XI[s] && AL[s][a] != kNoCell && AL[s][a] != C[s]) {
+              const uint32_t dst = s_xc[coarse(AL[s][a])] + XK[s][a];
+              s_xp[dst] = make_uint4(__float_as_uint(P[s].x), __float_as_uint(P[s].y),
+                                     __float_as_uint(P[s].z), pack11(AL[s][a]));
+              s_xe[dst] = pos;
+            }
           }
-          if (no) {
-            for (uint32_t a = no; a < kMaxAlias; ++a) s_ao[pos * kMaxAlias + a] = pack11(kNoCell);
-            s_alist[atomicAdd(&s_nal, 1u)] = pos;
-          }
+          if (NO[s] && !XI[s]) s_alist[atomicAdd(&s_nal, 1u)] = pos;
         }
       }
     }
@@ -1417,11 +1469,16 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
             const uint32_t rz = (uint32_t)(((float)rr + 0.5f) * rny), ry = rr - rz * ny;
             const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
             const uint32_t e0 = s_cell[rw + x0], e1 = s_cell[rw + x1 + 1];
-            if (e1 - e0 > budget) {
+            uint32_t f0 = 0, f1 = 0;
+            if (ALIAS) {
+              f0 = s_xc[rw + x0];
+              f1 = s_xc[rw + x1 + 1];
+            }
+            if (e1 - e0 + (f1 - f0) > budget) {
               big = true;
               break;
             }
-            budget -= e1 - e0;
+            budget -= e1 - e0 + (f1 - f0);
             // two entries per step, their reads in flight together (an odd
             // last entry is taken twice: min is idempotent); one 16-byte read
             // each, and the min is unconditional (a no-op outside the cube),
@@ -1439,6 +1496,15 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
               atomicMin(&s_dd[e], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
               atomicMin(&s_dd[eb], in_box11(pb.w | kGuards, pb.w, lo11, hi11g) ? db : 0xffffffffu);
             }
+            // ALIAS: the other cells of entries in these rows' coarse cells
+            for (uint32_t f = f0; f < f1; ++f) {
+              const uint4 pa = s_xp[f];
+              const uint32_t ea = s_xe[f];
+              const uint32_t da =
+                  __float_as_uint(sqdist(__uint_as_float(pa.x), __uint_as_float(pa.y),
+                                         __uint_as_float(pa.z), px, py, pz));
+              atomicMin(&s_dd[ea], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
+            }
           }
         }
         if (big) atomicOr(&s_big[hj >> 5], 1u << (hj & 31u));
@@ -1450,11 +1516,11 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         __hip_atomic_store(&rs.pub, ((uint64_t)tag << 32) | (np + npk), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       if (ALIAS) {
-        // the entries whose bucket has other cells than their own (the walk
-        // reached them by their own cell), against every sample of the hot
-        // set: a thread per entry; lane k of every wave holds sample k's cube
-        // corners, which the loop reads lane by lane (the walk is done, so
-        // the thread owns the entry's distance)
+        // the entries whose other cells did not fit the second index (the
+        // walk reached them by their own cell alone), against every sample
+        // of the hot set: a thread per entry; lane k of every wave holds
+        // sample k's cube corners, which the loop reads lane by lane (the
+        // walk is done, so the thread owns the entry's distance)
         const uint32_t nal = uniform(s_nal), nk = uniform(npk);
         const uint2 bx = s_sbox[lane < nk ? lane : 0u];
         if (PROF) pf[kRpAliasN] += nal;
@@ -1469,24 +1535,18 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                                     __uint_as_float(pp.z), q.x, q.y, q.z);
             dm = min(dm, __float_as_uint(dd));  // non-negative floats order like their bits
           };
-          if (na == 2) {  // one other cell (grids near powers of two)
-            const uint32_t e0 = s_ao[pe * kMaxAlias];
-            const uint32_t e0g = e0 | kGuards;
-            for (uint32_t k = 0; k < nk; ++k)
-              if (in_box11(e0g, e0, rdlane(bx.x, k), rdlane(bx.y, k))) take(k);
-          } else {
-            uint32_t eo[kMaxAlias - 1];
+          // every cell of the bucket (its own again: min is idempotent)
+          uint32_t eo[kMaxAlias];
 #pragma unroll
-            for (uint32_t a = 0; a + 1 < kMaxAlias; ++a)
-              eo[a] = a + 1 < na ? s_ao[pe * kMaxAlias + a] : pack11(kNoCell);
-            for (uint32_t k = 0; k < nk; ++k) {
-              const uint32_t lo = rdlane(bx.x, k), hig = rdlane(bx.y, k);
-              uint32_t in = 0;
+          for (uint32_t a = 0; a < kMaxAlias; ++a)
+            eo[a] = a < na ? s_al[pe * kMaxAlias + a] : pack11(kNoCell);
+          for (uint32_t k = 0; k < nk; ++k) {
+            const uint32_t lo = rdlane(bx.x, k), hig = rdlane(bx.y, k);
+            uint32_t in = 0;
 #pragma unroll
-              for (uint32_t a = 0; a + 1 < kMaxAlias; ++a)
-                in |= in_box11(eo[a] | kGuards, eo[a], lo, hig);
-              if (in) take(k);
-            }
+            for (uint32_t a = 0; a < kMaxAlias; ++a)
+              in |= in_box11(eo[a] | kGuards, eo[a], lo, hig);
+            if (in) take(k);
           }
           s_dd[pe] = dm;
         }
@@ -1506,7 +1566,15 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
           const uint2 bx = s_rc[kb];
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
-            if (in_box11(c11[s] | kGuards, c11[s], bx.x, bx.y)) {
+            uint32_t in = in_box11(c11[s] | kGuards, c11[s], bx.x, bx.y);
+            if (ALIAS) {  // every cell of the bucket (the own cell among them)
+              const uint32_t i = s * kRunThreads + tid;
+              for (uint32_t a = 0; a < na; ++a) {
+                const uint32_t e = s_al[i * kMaxAlias + a];
+                in |= in_box11(e | kGuards, e, bx.x, bx.y);
+              }
+            }
+            if (in) {
               const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
                                       __uint_as_float(a0.y), __uint_as_float(a0.z));
               d[s] = dd < d[s] ? dd : d[s];
