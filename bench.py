@@ -400,6 +400,13 @@ def run_phases(lib, hip, w):
     v = dict(zip(RUN_PHASES, words[:21]))
     ctr = dict(zip(PASS_COUNTERS, words[24:28]))
     ctr.update(zip(["up_t_picks", "up_t_leaves", "up_t_flush", "up_groups"], words[32:36]))
+    ctr.update(zip(["up_t_load", "up_t_zero", "up_t_hits", "up_t_points"], words[40:44]))
+    ctr.update(zip(["ga_t_select", "ga_t_records", "ga_t_points_claim", "ga_t_writes", "ga_groups"],
+                   words[44:49]))
+    ctr.update(zip(["up_w_points_max", "up_w_points_sum", "up_w_loop_max", "up_w_loop_sum"],
+                   words[49:53]))
+    ctr.update(zip(["update_touched_leaves", "update_touched_points"], words[53:55]))
+    ctr.update(zip(["up_w_hits_max", "up_w_hits_sum"], words[55:57]))
     v["walk_wait"], v["alias"], v["alias_entries"] = words[28], words[29], words[30]
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
@@ -448,6 +455,29 @@ def pass_counts(wname, ctr, rounds):
             "state_node_picks": round(ctr["up_t_picks"] * 0.01 / ng, 2),
             "leaves": round(ctr["up_t_leaves"] * 0.01 / ng, 2),
             "node_key_flush": round(ctr["up_t_flush"] * 0.01 / ng, 2),
+            "workgroups_per_round": round(ng / rounds, 1),
+            "touched_leaves_per_round": round(ctr.get("update_touched_leaves", 0) / rounds, 1),
+            "touched_points_per_round": round(ctr.get("update_touched_points", 0) / rounds, 1),
+            # parts of the first two: the first reads, clearing the histogram,
+            # finding the touched leaves, their points' reads
+            "first_reads": round(ctr.get("up_t_load", 0) * 0.01 / ng, 2),
+            "hist_clear": round(ctr.get("up_t_zero", 0) * 0.01 / ng, 2),
+            "touched_leaves": round(ctr.get("up_t_hits", 0) * 0.01 / ng, 2),
+            "point_reads": round(ctr.get("up_t_points", 0) * 0.01 / ng, 2),
+            # over the 16 waves, from the picks' barrier: points in, loop done
+            "waves_touched_found_latest": round(ctr.get("up_w_hits_max", 0) * 0.01 / ng, 2),
+            "waves_touched_found_mean": round(ctr.get("up_w_hits_sum", 0) * 0.01 / ng / 16, 2),
+            "waves_points_in_latest": round(ctr.get("up_w_points_max", 0) * 0.01 / ng, 2),
+            "waves_points_in_mean": round(ctr.get("up_w_points_sum", 0) * 0.01 / ng / 16, 2),
+            "waves_loop_done_latest": round(ctr.get("up_w_loop_max", 0) * 0.01 / ng, 2),
+            "waves_loop_done_mean": round(ctr.get("up_w_loop_sum", 0) * 0.01 / ng / 16, 2)}
+    if ctr.get("ga_groups"):
+        ng = ctr["ga_groups"]
+        out["gather_pass_us_per_workgroup"] = {  # the first node chunk of each workgroup
+            "selection": round(ctr["ga_t_select"] * 0.01 / ng, 2),
+            "leaf_records": round(ctr["ga_t_records"] * 0.01 / ng, 2),
+            "points_and_claim": round(ctr["ga_t_points_claim"] * 0.01 / ng, 2),
+            "writes": round(ctr["ga_t_writes"] * 0.01 / ng, 2),
             "workgroups_per_round": round(ng / rounds, 1)}
     if census is not None:
         out["census_alg_bytes"] = census["total"]

@@ -183,8 +183,8 @@ class Lib:
         return s.as_dict()
 
     def loop_profile(self):
-        w = (ctypes.c_uint64 * 40)()
-        self._check(self.lib.nsfps_get_loop_profile(w, ctypes.c_uint32(40)))
+        w = (ctypes.c_uint64 * 64)()
+        self._check(self.lib.nsfps_get_loop_profile(w, ctypes.c_uint32(64)))
         return list(w)
 
 

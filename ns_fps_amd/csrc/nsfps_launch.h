@@ -79,7 +79,7 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
 hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t lds_bytes,
                             bool profile, uint32_t threads, hipStream_t st);
-constexpr uint32_t kProfWords = 40;
+constexpr uint32_t kProfWords = 64;
 
 // speculative-run engine
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);

@@ -49,16 +49,70 @@ enum : uint32_t { kCtUpLeaves = 24, kCtUpPoints, kCtGaLeaves, kCtGaPoints };
 // workgroups that update a node): run state, node and picks; the leaves; the
 // node key and the histogram's flush; and those workgroups.
 enum : uint32_t { kUpTPicks = 32, kUpTLeaves, kUpTFlush, kUpGroups };
+// Finer update-pass clocks: the first reads, clearing the histogram, finding
+// the touched leaves, and their points' reads (parts of the two above); the
+// gather pass's: the selection's replay, the leaf records, the held points
+// and the list range's claim, the writes; and its workgroups.
+enum : uint32_t {
+  kUpTLoad = 40, kUpTZero, kUpTHits, kUpTPts,
+  kGaTSel = 44, kGaTLeaf, kGaTClaim, kGaTWrite, kGaGroups,
+  // per update workgroup, over its waves: the latest and the summed times
+  // from the picks' barrier to the points' arrival and to the leaf loop's end
+  kUpWPtsMax = 49, kUpWPtsSum, kUpWLoopMax, kUpWLoopSum,
+  // leaves the update pass reads because a pick touches them, and their points
+  kCtUpHitLeaves = 53, kCtUpHitPoints,
+  // per update workgroup, over its waves: the latest and the summed times of
+  // finding the touched leaves
+  kUpWHitsMax = 55, kUpWHitsSum
+};
 
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
   return x | (y << 10) | (z << 20);
 }
 
+// Squared distance from q to the nearest point of the box lo..hi, in the
+// operation order of sqdist.  Rounding is monotonic, so it never exceeds
+// sqdist of q and a point in the box: when it is >= every distance of the
+// box's points, q lowers none of them (a point is lowered by a strictly
+// smaller distance).  NaN when q has a NaN coordinate.
+__device__ __forceinline__ float box_bound(float qx, float qy, float qz, float lx, float ly,
+                                           float lz, float hx, float hy, float hz) {
+  const float qv[3] = {qx, qy, qz}, lv[3] = {lx, ly, lz}, hv[3] = {hx, hy, hz};
+  float g[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const float below = lv[a] - qv[a], above = qv[a] - hv[a];
+    const float gg = below > above ? below : above;
+    g[a] = gg > 0.f ? gg : 0.f;
+  }
+  return (g[0] * g[0] + g[1] * g[1]) + g[2] * g[2];
+}
+
 // Cell inside a cube given as packed lo / hi corners.
 __device__ __forceinline__ bool cell_in(uint32_t cell, uint2 cube) {
   const uint32_t x = cell & 1023u, y = (cell >> 10) & 1023u, z = cell >> 20;
-  return x >= (cube.x & 1023u) && x <= (cube.y & 1023u) && y >= ((cube.x >> 10) & 1023u) &&
-         y <= ((cube.y >> 10) & 1023u) && z >= (cube.x >> 20) && z <= (cube.y >> 20);
+  // & rather than &&: straight-line compares, no branch per axis
+  return (x >= (cube.x & 1023u)) & (x <= (cube.y & 1023u)) & (y >= ((cube.x >> 10) & 1023u)) &
+         (y <= ((cube.y >> 10) & 1023u)) & (z >= (cube.x >> 20)) & (z <= (cube.y >> 20));
+}
+
+// Cells packed 11 bits per axis (x | y << 11 | z << 22): bits 10 and 21 stay
+// clear and act as guards, so lo <= c <= hi on all three axes takes two
+// subtractions.  cg = pack11(c) | kGuards, c11 = pack11(c), hig = pack11(hi) |
+// kGuards.  Per axis, cg - lo keeps its guard bit (or, for z, does not borrow)
+// exactly when c >= lo, and hig - c11 likewise when c <= hi.
+constexpr uint32_t kGuards = (1u << 10) | (1u << 21);
+
+__device__ __forceinline__ uint32_t pack11(uint32_t c10) {
+  return (c10 & 1023u) | (((c10 >> 10) & 1023u) << 11) | ((c10 >> 20) << 22);
+}
+
+__device__ __forceinline__ uint32_t in_box11(uint32_t cg, uint32_t c11, uint32_t lo,
+                                             uint32_t hig) {
+  uint32_t t1, t2;
+  const bool b1 = __builtin_usub_overflow(cg, lo, &t1);
+  const bool b2 = __builtin_usub_overflow(hig, c11, &t2);
+  return (uint32_t)(((t1 & t2 & kGuards) == kGuards) & !b1 & !b2);
 }
 
 // Cube overlapping the cell range [lo, hi] (packed corners).
@@ -197,10 +251,15 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 
 // Applies the picks of the last run to the points of level-1 node blockIdx.x,
 // rewrites the keys of the touched leaves and of the node, and counts the keys
-// inside the histogram window.  Leaves no pick touches whose key lies below
-// the window keep their key and are not read.  A leaf keeps its key too when
-// no pick lowers the point that holds it (keys only decrease), so its maximum
-// is searched only otherwise.  Reads that do not depend on each other are
+// inside the histogram window.  A pick takes part in a node only when its
+// cube overlaps the node's cells and it may lower one of the node's points:
+// its least squared distance to the node's box (box_bound) is below the
+// largest distance of those points, which the node's key holds (the
+// reference's cube rule, src/yuezu_fps.cpp:560-597, also visits points no
+// pick lowers; skipping them changes no distance).  Leaves no pick touches
+// whose key lies below the window keep their key and are not read.  A leaf
+// keeps its key too when no pick lowers the point that holds it (keys only
+// decrease), so its maximum is searched only otherwise.  Reads that do not depend on each other are
 // issued together: the wave's leaf records with the run state and the node's
 // record, a pick's cube with its position, and the points of every leaf of
 // the wave that needs reading.  PROF: counts the leaves and points it reads.
@@ -213,10 +272,11 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ float4 s_pp[kListCap];
-  __shared__ uint2 s_pc[kListCap];
+  __shared__ uint2 s_pc[kListCap];  // the picks' cube corners: pack11(lo), pack11(hi) | kGuards
   __shared__ uint64_t s_lk[kFan];
   __shared__ uint32_t s_np;
-  __shared__ uint32_t s_ct[2];  // PROF: leaves and points read by the workgroup
+  __shared__ uint32_t s_ct[4];  // PROF: leaves and points read by the workgroup, and of them touched
+  __shared__ uint32_t s_wt[PROF ? 3 * kPassWaves : 1];  // PROF: per-wave clocks
   const CloudDev &c = clouds[blockIdx.y];
   const uint32_t g = blockIdx.x;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -241,6 +301,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t gn = g < c.nl1 ? g : 0u;  // read unconditionally, used only if g < nl1
   const uint64_t nkey = gptr(c.l1_key)[gn];
   uint32_t clo, chi;
+  uint64_t uta = 0, utb = 0, utc = 0, utd = 0;
+  // the node's box of points (x > its hi x: no points)
+  const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
   // the cells of this wave's leaves' buckets: lane i < kLeavesPerWave * na
   // holds word i of the wave's stretch of leaf_al
   const uint32_t na = ALIAS ? c.r.na : 1u;
@@ -249,33 +312,40 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const uint2 cb = gptr(c.l1_cbox)[gn];
     if (lane < kLeavesPerWave * na && leaf0 + lane / na < c.nleaves)
       mal = gptr(c.leaf_al)[(size_t)leaf0 * na + lane];
-    pin_sgpr(done, npicks, kref, S, hsel, nkey, cb.x, cb.y);
+    pin_sgpr(done, npicks, kref, S, hsel, nkey, cb.x, cb.y, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y,
+             nhi.z);
     if (g >= c.nl1 || done || cb.x == kNone) return;  // finished, or no points
+    if (PROF) uta = __builtin_amdgcn_s_memrealtime();
     clo = cb.x;
     chi = cb.y;
   } else {
-    const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
     // the run state and the node's record are read together, ahead of the exit
     pin_sgpr(done, npicks, kref, S, hsel, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
     if (g >= c.nl1 || done || nlo.x > nhi.x) return;  // finished, or no points
+    if (PROF) uta = __builtin_amdgcn_s_memrealtime();
     clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y), cell_axis(c.r, 2, nlo.z));
     chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y), cell_axis(c.r, 2, nhi.z));
   }
   const uint64_t wlo = window_lo(kref, S);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   if (tid == 0) s_np = 0;
-  if (PROF && tid < 2) s_ct[tid] = 0;
+  if (PROF && tid < 4) s_ct[tid] = 0;
   __syncthreads();
+  if (PROF) utb = __builtin_amdgcn_s_memrealtime();
   for (uint32_t i = tid; i < npicks; i += kPassThreads) {
     const uint2 cb = gptr(c.pick_c)[i];
     const float4 pp = gptr(c.pick_p)[i];
     const float px = pp.x, py = pp.y, pz = pp.z;
     const uint32_t c0 = cb.x, c1 = cb.y;
     pin_vgpr(c0, c1, px, py, pz);  // both reads in flight together
-    if (cube_overlaps(make_uint2(c0, c1), clo, chi)) {
+    // the cube overlaps the node's cells, and the pick may lower one of its
+    // points (the node key holds their largest distance)
+    if (cube_overlaps(make_uint2(c0, c1), clo, chi) &&
+        !(box_bound(px, py, pz, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z) >=
+          __uint_as_float((uint32_t)(nkey >> 32)))) {
       const uint32_t k = atomicAdd(&s_np, 1u);
       s_pp[k] = make_float4(px, py, pz, 0.f);
-      s_pc[k] = make_uint2(c0, c1);
+      s_pc[k] = make_uint2(pack11(c0), pack11(c1) | kGuards);  // the box test's form
     }
   }
   __syncthreads();
@@ -284,41 +354,64 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   if (nsel == 0 && nkey < wlo) return;  // nothing changes, nothing to count
   // which leaves a pick touches (hm: the first 64 picks whose cube holds the
   // leaf's cell), and which must be read
-  uint32_t cell[kLeavesPerWave], st[kLeavesPerWave], cnt[kLeavesPerWave];
+  uint32_t c11[kLeavesPerWave], st[kLeavesPerWave], cnt[kLeavesPerWave];
   uint64_t okey[kLeavesPerWave], hm[kLeavesPerWave];
   bool hit[kLeavesPerWave], need[kLeavesPerWave];
-  // pick i's cube holds (a cell of the bucket of) leaf k
-  const auto touches = [&](uint32_t k, uint32_t i) -> bool {
-    const uint2 cube = s_pc[i];
-    if (!ALIAS) return cell_in(cell[k], cube);
-    if (na == 2) return cell_in(rdlane(mal, 2 * k), cube) || cell_in(rdlane(mal, 2 * k + 1), cube);
-    bool in = false;
-    for (uint32_t a = 0; a < na; ++a) in |= cell_in(rdlane(mal, k * na + a), cube);
-    return in;
+  // pick i's cube (its s_pc record) holds (a cell of the bucket of) leaf k.
+  // Testing the leaf's box against the pick as the node's is tested costs
+  // more here than the reads it saves on points that fill their cells.
+  const auto touches_pick = [&](uint32_t k, uint2 cube) -> bool {
+    uint32_t in;
+    if (!ALIAS) {
+      in = in_box11(c11[k] | kGuards, c11[k], cube.x, cube.y);
+    } else if (na == 2) {
+      const uint32_t a0 = pack11(rdlane(mal, 2 * k)), a1 = pack11(rdlane(mal, 2 * k + 1));
+      in = in_box11(a0 | kGuards, a0, cube.x, cube.y) | in_box11(a1 | kGuards, a1, cube.x, cube.y);
+    } else {
+      in = 0;
+      for (uint32_t a = 0; a < na; ++a) {
+        const uint32_t a0 = pack11(rdlane(mal, k * na + a));
+        in |= in_box11(a0 | kGuards, a0, cube.x, cube.y);
+      }
+    }
+    return in != 0;
   };
+  const auto touches = [&](uint32_t k, uint32_t i) -> bool { return touches_pick(k, s_pc[i]); };
+  // the first 64 picks' cubes, lane i holding pick i's, read once for the
+  // four leaves (past nsel: stale LDS, masked out)
+  const uint2 pc0 = s_pc[lane];
+  const bool in0 = lane < nsel;
 #pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-    cell[k] = rdlane(mcell, k);
+    c11[k] = pack11(rdlane(mcell, k));
     st[k] = rdlane(mst, k);
     cnt[k] = rdlane(mcnt, k);
     okey[k] = ((uint64_t)rdlane((uint32_t)(mkey >> 32), k) << 32) | rdlane((uint32_t)mkey, k);
-    hm[k] = __ballot(lane < nsel && touches(k, lane));
+    hm[k] = __ballot(in0 & touches_pick(k, pc0));
     bool h = hm[k] != 0;
     for (uint32_t cb = 64; cb < nsel && !h; cb += 64)
-      h = __ballot(cb + lane < nsel && touches(k, cb + lane)) != 0;
+      h = __ballot((cb + lane < nsel) & touches(k, cb + lane)) != 0;
     hit[k] = h;
     need[k] = leaf0 + k < c.nleaves && (h || okey[k] >= wlo);
   }
+  if (PROF) {
+    utc = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) s_wt[2 * kPassWaves + wave] = (uint32_t)(utc - ut1);
+  }
   if (PROF && lane == 0) {
-    uint32_t nl = 0, npt = 0;
+    uint32_t nl = 0, npt = 0, nh = 0, nhp = 0;
 #pragma unroll
     for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
       nl += need[k] ? 1u : 0u;
       npt += need[k] ? cnt[k] : 0u;
+      nh += need[k] && hit[k] ? 1u : 0u;
+      nhp += need[k] && hit[k] ? cnt[k] : 0u;
     }
     if (nl) {
       atomicAdd(&s_ct[0], nl);
       atomicAdd(&s_ct[1], npt);
+      atomicAdd(&s_ct[2], nh);
+      atomicAdd(&s_ct[3], nhp);
     }
   }
   float4 p[kLeavesPerWave];
@@ -332,6 +425,12 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const uint32_t idx = need[k] && lane < cnt[k] ? st[k] + lane : 0u;
     p[k] = gptr(c.P4)[idx];
     rk[k] = gptr(c.R)[idx];
+  }
+  if (PROF) {  // wait for the points (profiled build only)
+#pragma unroll
+    for (uint32_t k = 0; k < kLeavesPerWave; ++k) pin_vgpr(p[k].x, rk[k]);
+    utd = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) s_wt[wave] = (uint32_t)(utd - ut1);
   }
   // each leaf's stores are issued as soon as it is worked out, so that they
   // overlap the next leaves' work (deferring them all to the end measured
@@ -349,7 +448,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
         float d = p[k].w;
         if (hit[k]) {
           for (uint32_t cb = 0; cb < nsel; cb += 64) {
-            uint64_t m = cb == 0 ? hm[k] : __ballot(cb + lane < nsel && touches(k, cb + lane));
+            uint64_t m = cb == 0 ? hm[k] : __ballot((cb + lane < nsel) & touches(k, cb + lane));
             while (m) {
               const uint32_t j = (uint32_t)__ffsll((long long)m) - 1;
               m &= m - 1;
@@ -377,6 +476,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     }
     if (lane == 0) s_lk[li] = key;
   }
+  if (PROF && lane == 0) s_wt[kPassWaves + wave] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - ut1);
   __syncthreads();
   const uint64_t ut2 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
   if (wave == 0) {
@@ -397,8 +497,29 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     atomicAdd(pw + kUpTLeaves, (unsigned long long)(ut2 - ut1));
     atomicAdd(pw + kUpTFlush, (unsigned long long)(ut3 - ut2));
     atomicAdd(pw + kUpGroups, 1ull);
+    atomicAdd(pw + kUpTLoad, (unsigned long long)(uta - ut0));
+    atomicAdd(pw + kUpTZero, (unsigned long long)(utb - uta));
+    atomicAdd(pw + kUpTHits, (unsigned long long)(utc - ut1));
+    atomicAdd(pw + kUpTPts, (unsigned long long)(utd - utc));
+    uint32_t pmax = 0, psum = 0, lmax = 0, lsum = 0, hmax = 0, hsum = 0;
+    for (uint32_t w = 0; w < kPassWaves; ++w) {
+      hmax = max(hmax, s_wt[2 * kPassWaves + w]);
+      hsum += s_wt[2 * kPassWaves + w];
+      pmax = max(pmax, s_wt[w]);
+      psum += s_wt[w];
+      lmax = max(lmax, s_wt[kPassWaves + w]);
+      lsum += s_wt[kPassWaves + w];
+    }
+    atomicAdd(pw + kUpWPtsMax, (unsigned long long)pmax);
+    atomicAdd(pw + kUpWPtsSum, (unsigned long long)psum);
+    atomicAdd(pw + kUpWLoopMax, (unsigned long long)lmax);
+    atomicAdd(pw + kUpWLoopSum, (unsigned long long)lsum);
+    atomicAdd(pw + kUpWHitsMax, (unsigned long long)hmax);
+    atomicAdd(pw + kUpWHitsSum, (unsigned long long)hsum);
     atomicAdd(pw + kCtUpLeaves, (unsigned long long)s_ct[0]);
     atomicAdd(pw + kCtUpPoints, (unsigned long long)s_ct[1]);
+    atomicAdd(pw + kCtUpHitLeaves, (unsigned long long)s_ct[2]);
+    atomicAdd(pw + kCtUpHitPoints, (unsigned long long)s_ct[3]);
   }
 }
 
@@ -462,9 +583,11 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   __shared__ uint32_t s_sc[kPassWaves + 2];
   __shared__ uint64_t s_wk[kPassWaves];
   const CloudDev &c = clouds[blockIdx.y];
+  const uint64_t gt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
   if (blockIdx.x >= c.nl1 || *gptr(c.done) || gptr(c.rs)->hold) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
+  uint64_t gt1 = 0, gt2 = 0, gt3 = 0;
   bool forced = false;
   const Sel s = sel_replay(c, passes + 1, passes, s_sc, &forced);
   uint64_t bkey = s.bkey;
@@ -481,6 +604,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     for (uint32_t w = 0; w < kPassWaves; ++w) best = s_wk[w] > best ? s_wk[w] : best;
     bkey = best;
   }
+  if (PROF) gt1 = __builtin_amdgcn_s_memrealtime();
   if (blockIdx.x == 0 && tid == 0) {
     rs.bkey = bkey;
     // the first rounds start from windows over the whole key range and are
@@ -512,6 +636,10 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       lst = sc.x;
       lcnt = sc.y;
       lcell = gptr(c.leaf_cell)[lf];
+    }
+    if (PROF) {
+      pin_vgpr(lst, lcnt, lcell, (uint32_t)hot);
+      if (!gt2) gt2 = __builtin_amdgcn_s_memrealtime();
     }
     if (tid == 0) s_cnt = 0;
     uint64_t rest = __ballot(hot);
@@ -573,6 +701,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     if (tid == 0) s_base = s_cnt ? atomicAdd(&rs.nlist, s_cnt) : 0u;
     __syncthreads();
     base = s_base + rdlane(base, 0);
+    if (PROF && !gt3) gt3 = __builtin_amdgcn_s_memrealtime();
     // the list's pointers in vector registers: a pointer loaded again from
     // the arguments after a store would first wait for the store
     NSFPS_GLOBAL float4 *const LP = vgpr_ptr(gptr(c.list_p));
@@ -617,6 +746,15 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       put(p, ro, rdlane(lcell, j), al, __ballot(take));
     }
     __syncthreads();  // s_base is read before the next chunk's claim
+  }
+  if (PROF && tid == 0 && gt3) {  // the first chunk's clocks; the writes: every chunk's rest
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    unsigned long long *pw = (unsigned long long *)gptr(c.prof);
+    atomicAdd(pw + kGaTSel, (unsigned long long)(gt1 - gt0));
+    atomicAdd(pw + kGaTLeaf, (unsigned long long)(gt2 - gt1));
+    atomicAdd(pw + kGaTClaim, (unsigned long long)(gt3 - gt2));
+    atomicAdd(pw + kGaTWrite, (unsigned long long)(t - gt3));
+    atomicAdd(pw + kGaGroups, 1ull);
   }
 }
 
@@ -681,25 +819,6 @@ enum : uint32_t {
   // and those entries summed over hot sets
   kRpWalkWait = 16, kRpAlias = 17, kRpAliasN = 18, kRpLocal = 19, kRpExtraAt = 28
 };
-
-// Cells packed 11 bits per axis (x | y << 11 | z << 22): bits 10 and 21 stay
-// clear and act as guards, so lo <= c <= hi on all three axes takes two
-// subtractions.  cg = pack11(c) | kGuards, c11 = pack11(c), hig = pack11(hi) |
-// kGuards.  Per axis, cg - lo keeps its guard bit (or, for z, does not borrow)
-// exactly when c >= lo, and hig - c11 likewise when c <= hi.
-constexpr uint32_t kGuards = (1u << 10) | (1u << 21);
-
-__device__ __forceinline__ uint32_t pack11(uint32_t c10) {
-  return (c10 & 1023u) | (((c10 >> 10) & 1023u) << 11) | ((c10 >> 20) << 22);
-}
-
-__device__ __forceinline__ uint32_t in_box11(uint32_t cg, uint32_t c11, uint32_t lo,
-                                             uint32_t hig) {
-  uint32_t t1, t2;
-  const bool b1 = __builtin_usub_overflow(cg, lo, &t1);
-  const bool b2 = __builtin_usub_overflow(hig, c11, &t2);
-  return (uint32_t)(((t1 & t2 & kGuards) == kGuards) & !b1 & !b2);
-}
 
 // Cube corners of a sample: cell qc, half-widths h, clipped to the grid.
 __device__ __forceinline__ void cube_corners(uint32_t qc, uint32_t h, uint32_t b0, uint32_t b1,
