@@ -175,9 +175,9 @@ struct Step {
 };
 
 // Block-wide, all kPassThreads threads; sc holds kPassWaves + 2 words of LDS.
-__device__ Step hist_step(const uint32_t *H, uint32_t cap, uint32_t *sc) {
+// h: this thread's four bins of the histogram.
+__device__ Step hist_step(uint4 h, uint32_t cap, uint32_t *sc) {
   const uint32_t tid = threadIdx.x;
-  const uint4 h = gptr(reinterpret_cast<const uint4 *>(H))[tid];
   uint32_t tot;
   const uint32_t pre = block_excl_scan<kPassWaves>(h.x + h.y + h.z + h.w, sc, &tot);
   const uint32_t bins[4] = {h.x, h.y, h.z, h.w};
@@ -198,14 +198,18 @@ __device__ Step hist_step(const uint32_t *H, uint32_t cap, uint32_t *sc) {
   __syncthreads();
   return st;
 }
+__device__ Step hist_step(const uint32_t *H, uint32_t cap, uint32_t *sc) {
+  return hist_step(gptr(reinterpret_cast<const uint4 *>(H))[threadIdx.x], cap, sc);
+}
 
 // Replays the selection from the update pass's histograms and the first
 // `avail - 1` refinement histograms; `passes` refinement passes run this
 // round, so the threshold is forced at step `passes` (forced is set when that
 // rule, not the histograms, ended the selection with a list under a quarter
-// full).
+// full).  h0: this thread's bins of the update pass's histogram, when the
+// caller read them already.
 __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, uint32_t *sc,
-                          bool *forced = nullptr) {
+                          bool *forced = nullptr, const uint4 *h0 = nullptr) {
   const NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   Sel s;
   s.kref = rs.kref0;
@@ -216,7 +220,7 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, ui
   s.state = 0;
   s.pass = 0;
   const uint32_t *H0 = c.hist + (size_t)rs.hsel * kHists * kHistBins;
-  Step st = hist_step(H0, s.cap, sc);
+  Step st = h0 ? hist_step(*h0, s.cap, sc) : hist_step(H0, s.cap, sc);
   for (uint32_t p = 0;; ++p) {
     if (st.bs == kNone) {  // the whole window fits
       s.total += st.tot;
@@ -584,12 +588,38 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   __shared__ uint64_t s_wk[kPassWaves];
   const CloudDev &c = clouds[blockIdx.y];
   const uint64_t gt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
-  if (blockIdx.x >= c.nl1 || *gptr(c.done) || gptr(c.rs)->hold) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // Reads that depend on nothing read before them go out together with the
+  // run state: both histogram sets' update-pass bins (the run state says
+  // which one the selection replays) and the first node chunk's leaf records.
+  const uint4 hA = gptr(reinterpret_cast<const uint4 *>(c.hist))[tid];
+  const uint4 hB = gptr(reinterpret_cast<const uint4 *>(c.hist + kHists * kHistBins))[tid];
+  const auto leaf_of = [&](uint32_t c0, uint32_t &gq) {
+    gq = c0 + (lane / kLeavesPerWave) * gridDim.x;
+    return gq * kFan + wave * kLeavesPerWave + lane % kLeavesPerWave;
+  };
+  uint64_t lkey = 0;
+  uint32_t lst = 0, lcnt = 0, lcell = 0;
+  const auto read_leaf = [&](uint32_t c0) {
+    uint32_t gq;
+    const uint32_t lf = leaf_of(c0, gq);
+    lkey = 0;
+    lst = lcnt = lcell = 0;
+    if (gq < c.nl1 && lf < c.nleaves) {
+      lkey = gptr(c.leaf_key)[lf];
+      const uint2 sc = gptr(c.leaf_sc)[lf];
+      lst = sc.x;
+      lcnt = sc.y;
+      lcell = gptr(c.leaf_cell)[lf];
+    }
+  };
+  read_leaf(blockIdx.x);
+  if (blockIdx.x >= c.nl1 || *gptr(c.done) || gptr(c.rs)->hold) return;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   uint64_t gt1 = 0, gt2 = 0, gt3 = 0;
   bool forced = false;
-  const Sel s = sel_replay(c, passes + 1, passes, s_sc, &forced);
+  const uint4 h0 = rs.hsel ? hB : hA;
+  const Sel s = sel_replay(c, passes + 1, passes, s_sc, &forced, &h0);
   uint64_t bkey = s.bkey;
   if (s.state == 2) {
     uint64_t best = 0;
@@ -626,17 +656,10 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   static_assert(kGatherNodes * kLeavesPerWave == 64, "one leaf record per lane");
   __shared__ uint32_t s_cnt, s_base;
   for (uint32_t c0 = blockIdx.x; c0 < c.nl1; c0 += kGatherNodes * gridDim.x) {
-    const uint32_t gq = c0 + (lane / kLeavesPerWave) * gridDim.x;
-    const uint32_t lf = gq * kFan + wave * kLeavesPerWave + lane % kLeavesPerWave;
-    bool hot = false;
-    uint32_t lst = 0, lcnt = 0, lcell = 0;
-    if (gq < c.nl1 && lf < c.nleaves) {
-      hot = gptr(c.leaf_key)[lf] >= bkey;
-      const uint2 sc = gptr(c.leaf_sc)[lf];
-      lst = sc.x;
-      lcnt = sc.y;
-      lcell = gptr(c.leaf_cell)[lf];
-    }
+    if (c0 != blockIdx.x) read_leaf(c0);
+    uint32_t gq;
+    const uint32_t lf = leaf_of(c0, gq);
+    const bool hot = lcnt != 0 && lkey >= bkey;  // an empty or absent leaf has key 0
     if (PROF) {
       pin_vgpr(lst, lcnt, lcell, (uint32_t)hot);
       if (!gt2) gt2 = __builtin_amdgcn_s_memrealtime();
