@@ -293,8 +293,8 @@ __device__ __forceinline__ void gather_at(uint32_t p, const uint32_t *__restrict
                                           uint32_t *__restrict__ phys0) {
   if (p >= n) return;
   // ranks and rows come from sorts that may hold other clouds: this cloud's
-  // start in them is base
-  uint32_t rkg = prank[p];
+  // start in them is base; no prank: the physical order is the logical one
+  uint32_t rkg = prank ? prank[p] : base + p;
   uint32_t rk = rkg - base;
   uint32_t o = lorig[rkg] - base;
   uint32_t slot = p;

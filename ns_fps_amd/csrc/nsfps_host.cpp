@@ -628,14 +628,16 @@ nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs) {
   return NSFPS_OK;
 }
 
-// Both stable sorts of `total` points: nclouds clouds of n_per points stored
+// The stable sorts of `total` points: nclouds clouds of n_per points stored
 // one after another (nclouds = 1: one cloud).  Sort 1 by (cloud, bucket) gives
-// the logical order (values: rows); sort 2 by (cloud, bucket, sub-cell) inside
-// it gives the physical order (values: logical positions).  Rows and positions
-// count from the first cloud's start.
+// the logical order (values: rows); with `physical`, sort 2 by (cloud, bucket,
+// sub-cell) inside it gives the physical order (values: logical positions),
+// which keeps the leaves of large buckets compact for box tests.  Without it
+// (no result depends on the physical order) the physical order is the
+// logical one and *prank is null.  Rows and positions count from the first cloud's start.
 nsfps_status sort_points(const uint32_t *bucket, const uint32_t *fine, uint32_t n_per,
-                         uint32_t nclouds, int cloud_bits, int bucket_bits, const Scratch &s,
-                         hipStream_t st, uint32_t **lorig, uint32_t **prank) {
+                         uint32_t nclouds, int cloud_bits, int bucket_bits, bool physical,
+                         const Scratch &s, hipStream_t st, uint32_t **lorig, uint32_t **prank) {
   const uint32_t total = n_per * nclouds;
   uint32_t *ko = nullptr;
   if (nclouds == 1)
@@ -644,6 +646,10 @@ nsfps_status sort_points(const uint32_t *bucket, const uint32_t *fine, uint32_t 
     HIP_TRY(launch_cloud_keys(bucket, total, n_per, bucket_bits, s.kA, st));
   HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, total, cloud_bits + bucket_bits, s.hist,
                             s.scan, true, &ko, lorig, st));
+  if (!physical) {
+    *prank = nullptr;
+    return NSFPS_OK;
+  }
   const int fb = std::min<int>((int)kFineBits, 32 - bucket_bits - cloud_bits);
   const int fshift = (int)kFineBits - fb;
   uint32_t *k2 = (ko == s.kA) ? s.kB : s.kA;
@@ -760,10 +766,15 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     nsfps_status rc = decide_layout(plans[i], &hs[4 * i]);
     if (rc) return rc;
   }
+  // the sub-cell sort for the tree engine, and where a bucket can fill a
+  // level-1 node (the update pass's node boxes then lie inside one cell)
+  bool physical = false;
+  for (size_t i = 0; i < nc; ++i)
+    physical = physical || plans[i].tree || hs[4 * i + 1] >= kFan * kLeaf;
   if (together) {
     uint32_t *lorig = nullptr, *prank = nullptr;
-    nsfps_status rc = sort_points(cb.bucket, cb.fine, plans[0].n, (uint32_t)nc, cbits, bbits, s,
-                                  st, &lorig, &prank);
+    nsfps_status rc = sort_points(cb.bucket, cb.fine, plans[0].n, (uint32_t)nc, cbits, bbits,
+                                  physical, s, st, &lorig, &prank);
     if (rc) return rc;
     if (many) {
       uint32_t slots_max = 0, leaves_max = 0, l1_max = 0;
@@ -773,7 +784,7 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
         b.c = p.dev;
         b.cap = (uint32_t)p.cap;
         b.base = (uint32_t)(i * plans[0].n);
-        b.prank = prank + b.base;
+        b.prank = prank ? prank + b.base : nullptr;
         b.lorig = lorig;
         if (p.dev.padded) slots_max = std::max(slots_max, p.dev.nslots);
         leaves_max = std::max(leaves_max, p.dev.nleaves);
@@ -787,14 +798,15 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     }
     for (size_t i = 0; i < nc; ++i) {
       const uint32_t base = (uint32_t)(i * plans[0].n);
-      rc = finish_cloud(plans[i], lorig, prank + base, base, st);
+      rc = finish_cloud(plans[i], lorig, prank ? prank + base : nullptr, base, st);
       if (rc) return rc;
     }
   } else {
     for (auto &p : plans) {
       uint32_t *lorig = nullptr, *prank = nullptr;
       nsfps_status rc = sort_points(p.d_bucket, p.d_fine, p.n, 1, 0,
-                                    std::max(1, key_bits_for(p.rng.dev.T)), s, st, &lorig, &prank);
+                                    std::max(1, key_bits_for(p.rng.dev.T)), physical, s, st,
+                                    &lorig, &prank);
       if (rc) return rc;
       rc = finish_cloud(p, lorig, prank, 0, st);
       if (rc) return rc;

@@ -61,7 +61,8 @@ struct BuildDev {
   uint32_t *counts, *lc;     // per bucket, scanned to first slot / first leaf
   uint32_t *small;           // [0] non-finite flag, [1] largest bucket, [2] slot of row 0,
                              // [3] dense leaves
-  const uint32_t *prank;     // the sorts: this cloud's part of the physical order
+  const uint32_t *prank;     // the sorts: this cloud's part of the physical order (null: the
+                             // logical order)
   const uint32_t *lorig;     //   and the logical order of all clouds sorted together
   uint32_t n, T, cap, base;  // cap: slots per bucket when padded; base: this cloud's
                              // first rank / row in the sorts
