@@ -407,6 +407,7 @@ def run_phases(lib, hip, w):
                    words[49:53]))
     ctr.update(zip(["update_touched_leaves", "update_touched_points"], words[53:55]))
     ctr.update(zip(["up_w_hits_max", "up_w_hits_sum"], words[55:57]))
+    ctr.update(zip(["window_keys", "listed", "window_keys_max"], words[57:60]))
     v["walk_wait"], v["alias"], v["alias_entries"] = words[28], words[29], words[30]
     rounds = max(1, v["rounds"])
     hot = max(1, v["hot_sets"])
@@ -471,6 +472,10 @@ def pass_counts(wname, ctr, rounds):
             "waves_points_in_mean": round(ctr.get("up_w_points_sum", 0) * 0.01 / ng / 16, 2),
             "waves_loop_done_latest": round(ctr.get("up_w_loop_max", 0) * 0.01 / ng, 2),
             "waves_loop_done_mean": round(ctr.get("up_w_loop_sum", 0) * 0.01 / ng / 16, 2)}
+    if ctr.get("window_keys"):
+        out["window_keys_per_round"] = round(ctr["window_keys"] / rounds, 1)
+        out["listed_per_round"] = round(ctr["listed"] / rounds, 1)
+        out["window_keys_max"] = int(ctr["window_keys_max"])
     if ctr.get("ga_groups"):
         ng = ctr["ga_groups"]
         out["gather_pass_us_per_workgroup"] = {  # the first node chunk of each workgroup

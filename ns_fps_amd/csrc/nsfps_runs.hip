@@ -63,7 +63,10 @@ enum : uint32_t {
   kCtUpHitLeaves = 53, kCtUpHitPoints,
   // per update workgroup, over its waves: the latest and the summed times of
   // finding the touched leaves
-  kUpWHitsMax = 55, kUpWHitsSum
+  kUpWHitsMax = 55, kUpWHitsSum,
+  // keys inside the update pass's histogram window (summed over rounds), and
+  // the list entries gathered
+  kGaWinKeys = 57, kGaListed, kGaWinMax
 };
 
 __device__ __forceinline__ uint32_t pack_cell(uint32_t x, uint32_t y, uint32_t z) {
@@ -166,6 +169,7 @@ struct Sel {
   uint32_t total;    // entries taken so far
   uint32_t state;    // 0: refinement pass `pass` needed, 1: resolved, 2: use the maximum key
   uint32_t pass;
+  uint32_t win;      // keys inside the update pass's histogram window
 };
 
 struct Step {
@@ -221,6 +225,7 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, ui
   s.pass = 0;
   const uint32_t *H0 = c.hist + (size_t)rs.hsel * kHists * kHistBins;
   Step st = h0 ? hist_step(*h0, s.cap, sc) : hist_step(H0, s.cap, sc);
+  s.win = st.tot;
   for (uint32_t p = 0;; ++p) {
     if (st.bs == kNone) {  // the whole window fits
       s.total += st.tot;
@@ -769,6 +774,12 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       put(p, ro, rdlane(lcell, j), al, __ballot(take));
     }
     __syncthreads();  // s_base is read before the next chunk's claim
+  }
+  if (PROF && tid == 0 && blockIdx.x == 0) {
+    unsigned long long *pw = (unsigned long long *)gptr(c.prof);
+    atomicAdd(pw + kGaWinKeys, (unsigned long long)s.win);
+    atomicAdd(pw + kGaListed, (unsigned long long)s.total);
+    atomicMax(pw + kGaWinMax, (unsigned long long)s.win);
   }
   if (PROF && tid == 0 && gt3) {  // the first chunk's clocks; the writes: every chunk's rest
     const uint64_t t = __builtin_amdgcn_s_memrealtime();
