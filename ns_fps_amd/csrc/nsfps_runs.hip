@@ -1777,8 +1777,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     }
   }
   // the set this round's selection read is cleared for the round after next
-  NSFPS_GLOBAL uint32_t *const hz = hist_set(c, hsel);
-  for (uint32_t j = tid; j < kHists * kHistBins; j += kRunThreads) hz[j] = 0;
+  // (16-byte stores: six a thread)
+  NSFPS_GLOBAL uint4 *const hz = reinterpret_cast<NSFPS_GLOBAL uint4 *>(hist_set(c, hsel));
+  for (uint32_t j = tid; j < kHists * kHistBins / 4; j += kRunThreads) hz[j] = make_uint4(0u, 0u, 0u, 0u);
   if (PROF && tid == 0) {
     NSFPS_RMARK(kRpTail);
     pf[kRpPicks] = np;
