@@ -40,7 +40,22 @@ __device__ __forceinline__ void cell_keys_at(uint32_t i, const float *__restrict
   uint32_t b = bucket_of(r, lut, c[0], c[1], c[2]);
   bucket[i] = b;
   fine[i] = f;
-  atomicAdd(&counts[b], 1u);
+  if (counts) atomicAdd(&counts[b], 1u);  // null: counted from the sorted buckets instead
+}
+
+// Bucket populations from the buckets sorted: each bucket's points are one
+// run; the run's first element adds -(its position) and its last element
+// adds its position + 1, so every bucket takes at most two atomics, never
+// contended (counts start at zero).
+__global__ void k_seg_counts(const uint32_t *__restrict__ keys, uint32_t n,
+                             uint32_t *__restrict__ counts) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t k = keys[i];
+  uint32_t delta = 0;
+  if (i == 0 || keys[i - 1] != k) delta -= i;
+  if (i + 1 == n || keys[i + 1] != k) delta += i + 1;
+  if (delta) atomicAdd(&counts[k], delta);
 }
 
 __global__ void k_cell_keys(const float *__restrict__ xyz, uint32_t n, RangeDev r,
@@ -528,6 +543,12 @@ hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t 
   if (words == 0) return hipSuccess;
   const uint64_t blocks = (words + 255) / 256;
   k_fill_u32<<<(uint32_t)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>((uint32_t *)p, value, words);
+  return hipGetLastError();
+}
+
+hipError_t launch_seg_counts(const uint32_t *keys, uint32_t n, uint32_t *counts, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  k_seg_counts<<<(n + 255) / 256, 256, 0, st>>>(keys, n, counts);
   return hipGetLastError();
 }
 

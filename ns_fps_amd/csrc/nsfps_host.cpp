@@ -581,7 +581,16 @@ bool sort_together(const std::vector<CloudPlan> &plans, int *cloud_bits, int *bu
 // then the stream is synchronised once and a few words per cloud decide each
 // layout; then both sorts run (once for all clouds when they can be sorted
 // together), and each cloud's slots, leaves and tree are built.
-nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &s, hipStream_t st) {
+nsfps_status sort_logical(const uint32_t *bucket, uint32_t n_per, uint32_t nclouds,
+                          int cloud_bits, int bucket_bits, const Scratch &s, hipStream_t st,
+                          uint32_t **keys, uint32_t **lorig);
+
+// sorted: the cloud is sorted by bucket here (its rows in *lorig, the sorted
+// buckets in *keys) and the bucket populations are counted from that order,
+// not by an atomic per point (contended where points crowd into few buckets).
+nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &s, hipStream_t st,
+                          bool sorted = false, uint32_t **keys = nullptr,
+                          uint32_t **lorig = nullptr) {
   const uint32_t T = p.rng.dev.T;
   if (lut_of) {
     p.d_lut = lut_of->d_lut;  // the same bit positions: the same tables
@@ -593,8 +602,14 @@ nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &
     HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
   }
   const float *xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
-  HIP_TRY(launch_cell_keys(xyz, p.n, p.rng.dev, p.d_lut, p.d_bucket, p.d_fine, p.d_counts,
-                           p.d_small, st));
+  HIP_TRY(launch_cell_keys(xyz, p.n, p.rng.dev, p.d_lut, p.d_bucket, p.d_fine,
+                           sorted ? nullptr : p.d_counts, p.d_small, st));
+  if (sorted) {
+    nsfps_status rc = sort_logical(p.d_bucket, p.n, 1, 0, std::max(1, key_bits_for(T)), s, st,
+                                   keys, lorig);
+    if (rc) return rc;
+    HIP_TRY(launch_seg_counts(*keys, p.n, p.d_counts, st));
+  }
   HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, p.d_small + 3, st));
   HIP_TRY(launch_scan(p.d_counts, T, s.scan, st));  // -> first dense position per bucket
   HIP_TRY(launch_scan(p.d_lc, T, s.scan, st));      // -> first leaf per bucket (dense)
@@ -635,32 +650,48 @@ nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs) {
 // which keeps the leaves of large buckets compact for box tests.  Without it
 // (no result depends on the physical order) the physical order is the
 // logical one and *prank is null.  Rows and positions count from the first cloud's start.
-nsfps_status sort_points(const uint32_t *bucket, const uint32_t *fine, uint32_t n_per,
-                         uint32_t nclouds, int cloud_bits, int bucket_bits, bool physical,
-                         const Scratch &s, hipStream_t st, uint32_t **lorig, uint32_t **prank) {
+nsfps_status sort_logical(const uint32_t *bucket, uint32_t n_per, uint32_t nclouds,
+                          int cloud_bits, int bucket_bits, const Scratch &s, hipStream_t st,
+                          uint32_t **keys, uint32_t **lorig) {
   const uint32_t total = n_per * nclouds;
-  uint32_t *ko = nullptr;
   if (nclouds == 1)
     HIP_TRY(hipMemcpyAsync(s.kA, bucket, (size_t)total * 4, hipMemcpyDeviceToDevice, st));
   else
     HIP_TRY(launch_cloud_keys(bucket, total, n_per, bucket_bits, s.kA, st));
   HIP_TRY(launch_radix_sort(s.kA, s.vA, s.kB, s.vB, total, cloud_bits + bucket_bits, s.hist,
-                            s.scan, true, &ko, lorig, st));
-  if (!physical) {
-    *prank = nullptr;
-    return NSFPS_OK;
-  }
+                            s.scan, true, keys, lorig, st));
+  return NSFPS_OK;
+}
+
+nsfps_status sort_physical(const uint32_t *bucket, const uint32_t *fine, uint32_t n_per,
+                           uint32_t nclouds, int cloud_bits, int bucket_bits, const Scratch &s,
+                           hipStream_t st, const uint32_t *keys, const uint32_t *lorig,
+                           uint32_t **prank) {
+  const uint32_t total = n_per * nclouds;
   const int fb = std::min<int>((int)kFineBits, 32 - bucket_bits - cloud_bits);
   const int fshift = (int)kFineBits - fb;
-  uint32_t *k2 = (ko == s.kA) ? s.kB : s.kA;
+  uint32_t *k2 = (keys == s.kA) ? s.kB : s.kA;
   uint32_t *k2tmp = (k2 == s.kA) ? s.kB : s.kA;
-  uint32_t *v2 = (*lorig == s.vA) ? s.vB : s.vA;
+  uint32_t *v2 = (lorig == s.vA) ? s.vB : s.vA;
   const int cloud_shift = std::min(bucket_bits + fb, 31);
-  HIP_TRY(launch_key2(*lorig, bucket, fine, total, n_per, cloud_shift, fshift, fb, k2, st));
+  HIP_TRY(launch_key2(lorig, bucket, fine, total, n_per, cloud_shift, fshift, fb, k2, st));
   uint32_t *kdummy = nullptr;
   HIP_TRY(launch_radix_sort(k2, v2, k2tmp, s.vC, total, cloud_bits + bucket_bits + fb, s.hist,
                             s.scan, true, &kdummy, prank, st));
   return NSFPS_OK;
+}
+
+nsfps_status sort_points(const uint32_t *bucket, const uint32_t *fine, uint32_t n_per,
+                         uint32_t nclouds, int cloud_bits, int bucket_bits, bool physical,
+                         const Scratch &s, hipStream_t st, uint32_t **lorig, uint32_t **prank) {
+  uint32_t *keys = nullptr;
+  nsfps_status rc = sort_logical(bucket, n_per, nclouds, cloud_bits, bucket_bits, s, st, &keys,
+                                 lorig);
+  if (rc) return rc;
+  *prank = nullptr;
+  if (!physical) return NSFPS_OK;
+  return sort_physical(bucket, fine, n_per, nclouds, cloud_bits, bucket_bits, s, st, keys,
+                       *lorig, prank);
 }
 
 // Slots, cell table, leaves and tree of one cloud from the sorts: its
@@ -722,6 +753,7 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   const bool together = sort_together(plans, &cbits, &bbits);
   const bool many = together && tmax <= kManyMaxBuckets;
   bd.assign(many ? nc : 0, BuildDev{});
+  uint32_t *keys1 = nullptr, *lorig1 = nullptr;  // one cloud: its sort by bucket
   for (size_t i = 0; i < nc; ++i) {
     const CloudPlan *lut_of = nullptr;
     if (i > 0 && plans[i].rng.lut[0] == plans[0].rng.lut[0] &&
@@ -752,7 +784,9 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
       b.T = p.rng.dev.T;
       continue;
     }
-    nsfps_status rc = build_phase1(plans[i], lut_of, s, st);
+    // one cloud: sorted by bucket before the layout is decided (the sort's
+    // scratch buffers then stay untouched until its finish)
+    nsfps_status rc = build_phase1(plans[i], lut_of, s, st, nc == 1, &keys1, &lorig1);
     if (rc) return rc;
   }
   if (many) {
@@ -804,9 +838,15 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   } else {
     for (auto &p : plans) {
       uint32_t *lorig = nullptr, *prank = nullptr;
-      nsfps_status rc = sort_points(p.d_bucket, p.d_fine, p.n, 1, 0,
-                                    std::max(1, key_bits_for(p.rng.dev.T)), physical, s, st,
-                                    &lorig, &prank);
+      const int bbits = std::max(1, key_bits_for(p.rng.dev.T));
+      nsfps_status rc = NSFPS_OK;
+      if (nc == 1) {  // sorted by bucket already
+        lorig = lorig1;
+        if (physical)
+          rc = sort_physical(p.d_bucket, p.d_fine, p.n, 1, 0, bbits, s, st, keys1, lorig, &prank);
+      } else {
+        rc = sort_points(p.d_bucket, p.d_fine, p.n, 1, 0, bbits, physical, s, st, &lorig, &prank);
+      }
       if (rc) return rc;
       rc = finish_cloud(p, lorig, prank, 0, st);
       if (rc) return rc;

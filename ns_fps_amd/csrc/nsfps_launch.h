@@ -14,9 +14,13 @@ namespace nsfps {
 hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t st);
 
 // build
+// counts null: no bucket populations (launch_seg_counts gives them from the
+// sorted buckets)
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
                             hipStream_t st);
+// bucket populations into zeroed counts from n sorted bucket keys
+hipError_t launch_seg_counts(const uint32_t *keys, uint32_t n, uint32_t *counts, hipStream_t st);
 // exclusive scan in place, data[len] = total; tmp holds scan_tmp_len(len) words
 uint32_t scan_tmp_len(uint32_t len);
 hipError_t launch_scan(uint32_t *data, uint32_t len, uint32_t *tmp, hipStream_t st);
