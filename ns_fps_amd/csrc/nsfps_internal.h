@@ -153,7 +153,8 @@ struct CloudDev {
   RunState *rs;
   uint32_t *hist;             // 2 sets of kHists x kHistBins (RunState::hsel picks one)
   float4 *pick_p;             // kListCap: x, y, z, D of each pick of a run
-  uint2 *pick_c;              // kListCap: cube lo / hi cells (10 bits per axis)
+  uint2 *pick_c;              // kListCap: cube lo / hi cells, 11 bits per axis with guard bits
+                              // (lo, hi | guards: the run kernel's box-test form)
   float4 *list_p;             // kListCap: x, y, z, min distance
   uint2 *list_r;              // kListCap: logical rank, input row
   uint32_t *list_c;           // kListCap: cell (10 bits per axis)

@@ -336,6 +336,8 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     chi = pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y), cell_axis(c.r, 2, nhi.z));
   }
   const uint64_t wlo = window_lo(kref, S);
+  // the node's cell range in the picks' box-test form
+  const uint32_t clo11 = pack11(clo), chi11g = pack11(chi) | kGuards;
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   if (tid == 0) s_np = 0;
   if (PROF && tid < 4) s_ct[tid] = 0;
@@ -347,14 +349,16 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const float px = pp.x, py = pp.y, pz = pp.z;
     const uint32_t c0 = cb.x, c1 = cb.y;
     pin_vgpr(c0, c1, px, py, pz);  // both reads in flight together
-    // the cube overlaps the node's cells, and the pick may lower one of its
-    // points (the node key holds their largest distance)
-    if (cube_overlaps(make_uint2(c0, c1), clo, chi) &&
+    // the cube overlaps the node's cells (cube lo <= node hi and node lo <=
+    // cube hi on every axis: the guard test of in_box11 crosswise), and the
+    // pick may lower one of its points (the node key holds their largest
+    // distance)
+    if (in_box11(c1, c0, clo11, chi11g) &&
         !(box_bound(px, py, pz, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z) >=
           __uint_as_float((uint32_t)(nkey >> 32)))) {
       const uint32_t k = atomicAdd(&s_np, 1u);
       s_pp[k] = make_float4(px, py, pz, 0.f);
-      s_pc[k] = make_uint2(pack11(c0), pack11(c1) | kGuards);  // the box test's form
+      s_pc[k] = make_uint2(c0, c1);
     }
   }
   __syncthreads();
@@ -1596,7 +1600,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
           out[it + my_out] = (int32_t)rp.w;
           pick_p[np + my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
                                             __uint_as_float(rp.z), 0.f);
-          pick_c[np + my_out] = make_uint2(lo_c, hi_c);
+          pick_c[np + my_out] = make_uint2(lo11, hi11g);
           s_rp[hj] = rp;
           s_rc[hj] = make_uint2(lo11, hi11g);
           if (ALIAS) {
@@ -2152,8 +2156,8 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
     rs.hold = 0;
     const float4 p0 = *gptr(c.root_pos);
     gptr(c.pick_p)[0] = make_float4(p0.x, p0.y, p0.z, INFINITY);
-    gptr(c.pick_c)[0] =
-        make_uint2(0u, pack_cell(c.r.blocks[0] - 1, c.r.blocks[1] - 1, c.r.blocks[2] - 1));
+    gptr(c.pick_c)[0] = make_uint2(
+        0u, pack11(pack_cell(c.r.blocks[0] - 1, c.r.blocks[1] - 1, c.r.blocks[2] - 1)) | kGuards);
     gptr(c.out)[0] = 0;
     *gptr(c.iter) = 1;
     *gptr(c.done) = c.m <= 1 ? 1u : 0u;
