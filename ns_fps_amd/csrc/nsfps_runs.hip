@@ -1525,7 +1525,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
         stop = 2;
         break;
       }
-      if (nge - P < kPhaseMin) {  // few copies left: they go back to the next selection
+      // few copies left: they go back to the next selection (always so at
+      // kPhaseMin = kHot, at most kHot copies being >= the hot threshold)
+      if (kPhaseMin >= kHot || nge - P < kPhaseMin) {
         stop = P >= nge ? 1u : 0u;
         break;
       }
