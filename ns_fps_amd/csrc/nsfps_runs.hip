@@ -836,9 +836,14 @@ constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
 // at 12, 8.26 at 32, 8.20 at 48, 8.09 at kHot; LiDAR scan 5.38 / 5.26 / 5.19 /
 // 5.14 ms).
 constexpr uint32_t kPhaseMin = kHot;
-constexpr uint32_t kWalkRows = 64;        // cubes over more coarse rows, or with more
-constexpr uint32_t kWalkLaneEntries = 16;  // list entries in one lane's rows, are
-                                          // applied by every thread
+// Cubes over more coarse rows, or with more list entries in one lane's rows,
+// are applied by every thread to its own entries instead of walked.  Rows
+// below 64 keep the walk's row arithmetic exact; 24 rows measured best (per
+// call: uniform cube 8.08 ms at 64 rows, 7.95 at 16-24, 9.40 at 8; LiDAR scan
+// 5.19 at 64, 5.10 at 24, 5.15 at 16).
+constexpr uint32_t kWalkRows = 24;
+constexpr uint32_t kWalkLaneEntries = 16;
+static_assert(kWalkRows <= 64, "the walk's row arithmetic");
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
 static_assert((kCopyLanes == 4 || kCopyLanes == 8 || kCopyLanes == 16) && kHot == 64,
               "the run kernel layout");
