@@ -1011,7 +1011,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
   __shared__ uint32_t s_nhot;
   __shared__ unsigned long long s_kmr;   // largest key of a hot copy left unaccepted
-  __shared__ uint32_t s_wn[kRunWaves * kOwnSlots];
+  __shared__ uint32_t s_wn[2 * kRunWaves];  // wave sums of the two cell-count scans
   __shared__ uint32_t s_wr[2][kRunWaves][2];
   __shared__ uint32_t s_geo[4];  // coarse cell shifts (x | y << 8 | z << 16), ncx, ncy
   // ALIAS: the cells of each entry's bucket (pack11, kNoCell-padded, at the
