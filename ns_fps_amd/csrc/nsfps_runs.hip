@@ -1729,11 +1729,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       NSFPS_RMARK(kRpApply);
       uint64_t bigm = ((uint64_t)uniform(s_big[1]) << 32) | uniform(s_big[0]);
       if (bigm) {
-        while (bigm) {
-          const uint32_t kb = (uint32_t)__builtin_ctzll(bigm);
-          bigm &= bigm - 1;
-          const uint4 a0 = s_rp[kb];
-          const uint2 bx = s_rc[kb];
+        // branch-free (the distance is always computed, the box test masks
+        // it), two samples a trip so that their LDS reads overlap; a lone
+        // last sample is applied twice (min is idempotent)
+        const auto take = [&](const uint4 a0, const uint2 bx) {
 #pragma unroll
           for (uint32_t s = 0; s < kOwnSlots; ++s) {
             uint32_t in = in_box11(c11[s] | kGuards, c11[s], bx.x, bx.y);
@@ -1744,12 +1743,22 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
                 in |= in_box11(e | kGuards, e, bx.x, bx.y);
               }
             }
-            if (in) {
-              const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
-                                      __uint_as_float(a0.y), __uint_as_float(a0.z));
-              d[s] = dd < d[s] ? dd : d[s];
-            }
+            const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
+                                    __uint_as_float(a0.y), __uint_as_float(a0.z));
+            // non-negative floats order like their bits; outside the cube the
+            // distance becomes all ones, which never wins
+            d[s] = __uint_as_float(min(__float_as_uint(d[s]), __float_as_uint(dd) | (in - 1u)));
           }
+        };
+        while (bigm) {
+          const uint32_t ka = (uint32_t)__builtin_ctzll(bigm);
+          bigm &= bigm - 1;
+          const uint32_t kc = bigm ? (uint32_t)__builtin_ctzll(bigm) : ka;
+          bigm &= bigm - 1;
+          const uint4 a0 = s_rp[ka], a1 = s_rp[kc];
+          const uint2 b0 = s_rc[ka], b1 = s_rc[kc];
+          take(a0, b0);
+          take(a1, b1);
         }
 #pragma unroll
         for (uint32_t s = 0; s < kOwnSlots; ++s)
