@@ -838,10 +838,11 @@ constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
 constexpr uint32_t kPhaseMin = kHot;
 // Cubes over more coarse rows, or with more list entries in one lane's rows,
 // are applied by every thread to its own entries instead of walked.  Rows
-// below 64 keep the walk's row arithmetic exact; 24 rows measured best (per
-// call: uniform cube 8.08 ms at 64 rows, 7.95 at 16-24, 9.40 at 8; LiDAR scan
-// 5.19 at 64, 5.10 at 24, 5.15 at 16).
-constexpr uint32_t kWalkRows = 24;
+// below 64 keep the walk's row arithmetic exact.  With a lane's rows walked
+// as one list, 16 rows (two a lane) measured best: per call, uniform cube
+// 7.73 ms at 16 rows and 7.88 at 24, LiDAR scan 4.49 and 4.50, clustered
+// 71.0 and 73.4 (row by row at 24 rows: 7.94, 4.75, 69.3).
+constexpr uint32_t kWalkRows = 16;
 constexpr uint32_t kWalkLaneEntries = 16;
 static_assert(kWalkRows <= 64, "the walk's row arithmetic");
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
@@ -1634,46 +1635,93 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
           const float rny = __builtin_amdgcn_rcpf((float)ny);
           const float px = __uint_as_float(rp.x), py = __uint_as_float(rp.y),
                       pz = __uint_as_float(rp.z);
-          uint32_t budget = kWalkLaneEntries;
-          for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
-            const uint32_t rz = (uint32_t)(((float)rr + 0.5f) * rny), ry = rr - rz * ny;
-            const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
-            const uint32_t e0 = s_cell[rw + x0], e1 = s_cell[rw + x1 + 1];
-            uint32_t f0 = 0, f1 = 0;
-            if (ALIAS) {
-              f0 = s_xc[rw + x0];
-              f1 = s_xc[rw + x1 + 1];
-            }
-            if (e1 - e0 + (f1 - f0) > budget) {
-              big = true;
-              break;
-            }
-            budget -= e1 - e0 + (f1 - f0);
-            // two entries per step, their reads in flight together (an odd
-            // last entry is taken twice: min is idempotent); one 16-byte read
-            // each, and the min is unconditional (a no-op outside the cube),
-            // so the cell is not read ahead of the coordinates
-            for (uint32_t e = e0; e < e1; e += 2) {
-              const uint32_t eb = e + 1 < e1 ? e + 1 : e;
-              const uint4 pa = s_pc[e], pb = s_pc[eb];
-              const uint32_t da =
-                  __float_as_uint(sqdist(__uint_as_float(pa.x), __uint_as_float(pa.y),
-                                         __uint_as_float(pa.z), px, py, pz));
-              const uint32_t db =
-                  __float_as_uint(sqdist(__uint_as_float(pb.x), __uint_as_float(pb.y),
-                                         __uint_as_float(pb.z), px, py, pz));
+          // four entries per step, their reads in flight together (a short
+          // last step repeats an entry: min is idempotent); one 16-byte read
+          // each, and the min is unconditional (a no-op outside the cube), so
+          // the cell is not read ahead of the coordinates
+          const auto walk4 = [&](const uint32_t(&ee)[4]) {
+            uint4 pe[4];
+#pragma unroll
+            for (uint32_t t = 0; t < 4; ++t) pe[t] = s_pc[ee[t]];
+#pragma unroll
+            for (uint32_t t = 0; t < 4; ++t) {
+              const uint32_t dt =
+                  __float_as_uint(sqdist(__uint_as_float(pe[t].x), __uint_as_float(pe[t].y),
+                                         __uint_as_float(pe[t].z), px, py, pz));
               // non-negative floats order like their bits
-              atomicMin(&s_dd[e], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
-              atomicMin(&s_dd[eb], in_box11(pb.w | kGuards, pb.w, lo11, hi11g) ? db : 0xffffffffu);
+              atomicMin(&s_dd[ee[t]],
+                        in_box11(pe[t].w | kGuards, pe[t].w, lo11, hi11g) ? dt : 0xffffffffu);
             }
-            // ALIAS: the other cells of entries in these rows' coarse cells
-            for (uint32_t f = f0; f < f1; ++f) {
-              const uint4 pa = s_xp[f];
-              const uint32_t ea = s_xe[f];
-              const uint32_t da =
-                  __float_as_uint(sqdist(__uint_as_float(pa.x), __uint_as_float(pa.y),
-                                         __uint_as_float(pa.z), px, py, pz));
-              atomicMin(&s_dd[ea], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
+          };
+          if (!ALIAS) {
+            // the lane's rows (rr = q, q + kCopyLanes, ...): their entry
+            // ranges read up front (one LDS wait; a lane with fewer rows reads
+            // row 0's again and counts it empty), then their entries walked
+            // as one list.  Per call, against row by row (whose last step in
+            // each row mostly repeats): uniform cube 2.6 % and LiDAR scan
+            // 5.5 % faster, clustered cloud (full rows) 2.5 % slower.
+            constexpr uint32_t kLaneRows = (kWalkRows + kCopyLanes - 1) / kCopyLanes;
+            uint32_t rs[kLaneRows], rn[kLaneRows], ne = 0;
+#pragma unroll
+            for (uint32_t t = 0; t < kLaneRows; ++t) {
+              const bool ok = q + t * kCopyLanes < nrows;
+              const uint32_t rr = ok ? q + t * kCopyLanes : 0u;
+              const uint32_t rz = (uint32_t)(((float)rr + 0.5f) * rny), ry = rr - rz * ny;
+              const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
+              const uint32_t e0 = s_cell[rw + x0], e1 = s_cell[rw + x1 + 1];
+              rs[t] = e0;
+              rn[t] = ok ? e1 - e0 : 0u;
+              ne += rn[t];
+            }
+            // more entries than the lane's budget: the sample is flagged (the
+            // same samples as a row-by-row test: running totals only grow)
+            if (ne > kWalkLaneEntries) {
+              big = true;
+            } else {
+              for (uint32_t f = 0; f < ne; f += 4) {
+                uint32_t ee[4];
+#pragma unroll
+                for (uint32_t t = 0; t < 4; ++t) {  // list position -> entry
+                  const uint32_t ff = f + t < ne ? f + t : ne - 1;
+                  uint32_t e = rs[0] + ff, acc = rn[0];
+#pragma unroll
+                  for (uint32_t u = 1; u < kLaneRows; ++u) {
+                    e = ff >= acc ? rs[u] + (ff - acc) : e;
+                    acc += rn[u];
+                  }
+                  ee[t] = e;
+                }
+                walk4(ee);
+              }
+            }
+          } else {
+            // shared buckets: row by row, each row's entries and then the
+            // other-cell records of its coarse cells (the budget counts both)
+            uint32_t budget = kWalkLaneEntries;
+            for (uint32_t rr = q; rr < nrows; rr += kCopyLanes) {
+              const uint32_t rz = (uint32_t)(((float)rr + 0.5f) * rny), ry = rr - rz * ny;
+              const uint32_t rw = ((z0 + rz) * gy + y0 + ry) * gx;
+              const uint32_t e0 = s_cell[rw + x0], e1 = s_cell[rw + x1 + 1];
+              const uint32_t f0 = s_xc[rw + x0], f1 = s_xc[rw + x1 + 1];
+              if (e1 - e0 + (f1 - f0) > budget) {
+                big = true;
+                break;
+              }
+              budget -= e1 - e0 + (f1 - f0);
+              for (uint32_t e = e0; e < e1; e += 4) {
+                uint32_t ee[4];
+#pragma unroll
+                for (uint32_t t = 0; t < 4; ++t) ee[t] = e + t < e1 ? e + t : e1 - 1;
+                walk4(ee);
+              }
+              for (uint32_t f = f0; f < f1; ++f) {
+                const uint4 pa = s_xp[f];
+                const uint32_t ea = s_xe[f];
+                const uint32_t da =
+                    __float_as_uint(sqdist(__uint_as_float(pa.x), __uint_as_float(pa.y),
+                                           __uint_as_float(pa.z), px, py, pz));
+                atomicMin(&s_dd[ea], in_box11(pa.w | kGuards, pa.w, lo11, hi11g) ? da : 0xffffffffu);
+              }
             }
           }
         }
