@@ -896,29 +896,26 @@ struct RoundSchedule {
 RoundSchedule g_schedule;
 
 // Helper workgroups of a fused round for a single cloud of nl1 level-1
-// nodes: one per node when that many fit beside the run on the device at
-// once and there are at least kFusedMinNodes of them, else 0 (classic
-// rounds).  Measured on the MI355X: a helper owning several nodes steps
-// slower than the run publishes (1M-point uniform cube, 512 nodes over 255
-// helpers: a 20 us tail per round against the 14 us update pass it
-// replaces), and on a small cloud the update pass is shorter than the
-// helpers' tail (10,000 points, 3 nodes: 1.64 against 1.38 ms per call);
-// the 120,000-point scan (93 nodes) gains 0.45 ms.  NSFPS_FUSED=1 uses them
-// whenever they fit (up to fused_max_nodes_per_helper() nodes per helper),
-// NSFPS_NO_FUSED=1 never.  Several clouds take classic rounds.
-constexpr uint32_t kFusedMinNodes = 64;
-
+// nodes, when NSFPS_FUSED=1: one per node where they fit beside the run on
+// the device at once (up to fused_max_nodes_per_helper() nodes per helper),
+// else 0 (classic rounds).  Off by default: measured on the MI355X, a helper
+// owning several nodes steps slower than the run publishes (1M-point uniform
+// cube, 512 nodes over 255 helpers: a 20 us tail per round against the 14 us
+// update pass it replaces), a small cloud's update pass is shorter than the
+// helpers' tail (10,000 points, 3 nodes: 1.64 against 1.38 ms per call), and
+// on the 120,000-point scan (93 nodes, one helper each), where they once
+// gained 0.45 ms, the present run kernel leaves them no gain (4.52 ms per
+// call either way).  Several clouds always take classic rounds.
 uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
-  if (nclouds != 1 || getenv("NSFPS_NO_FUSED")) return 0;
+  if (nclouds != 1) return 0;
   const char *force = getenv("NSFPS_FUSED");
-  const bool forced = force && atoi(force) == 1;
+  if (!(force && atoi(force) == 1) || getenv("NSFPS_NO_FUSED")) return 0;
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       fused_blocks_per_cu(&per_cu) != hipSuccess || per_cu < 1 || cus < 2)
     return 0;
   const uint32_t cap = (uint32_t)(cus * per_cu - 1);
-  if (!forced) return nl1 <= cap && nl1 >= kFusedMinNodes ? nl1 : 0u;
   const uint32_t h = std::min<uint32_t>(nl1, cap);
   if (h == 0 || (nl1 + h - 1) / h > fused_max_nodes_per_helper()) return 0;
   return h;
