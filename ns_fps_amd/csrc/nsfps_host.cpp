@@ -300,12 +300,23 @@ void bbox_of(const float *xyz, uint64_t n, nsfps_range &r) { bboxes(xyz, 1, n, &
 
 // ------------------------------------------------------------ workspace ----
 
+// Pinned host memory that host-buffer inputs pass through on their way to
+// the device: allocated once, grown when a call needs more, kept until the
+// process ends.  `done` is recorded after the last copy out of it.
+struct PinStage {
+  char *p = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+
 struct Arena {
   char *base = nullptr;
   size_t cap = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   int device = -1;
+  PinStage pin;
 };
 
 std::mutex g_mu;
@@ -357,6 +368,62 @@ nsfps_status arena_reserve(Arena &a, size_t bytes) {
     return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", want, hipGetErrorString(e));
   }
   a.cap = want;
+  return NSFPS_OK;
+}
+
+// Host-buffer inputs to the device through the arena's pinned stage, in
+// chunks: the CPU copies a chunk into pinned memory and the DMA of each
+// chunk overlaps the copy of the next.  A pageable source would instead be
+// pinned by the runtime on every new buffer (measured on the MI355X box: the
+// upload of a fresh 12.6 MB array cost 4.4 ms, of one whose pages the
+// runtime had cached 0.37 ms; pinned, 0.23 ms).  Without pinned memory the
+// copies are made from the source as it is.
+struct HostUp {
+  void *dst;
+  const void *src;
+  size_t bytes;
+};
+
+nsfps_status upload_host(const std::vector<HostUp> &ups, hipStream_t st) {
+  size_t total = 0;
+  for (const auto &u : ups) total += (u.bytes + 255) & ~size_t(255);
+  if (total == 0) return NSFPS_OK;
+  Arena *ap = nullptr;
+  nsfps_status rc = arena_for_device(&ap);
+  if (rc) return rc;
+  PinStage &ps = ap->pin;
+  if (ps.pending) {  // an earlier call's copies may still read the stage
+    HIP_TRY(hipEventSynchronize(ps.done));
+    ps.pending = false;
+  }
+  if (!ps.done) HIP_TRY(hipEventCreateWithFlags(&ps.done, hipEventDisableTiming));
+  if (total > ps.cap) {
+    if (ps.p) HIP_TRY(hipHostFree(ps.p));
+    ps.p = nullptr;
+    ps.cap = 0;
+    const size_t want = total + total / 8 + (1u << 20);
+    if (hipHostMalloc(reinterpret_cast<void **>(&ps.p), want, hipHostMallocDefault) != hipSuccess) {
+      ps.p = nullptr;
+      (void)hipGetLastError();
+      for (const auto &u : ups)
+        HIP_TRY(hipMemcpyAsync(u.dst, u.src, u.bytes, hipMemcpyHostToDevice, st));
+      return NSFPS_OK;
+    }
+    ps.cap = want;
+  }
+  constexpr size_t kChunk = size_t(2) << 20;
+  size_t at = 0;
+  for (const auto &u : ups) {
+    for (size_t off = 0; off < u.bytes; off += kChunk) {
+      const size_t n = std::min(kChunk, u.bytes - off);
+      memcpy(ps.p + at + off, static_cast<const char *>(u.src) + off, n);
+      HIP_TRY(hipMemcpyAsync(static_cast<char *>(u.dst) + off, ps.p + at + off, n,
+                             hipMemcpyHostToDevice, st));
+    }
+    at += (u.bytes + 255) & ~size_t(255);
+  }
+  HIP_TRY(hipEventRecord(ps.done, st));
+  ps.pending = true;
   return NSFPS_OK;
 }
 
@@ -731,14 +798,16 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   for (size_t i = 0; i < nc && one_copy; ++i)
     one_copy = plans[i].h_xyz && (i == 0 || plans[i].h_xyz == plans[i - 1].h_xyz +
                                                                 (size_t)plans[i - 1].n * 3);
+  std::vector<HostUp> ups;
   if (one_copy) {
-    HIP_TRY(hipMemcpyAsync(cb.xyz_stage, plans[0].h_xyz, cb.n_total * 12, hipMemcpyHostToDevice,
-                           st));
+    ups.push_back({cb.xyz_stage, plans[0].h_xyz, (size_t)cb.n_total * 12});
   } else {
     for (auto &p : plans)
-      if (p.h_xyz)
-        HIP_TRY(hipMemcpyAsync(p.d_xyz_stage, p.h_xyz, (size_t)p.n * 12, hipMemcpyHostToDevice,
-                               st));
+      if (p.h_xyz) ups.push_back({p.d_xyz_stage, p.h_xyz, (size_t)p.n * 12});
+  }
+  {
+    const nsfps_status rc = upload_host(ups, st);
+    if (rc) return rc;
   }
   HIP_TRY(launch_fill_u32(cb.counts, 0u, cb.counts_total, st));
   HIP_TRY(launch_fill_u32(cb.small, 0u, nc * 4, st));
