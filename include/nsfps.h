@@ -235,7 +235,8 @@ nsfps_status nsfps_get_stats(nsfps_stats *stats);
  * (100 MHz).  No counterpart in the reference (it has no instrumentation). */
 nsfps_status nsfps_get_loop_profile(uint64_t *words, uint32_t nwords);
 
-/* Releases the cached device workspace of the calling process. */
+/* Releases the cached device workspace of the calling process, and the pinned
+ * host buffer that host-buffer inputs are staged through. */
 void nsfps_release_workspace(void);
 
 #ifdef __cplusplus

@@ -79,6 +79,11 @@ class Lib:
                                        r, out.ctypes.data_as(_vp), ctypes.byref(n)))
         return out[:n.value].copy()
 
+    def release_workspace(self):
+        """Frees the cached device workspace and the pinned input stage."""
+        self.lib.nsfps_release_workspace.restype = None
+        self.lib.nsfps_release_workspace()
+
     def fps_bbox(self, points, n_samples, blocks=(16, 16, 16)):
         p = np.ascontiguousarray(points, dtype=np.float32)
         out = np.zeros(max(int(n_samples), 1), np.int32)

@@ -1995,6 +1995,13 @@ void nsfps_release_workspace(void) {
       a.base = nullptr;
       a.cap = 0;
     }
+    if (a.pin.p) {
+      if (a.pin.pending) (void)hipEventSynchronize(a.pin.done);
+      (void)hipHostFree(a.pin.p);
+      a.pin.p = nullptr;
+      a.pin.cap = 0;
+      a.pin.pending = false;
+    }
   }
 }
 

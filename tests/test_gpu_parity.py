@@ -339,3 +339,24 @@ def test_repeated_calls_are_bit_identical(lib, name):
         else:
             got = lib.fps(case.points, case.n_samples, case.range)
         assert np.array_equal(got, case.expected), (name, i)
+
+
+def test_host_buffer_calls_across_a_workspace_release(lib):
+    """Host-buffer inputs reach the device through a pinned buffer kept per
+    device, in 2 MB chunks.  Fresh arrays each call, a 1M-point cloud (six
+    chunks) and calls after nsfps_release_workspace has freed the buffer all
+    return the reference's samples."""
+    from ns_fps_amd.workloads import make_workload
+    case = next(c for c in GOLDEN_CASES if c.name == "quickstart_full")
+    w = make_workload("uniform_cube")
+    P, m = w["clouds"][0], int(w["n_samples"])
+    digest = GOLDEN_CONFIGS["uniform_cube"]["output_sha256"][0]
+    for step in ("before", "after"):
+        for _ in range(2):
+            got = lib.fps(case.points.copy(), case.n_samples, case.range)
+            assert np.array_equal(got, case.expected), step
+        assert sha256_i32(lib.fps(P.copy(), m, w["range"])) == digest, step
+        assert np.array_equal(lib.fps(case.points.copy(), case.n_samples, case.range),
+                              case.expected), step
+        if step == "before":
+            lib.release_workspace()
