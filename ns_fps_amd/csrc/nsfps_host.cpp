@@ -11,6 +11,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <condition_variable>
+#include <functional>
 #include <cmath>
 #include <cstdarg>
 #include <cstddef>
@@ -241,9 +243,80 @@ void bounds_piece(const float *xyz, uint64_t lo, uint64_t hi, const float *p0, f
   }
 }
 
+// Worker threads for host-side scans, started on first need and kept until
+// the process ends (starting threads on every call cost about as much as the
+// scan they split).  run() splits f(0 .. n - 1) statically between the caller
+// (q % parts == 0) and every worker (q % parts == its id), and returns once
+// each worker has checked in for that call.  Calls to run() are serialised.
+class HostPool {
+ public:
+  ~HostPool() {
+    {
+      std::lock_guard<std::mutex> l(m_);
+      stop_ = true;
+    }
+    go_.notify_all();
+    for (auto &t : th_) t.join();
+  }
+  void run(uint64_t n, unsigned want, const std::function<void(uint64_t)> &f) {
+    std::lock_guard<std::mutex> one(run_mu_);
+    std::unique_lock<std::mutex> l(m_);
+    while (th_.size() + 1 < want) {
+      try {  // a worker that cannot be started leaves its share to the others
+        const unsigned id = (unsigned)th_.size() + 1;
+        th_.emplace_back([this, id, g = gen_] { loop(id, g); });
+      } catch (...) {
+        break;
+      }
+    }
+    const unsigned k = (unsigned)th_.size();
+    job_ = &f;
+    n_ = n;
+    parts_ = k + 1;
+    finished_ = 0;
+    ++gen_;
+    l.unlock();
+    go_.notify_all();
+    for (uint64_t q = 0; q < n; q += k + 1) f(q);
+    l.lock();
+    done_.wait(l, [&] { return finished_ == k; });
+    job_ = nullptr;
+  }
+
+ private:
+  void loop(unsigned id, uint64_t seen) {
+    std::unique_lock<std::mutex> l(m_);
+    for (;;) {
+      go_.wait(l, [&] { return stop_ || gen_ != seen; });
+      if (stop_) return;
+      seen = gen_;
+      const std::function<void(uint64_t)> *f = job_;
+      const uint64_t n = n_, step = parts_;
+      l.unlock();
+      for (uint64_t q = id; q < n; q += step) (*f)(q);
+      l.lock();
+      ++finished_;
+      done_.notify_one();
+    }
+  }
+  std::mutex run_mu_, m_;
+  std::condition_variable go_, done_;
+  std::vector<std::thread> th_;
+  const std::function<void(uint64_t)> *job_ = nullptr;
+  uint64_t n_ = 0, parts_ = 1, gen_ = 0;
+  unsigned finished_ = 0;
+  bool stop_ = false;
+};
+
+HostPool &host_pool() {
+  static HostPool pool;
+  return pool;
+}
+
 // compute_bbox of `count` clouds of n points each (ranges[b] gets cloud b's
 // bounds +- 1e-6; block counts untouched).  Pieces of at least kPiece points
-// are spread over up to 16 threads when there is enough work.
+// are spread over up to 16 threads of the host pool when there is enough
+// work.
 void bboxes(const float *xyz, uint64_t count, uint64_t n, nsfps_range *ranges) {
   constexpr uint64_t kPiece = 1u << 16;
   const uint64_t per = n ? (n + kPiece - 1) / kPiece : 0;  // pieces per cloud
@@ -259,19 +332,7 @@ void bboxes(const float *xyz, uint64_t count, uint64_t n, nsfps_range *ranges) {
   if (nt <= 1 || count * n < 4 * kPiece) {
     for (uint64_t q = 0; q < pieces; ++q) run(q);
   } else {
-    std::vector<std::thread> th;
-    uint64_t started = 0;
-    try {  // a thread that cannot be started leaves its share to this one
-      th.reserve(nt);
-      for (; started < nt; ++started)
-        th.emplace_back([&, t = started] {
-          for (uint64_t q = t; q < pieces; q += nt) run(q);
-        });
-    } catch (...) {
-    }
-    for (uint64_t t = started; t < nt; ++t)
-      for (uint64_t q = t; q < pieces; q += nt) run(q);
-    for (auto &x : th) x.join();
+    host_pool().run(pieces, (unsigned)nt, run);
   }
   for (uint64_t b = 0; b < count; ++b) {
     nsfps_range &r = ranges[b];

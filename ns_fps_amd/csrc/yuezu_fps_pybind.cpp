@@ -203,21 +203,30 @@ py::tuple fps_batched_py(py::handle points, uint64_t n_samples, py::object range
   uint64_t cols = std::min<uint64_t>(n_samples, n);
   py::array_t<int32_t> out({(py::ssize_t)B, (py::ssize_t)cols});
   py::array_t<int64_t> lens((py::ssize_t)B);
-  std::vector<int32_t> buf((size_t)std::max<uint64_t>(B * std::max<uint64_t>(n_samples, 1), 1));
+  // rows of n_samples on both sides (n_samples <= n): the library writes the
+  // result array itself; otherwise through a buffer of its row stride
+  const bool direct = cols == n_samples && cols > 0;
+  std::vector<int32_t> buf(
+      direct ? 0 : (size_t)std::max<uint64_t>(B * std::max<uint64_t>(n_samples, 1), 1));
   std::vector<uint64_t> lv(B);
   uint32_t blocks[3] = {xb, yb, zb};
+  int32_t *o = out.mutable_data();
+  int32_t *dst = direct ? o : buf.data();
   nsfps_status s;
   {
     py::gil_scoped_release nogil;
     s = nsfps_fps_batched(p.data(), B, n, n_samples, rs.empty() ? nullptr : rs.data(), blocks,
-                          buf.data(), lv.data());
+                          dst, lv.data());
   }
   if (s != NSFPS_OK) raise_status(s);
-  int32_t *o = out.mutable_data();
   int64_t *l = lens.mutable_data();
   for (uint64_t b = 0; b < B; ++b) {
     l[b] = (int64_t)lv[b];
-    for (uint64_t j = 0; j < cols; ++j) o[b * cols + j] = j < lv[b] ? buf[b * n_samples + j] : -1;
+    if (direct) {
+      for (uint64_t j = lv[b]; j < cols; ++j) o[b * cols + j] = -1;
+    } else {
+      for (uint64_t j = 0; j < cols; ++j) o[b * cols + j] = j < lv[b] ? buf[b * n_samples + j] : -1;
+    }
   }
   return py::make_tuple(out, lens);
 }
