@@ -27,6 +27,8 @@
 #include <thread>
 #include <vector>
 
+#include <unistd.h>
+
 #include "nsfps_internal.h"
 #include "nsfps_launch.h"
 
@@ -248,17 +250,17 @@ void bounds_piece(const float *xyz, uint64_t lo, uint64_t hi, const float *p0, f
 // scan they split).  run() splits f(0 .. n - 1) statically between the caller
 // (q % parts == 0) and every worker (q % parts == its id), and returns once
 // each worker has checked in for that call.  Calls to run() are serialised.
+// A process forked from the owner has none of its threads (and maybe a lock
+// held at the fork): there run() works alone, touching no pool state.  The
+// pool is never destroyed, so no thread is joined at exit.
 class HostPool {
  public:
-  ~HostPool() {
-    {
-      std::lock_guard<std::mutex> l(m_);
-      stop_ = true;
-    }
-    go_.notify_all();
-    for (auto &t : th_) t.join();
-  }
+  HostPool() : pid_(getpid()) {}
   void run(uint64_t n, unsigned want, const std::function<void(uint64_t)> &f) {
+    if (getpid() != pid_) {
+      for (uint64_t q = 0; q < n; ++q) f(q);
+      return;
+    }
     std::lock_guard<std::mutex> one(run_mu_);
     std::unique_lock<std::mutex> l(m_);
     while (th_.size() + 1 < want) {
@@ -287,8 +289,7 @@ class HostPool {
   void loop(unsigned id, uint64_t seen) {
     std::unique_lock<std::mutex> l(m_);
     for (;;) {
-      go_.wait(l, [&] { return stop_ || gen_ != seen; });
-      if (stop_) return;
+      go_.wait(l, [&] { return gen_ != seen; });
       seen = gen_;
       const std::function<void(uint64_t)> *f = job_;
       const uint64_t n = n_, step = parts_;
@@ -299,18 +300,18 @@ class HostPool {
       done_.notify_one();
     }
   }
+  const pid_t pid_;
   std::mutex run_mu_, m_;
   std::condition_variable go_, done_;
   std::vector<std::thread> th_;
   const std::function<void(uint64_t)> *job_ = nullptr;
   uint64_t n_ = 0, parts_ = 1, gen_ = 0;
   unsigned finished_ = 0;
-  bool stop_ = false;
 };
 
 HostPool &host_pool() {
-  static HostPool pool;
-  return pool;
+  static HostPool *const pool = new HostPool;  // never destroyed (see above)
+  return *pool;
 }
 
 // compute_bbox of `count` clouds of n points each (ranges[b] gets cloud b's

@@ -151,6 +151,39 @@ def test_capi_bbox_nan_rules_match_the_running_pass(capi, oracle, n):
         assert np.isnan(got[2]) == (where == 0)
 
 
+def test_capi_bbox_in_a_child_forked_after_the_worker_threads_started(capi, oracle):
+    """Large bounds run on worker threads that the library starts once and
+    keeps.  A process forked after they started (multiprocessing's default on
+    Linux) has none of them; its calls must still return, with the same
+    bounds."""
+    import signal
+    import time
+    pts = np.random.RandomState(11).randn(1 << 20, 3).astype(np.float32)
+    want = _capi_bbox(capi, pts)  # starts the workers in this process
+    assert want.tobytes() == oracle.bbox(pts).tobytes()
+    pid = os.fork()
+    if pid == 0:  # the child: exit status 0 only for the same bounds, twice
+        code = 1
+        try:
+            ok = all(_capi_bbox(capi, pts).tobytes() == want.tobytes() for _ in range(2))
+            code = 0 if ok else 1
+        finally:
+            os._exit(code)
+    deadline = time.monotonic() + 60
+    while True:
+        done, status = os.waitpid(pid, os.WNOHANG)
+        if done:
+            break
+        if time.monotonic() > deadline:
+            os.kill(pid, signal.SIGKILL)
+            os.waitpid(pid, 0)
+            pytest.fail("the forked child's bounds call did not return")
+        time.sleep(0.05)
+    assert os.WIFEXITED(status) and os.WEXITSTATUS(status) == 0
+    # and the parent's workers still serve it
+    assert _capi_bbox(capi, pts).tobytes() == want.tobytes()
+
+
 def test_capi_rejects_bad_arguments(capi):
     capi.nsfps_last_error.restype = ctypes.c_char_p
     pts = np.zeros((10, 3), np.float32)
