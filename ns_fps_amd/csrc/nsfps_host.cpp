@@ -1052,14 +1052,24 @@ uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
   return h;
 }
 
+// Rounds whose clouds all have at most this many points use the update pass
+// that also bounds each pick by each leaf's box of points (the bound's extra
+// work pays where cubes are large against the leaves: sparse clouds).
+// Measured on the MI355X: 10,000-point quickstart 1.04 -> 0.99 ms per call,
+// 120,000-point scan 4.55 -> 4.40; with it, the 1M-point uniform cube was
+// 1.8 % slower and the 8M-point clustered cloud 0.8 %.
+constexpr uint32_t kLeafBoundMaxPoints = 262144;
+
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
                         uint64_t *rounds_out, uint32_t *repairs_out) {
   uint32_t max_nl1 = 1;
   bool alias = false;  // some cloud's cells share buckets
+  bool leaf_bound = true;  // every cloud small enough for the leaf-box bound
   for (auto &p : plans) {
     max_nl1 = std::max(max_nl1, p.dev.nl1);
     alias = alias || !p.rng.dev.bijective;
+    leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
   }
   const uint32_t nc = (uint32_t)plans.size();
   const uint32_t helpers = alias ? 0u : fused_helpers(nc, max_nl1);
@@ -1078,8 +1088,8 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     for (const auto &bp : g_schedule.batches) {
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, helpers, &seq,
-                            st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
+                            helpers, &seq, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1088,8 +1098,8 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   }
   while (true) {
     if (!launched) {
-      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, helpers, &seq,
-                            st));
+      HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
+                            helpers, &seq, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }

@@ -276,7 +276,7 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // any cell of the leaf's bucket (src/yuezu_fps.cpp:573-597 updates every point
 // of every bucket of the cube's cells); nodes are screened by the corners of
 // those cells.
-template <bool PROF, bool ALIAS>
+template <bool PROF, bool ALIAS, bool LB>
 __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
@@ -294,12 +294,19 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t leaf0 = g * kFan + wave * kLeavesPerWave;
   uint64_t mkey = 0;
   uint32_t mcell = 0, mst = 0, mcnt = 0;
+  // LB (leaf bounds): the leaf's box of points (an absent leaf's stays empty)
+  constexpr bool lbound = LB;
+  float4 mlo = make_float4(0.f, 0.f, 0.f, 0.f), mhi = mlo;
   if (lane < kLeavesPerWave && leaf0 + lane < c.nleaves) {
     mkey = gptr(c.leaf_key)[leaf0 + lane];
     mcell = gptr(c.leaf_cell)[leaf0 + lane];
     const uint2 sc = gptr(c.leaf_sc)[leaf0 + lane];
     mst = sc.x;
     mcnt = sc.y;
+    if (lbound) {
+      mlo = gptr(c.leaf_lo)[leaf0 + lane];
+      mhi = gptr(c.leaf_hi)[leaf0 + lane];
+    }
   }
   const NSFPS_GLOBAL RunState &rs = rstate(c);
   const uint32_t done = *gptr(c.done);
@@ -394,16 +401,32 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   // four leaves (past nsel: stale LDS, masked out)
   const uint2 pc0 = s_pc[lane];
   const bool in0 = lane < nsel;
+  const float4 pp0 = lbound ? s_pp[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
     c11[k] = pack11(rdlane(mcell, k));
     st[k] = rdlane(mst, k);
     cnt[k] = rdlane(mcnt, k);
     okey[k] = ((uint64_t)rdlane((uint32_t)(mkey >> 32), k) << 32) | rdlane((uint32_t)mkey, k);
-    hm[k] = __ballot(in0 & touches_pick(k, pc0));
+    // with leaf bounds, a pick takes part in leaf k only if its squared
+    // distance to the leaf's box (in sqdist's operation order, so never above
+    // a point's distance) is below the leaf key's distance, the largest of
+    // its points: otherwise it lowers none of them
+    const float lmax = __uint_as_float((uint32_t)(okey[k] >> 32));
+    const float4 blo = make_float4(__uint_as_float(rdlane(__float_as_uint(mlo.x), k)),
+                                   __uint_as_float(rdlane(__float_as_uint(mlo.y), k)),
+                                   __uint_as_float(rdlane(__float_as_uint(mlo.z), k)), 0.f);
+    const float4 bhi = make_float4(__uint_as_float(rdlane(__float_as_uint(mhi.x), k)),
+                                   __uint_as_float(rdlane(__float_as_uint(mhi.y), k)),
+                                   __uint_as_float(rdlane(__float_as_uint(mhi.z), k)), 0.f);
+    const auto may_lower = [&](float4 q) -> bool {
+      return !lbound ||
+             !(box_bound(q.x, q.y, q.z, blo.x, blo.y, blo.z, bhi.x, bhi.y, bhi.z) >= lmax);
+    };
+    hm[k] = __ballot(in0 & touches_pick(k, pc0) & may_lower(pp0));
     bool h = hm[k] != 0;
     for (uint32_t cb = 64; cb < nsel && !h; cb += 64)
-      h = __ballot((cb + lane < nsel) & touches(k, cb + lane)) != 0;
+      h = __ballot((cb + lane < nsel) && touches(k, cb + lane) && may_lower(s_pp[cb + lane])) != 0;
     hit[k] = h;
     need[k] = leaf0 + k < c.nleaves && (h || okey[k] >= wlo);
   }
@@ -2246,7 +2269,7 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 
 hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                               hipStream_t st) {
-  k_update<false, false><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
+  k_update<false, false, false><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
   return hipGetLastError();
 }
 
@@ -2263,10 +2286,10 @@ hipError_t fused_blocks_per_cu(int *blocks) {
 }
 
 // The classic round's update, gather and run kernels of one variant.
-template <bool PROF, bool ALIAS>
+template <bool PROF, bool ALIAS, bool LB>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
                     uint32_t passes, hipStream_t st) {
-  k_update<PROF, ALIAS><<<grid, kPassThreads, 0, st>>>(d_clouds);
+  k_update<PROF, ALIAS, LB><<<grid, kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
@@ -2275,7 +2298,7 @@ void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         uint32_t helpers, uint32_t *seq, hipStream_t st) {
+                         bool leaf_bound, uint32_t helpers, uint32_t *seq, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
   if (helpers) {  // fused rounds of one cloud (one cell per bucket)
@@ -2295,12 +2318,14 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
     }
     return hipGetLastError();
   }
-  for (uint32_t r = 0; r < rounds; ++r) {
-    if (profile && alias) launch_classic<true, true>(d_clouds, nclouds, grid, sparse, passes, st);
-    else if (profile) launch_classic<true, false>(d_clouds, nclouds, grid, sparse, passes, st);
-    else if (alias) launch_classic<false, true>(d_clouds, nclouds, grid, sparse, passes, st);
-    else launch_classic<false, false>(d_clouds, nclouds, grid, sparse, passes, st);
-  }
+  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, hipStream_t);
+  static constexpr Launch kClassic[2][2][2] = {  // [profile][alias][leaf_bound]
+      {{launch_classic<false, false, false>, launch_classic<false, false, true>},
+       {launch_classic<false, true, false>, launch_classic<false, true, true>}},
+      {{launch_classic<true, false, false>, launch_classic<true, false, true>},
+       {launch_classic<true, true, false>, launch_classic<true, true, true>}}};
+  const Launch classic = kClassic[profile][alias][leaf_bound];
+  for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, st);
   return hipGetLastError();
 }
 
