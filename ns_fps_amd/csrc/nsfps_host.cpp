@@ -566,6 +566,8 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.leaf_key = bp.take<uint64_t>(leaves);
   c.leaf_pos = bp.take<float4>(leaves);
   c.l1_key = bp.take<uint64_t>(p.l1_ub);
+  c.l1_part = bp.take<uint64_t>((size_t)p.l1_ub * kUpdateSplit);
+  c.l1_cnt = bp.take<uint32_t>(p.l1_ub);
   c.l1_pos = bp.take<float4>(p.l1_ub);
   c.l1_lo = bp.take<float4>(p.l1_ub);
   c.l1_hi = bp.take<float4>(p.l1_ub);
@@ -1059,6 +1061,11 @@ uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
 // 120,000-point scan 4.55 -> 4.40; with it, the 1M-point uniform cube was
 // 1.8 % slower and the 8M-point clustered cloud 0.8 %.
 constexpr uint32_t kLeafBoundMaxPoints = 262144;
+// Rounds with at most this many level-1 nodes over all clouds split each
+// node's leaves over kUpdateSplit workgroups of the update pass (its work
+// then spreads over that many more CUs; a node's key is folded by the last
+// of its workgroups to finish)
+constexpr uint32_t kSplitMaxNodes = 128;
 
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
@@ -1072,6 +1079,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
   }
   const uint32_t nc = (uint32_t)plans.size();
+  const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
   const uint32_t helpers = alias ? 0u : fused_helpers(nc, max_nl1);
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
@@ -1089,7 +1097,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            helpers, &seq, st));
+                            split, helpers, &seq, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1099,7 +1107,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            helpers, &seq, st));
+                            split, helpers, &seq, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }

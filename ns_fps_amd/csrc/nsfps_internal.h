@@ -29,6 +29,8 @@ constexpr uint32_t kNone = 0xffffffffu;
 // the most picks one run can accept), bins per key histogram, histograms per
 // round (one from the update pass, then two refinement passes).
 constexpr uint32_t kListCap = 1024;
+// workgroups per level-1 node in the split update pass
+constexpr uint32_t kUpdateSplit = 4;
 constexpr uint32_t kHistBins = 4096;
 constexpr uint32_t kHists = 3;
 constexpr uint32_t kRefinePasses = 2;  // refinement passes when they are launched
@@ -137,6 +139,8 @@ struct CloudDev {
   uint64_t *leaf_key;         // max key of the leaf
   float4 *leaf_pos;           // x, y, z, input row (bits) of that key
   uint64_t *l1_key;
+  uint64_t *l1_part;  // split update pass: kUpdateSplit partial keys per node
+  uint32_t *l1_cnt;   //   and each node's arrivals (zero between launches)
   float4 *l1_pos;
   const float4 *l1_lo;        // level-1 bounding boxes
   const float4 *l1_hi;

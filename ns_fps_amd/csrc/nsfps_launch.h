@@ -94,10 +94,12 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 // (launch_update_pass) for the first pick.
 // *seq counts the call's fused launches (each gets the next number).  alias:
 // some cloud's cells share buckets (classic rounds only).  leaf_bound: the
-// update pass also bounds each pick by each leaf's box (classic rounds only).
+// update pass also bounds each pick by each leaf's box; split: it takes
+// kUpdateSplit workgroups per level-1 node (both classic rounds only).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, uint32_t helpers, uint32_t *seq, hipStream_t st);
+                         bool leaf_bound, bool split, uint32_t helpers, uint32_t *seq,
+                         hipStream_t st);
 hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                               hipStream_t st);
 uint32_t fused_max_nodes_per_helper();

@@ -276,7 +276,7 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // any cell of the leaf's bucket (src/yuezu_fps.cpp:573-597 updates every point
 // of every bucket of the cube's cells); nodes are screened by the corners of
 // those cells.
-template <bool PROF, bool ALIAS, bool LB>
+template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT>
 __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
   __shared__ uint32_t s_hist[kHistBins];
@@ -287,17 +287,20 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   __shared__ uint32_t s_ct[4];  // PROF: leaves and points read by the workgroup, and of them touched
   __shared__ uint32_t s_wt[PROF ? 3 * kPassWaves : 1];  // PROF: per-wave clocks
   const CloudDev &c = clouds[blockIdx.y];
-  const uint32_t g = blockIdx.x;
+  // SPLIT workgroups per node: this one takes leaves sub * kFan / SPLIT ..
+  constexpr uint32_t kLPW = kLeavesPerWave / SPLIT;  // leaves per wave
+  static_assert(kLPW >= 1 && kLPW * SPLIT == kLeavesPerWave, "whole leaves per wave");
+  const uint32_t g = blockIdx.x / SPLIT, sub = blockIdx.x % SPLIT;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint64_t ut0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
-  // this wave's leaves: lane k < kLeavesPerWave holds leaf leaf0 + k's record
-  const uint32_t leaf0 = g * kFan + wave * kLeavesPerWave;
+  // this wave's leaves: lane k < kLPW holds leaf leaf0 + k's record
+  const uint32_t leaf0 = g * kFan + sub * (kFan / SPLIT) + wave * kLPW;
   uint64_t mkey = 0;
   uint32_t mcell = 0, mst = 0, mcnt = 0;
   // LB (leaf bounds): the leaf's box of points (an absent leaf's stays empty)
   constexpr bool lbound = LB;
   float4 mlo = make_float4(0.f, 0.f, 0.f, 0.f), mhi = mlo;
-  if (lane < kLeavesPerWave && leaf0 + lane < c.nleaves) {
+  if (lane < kLPW && leaf0 + lane < c.nleaves) {
     mkey = gptr(c.leaf_key)[leaf0 + lane];
     mcell = gptr(c.leaf_cell)[leaf0 + lane];
     const uint2 sc = gptr(c.leaf_sc)[leaf0 + lane];
@@ -320,13 +323,13 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   uint64_t uta = 0, utb = 0, utc = 0, utd = 0;
   // the node's box of points (x > its hi x: no points)
   const float4 nlo = gptr(c.l1_lo)[gn], nhi = gptr(c.l1_hi)[gn];
-  // the cells of this wave's leaves' buckets: lane i < kLeavesPerWave * na
+  // the cells of this wave's leaves' buckets: lane i < kLPW * na
   // holds word i of the wave's stretch of leaf_al
   const uint32_t na = ALIAS ? c.r.na : 1u;
   uint32_t mal = kNoCell;
   if (ALIAS) {
     const uint2 cb = gptr(c.l1_cbox)[gn];
-    if (lane < kLeavesPerWave * na && leaf0 + lane / na < c.nleaves)
+    if (lane < kLPW * na && leaf0 + lane / na < c.nleaves)
       mal = gptr(c.leaf_al)[(size_t)leaf0 * na + lane];
     pin_sgpr(done, npicks, kref, S, hsel, nkey, cb.x, cb.y, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y,
              nhi.z);
@@ -374,9 +377,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   if (nsel == 0 && nkey < wlo) return;  // nothing changes, nothing to count
   // which leaves a pick touches (hm: the first 64 picks whose cube holds the
   // leaf's cell), and which must be read
-  uint32_t c11[kLeavesPerWave], st[kLeavesPerWave], cnt[kLeavesPerWave];
-  uint64_t okey[kLeavesPerWave], hm[kLeavesPerWave];
-  bool hit[kLeavesPerWave], need[kLeavesPerWave];
+  uint32_t c11[kLPW], st[kLPW], cnt[kLPW];
+  uint64_t okey[kLPW], hm[kLPW];
+  bool hit[kLPW], need[kLPW];
   // pick i's cube (its s_pc record) holds (a cell of the bucket of) leaf k.
   // Testing the leaf's box against the pick as the node's is tested costs
   // more here than the reads it saves on points that fill their cells.
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const bool in0 = lane < nsel;
   const float4 pp0 = lbound ? s_pp[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+  for (uint32_t k = 0; k < kLPW; ++k) {
     c11[k] = pack11(rdlane(mcell, k));
     st[k] = rdlane(mst, k);
     cnt[k] = rdlane(mcnt, k);
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   if (PROF && lane == 0) {
     uint32_t nl = 0, npt = 0, nh = 0, nhp = 0;
 #pragma unroll
-    for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+    for (uint32_t k = 0; k < kLPW; ++k) {
       nl += need[k] ? 1u : 0u;
       npt += need[k] ? cnt[k] : 0u;
       nh += need[k] && hit[k] ? 1u : 0u;
@@ -450,21 +453,21 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
       atomicAdd(&s_ct[3], nhp);
     }
   }
-  float4 p[kLeavesPerWave];
-  uint32_t rk[kLeavesPerWave];  // logical ranks
+  float4 p[kLPW];
+  uint32_t rk[kLPW];  // logical ranks
   // every lane loads, without a branch, so that the four leaves' loads are in
   // flight together; a lane without a point of a needed leaf reads slot 0
   // (one line for the whole wave) and its values are never used: every use
   // below is guarded by lane < cnt
 #pragma unroll
-  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
+  for (uint32_t k = 0; k < kLPW; ++k) {
     const uint32_t idx = need[k] && lane < cnt[k] ? st[k] + lane : 0u;
     p[k] = gptr(c.P4)[idx];
     rk[k] = gptr(c.R)[idx];
   }
   if (PROF) {  // wait for the points (profiled build only)
 #pragma unroll
-    for (uint32_t k = 0; k < kLeavesPerWave; ++k) pin_vgpr(p[k].x, rk[k]);
+    for (uint32_t k = 0; k < kLPW; ++k) pin_vgpr(p[k].x, rk[k]);
     utd = __builtin_amdgcn_s_memrealtime();
     if (lane == 0) s_wt[wave] = (uint32_t)(utd - ut1);
   }
@@ -472,8 +475,8 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   // overlap the next leaves' work (deferring them all to the end measured
   // 0.23 ms slower per call on the 1M uniform cube)
 #pragma unroll
-  for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
-    const uint32_t li = wave * kLeavesPerWave + k;
+  for (uint32_t k = 0; k < kLPW; ++k) {
+    const uint32_t li = wave * kLPW + k;
     uint64_t key = 0;
     if (leaf0 + k < c.nleaves) {
       // unchanged unless the point holding the key is lowered below
@@ -515,11 +518,30 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   if (PROF && lane == 0) s_wt[kPassWaves + wave] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - ut1);
   __syncthreads();
   const uint64_t ut2 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
-  if (wave == 0) {
+  if (wave == 0 && SPLIT == 1) {
     const uint64_t k = s_lk[lane];
     uint32_t mh;
     const uint32_t wl = key_winner((uint32_t)(k >> 32), (uint32_t)k, true, mh);
     if (lane == 0) gptr(c.l1_key)[g] = ((uint64_t)mh << 32) | (uint32_t)s_lk[wl];
+  } else if (wave == 0) {
+    // this part's largest key (keys are unique: the rank is their low word);
+    // the node's last workgroup to arrive folds the parts into its key and
+    // clears the count for the next launch
+    const uint64_t part = wave_max_u64(lane < kFan / SPLIT ? s_lk[lane] : 0ull);
+    if (lane == 0) {
+      NSFPS_GLOBAL uint64_t *const parts = gptr(c.l1_part) + (size_t)g * SPLIT;
+      NSFPS_GLOBAL uint32_t *const cnt = gptr(c.l1_cnt) + g;
+      __hip_atomic_store(parts + sub, part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == SPLIT - 1) {
+        uint64_t m = 0;
+        for (uint32_t s = 0; s < SPLIT; ++s) {
+          const uint64_t v = __hip_atomic_load(parts + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          m = v > m ? v : m;
+        }
+        gptr(c.l1_key)[g] = m;
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
   NSFPS_GLOBAL uint32_t *H = hist_set(c, hsel);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
@@ -2231,6 +2253,9 @@ __global__ __launch_bounds__(kRunThreads) void k_round(const CloudDev *__restric
 __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__restrict__ clouds) {
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x;
+  // the split update pass's arrival counts start at zero (each launch's last
+  // arrival of a node clears them again)
+  for (uint32_t i = tid; i < c.nl1; i += kPassThreads) gptr(c.l1_cnt)[i] = 0;
   if (tid == 0) {
     NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
     rs.kref0 = ~0ull;
@@ -2269,7 +2294,7 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStrea
 
 hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                               hipStream_t st) {
-  k_update<false, false, false><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
+  k_update<false, false, false, 1><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
   return hipGetLastError();
 }
 
@@ -2286,10 +2311,10 @@ hipError_t fused_blocks_per_cu(int *blocks) {
 }
 
 // The classic round's update, gather and run kernels of one variant.
-template <bool PROF, bool ALIAS, bool LB>
+template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
                     uint32_t passes, hipStream_t st) {
-  k_update<PROF, ALIAS, LB><<<grid, kPassThreads, 0, st>>>(d_clouds);
+  k_update<PROF, ALIAS, LB, SPLIT><<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
@@ -2298,7 +2323,8 @@ void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, uint32_t helpers, uint32_t *seq, hipStream_t st) {
+                         bool leaf_bound, bool split, uint32_t helpers, uint32_t *seq,
+                         hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
   if (helpers) {  // fused rounds of one cloud (one cell per bucket)
@@ -2319,12 +2345,17 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
     return hipGetLastError();
   }
   using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, hipStream_t);
-  static constexpr Launch kClassic[2][2][2] = {  // [profile][alias][leaf_bound]
-      {{launch_classic<false, false, false>, launch_classic<false, false, true>},
-       {launch_classic<false, true, false>, launch_classic<false, true, true>}},
-      {{launch_classic<true, false, false>, launch_classic<true, false, true>},
-       {launch_classic<true, true, false>, launch_classic<true, true, true>}}};
-  const Launch classic = kClassic[profile][alias][leaf_bound];
+  constexpr uint32_t S = kUpdateSplit;
+  static constexpr Launch kClassic[2][2][2][2] = {  // [profile][alias][leaf_bound][split]
+      {{{launch_classic<false, false, false, 1>, launch_classic<false, false, false, S>},
+        {launch_classic<false, false, true, 1>, launch_classic<false, false, true, S>}},
+       {{launch_classic<false, true, false, 1>, launch_classic<false, true, false, S>},
+        {launch_classic<false, true, true, 1>, launch_classic<false, true, true, S>}}},
+      {{{launch_classic<true, false, false, 1>, launch_classic<true, false, false, S>},
+        {launch_classic<true, false, true, 1>, launch_classic<true, false, true, S>}},
+       {{launch_classic<true, true, false, 1>, launch_classic<true, true, false, S>},
+        {launch_classic<true, true, true, 1>, launch_classic<true, true, true, S>}}}};
+  const Launch classic = kClassic[profile][alias][leaf_bound][split];
   for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, st);
   return hipGetLastError();
 }
