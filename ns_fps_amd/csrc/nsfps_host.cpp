@@ -567,7 +567,6 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.leaf_pos = bp.take<float4>(leaves);
   c.l1_key = bp.take<uint64_t>(p.l1_ub);
   c.l1_part = bp.take<uint64_t>((size_t)p.l1_ub * kUpdateSplit);
-  c.l1_cnt = bp.take<uint32_t>(p.l1_ub);
   c.l1_pos = bp.take<float4>(p.l1_ub);
   c.l1_lo = bp.take<float4>(p.l1_ub);
   c.l1_hi = bp.take<float4>(p.l1_ub);
@@ -1063,8 +1062,8 @@ uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
 constexpr uint32_t kLeafBoundMaxPoints = 262144;
 // Rounds with at most this many level-1 nodes over all clouds split each
 // node's leaves over kUpdateSplit workgroups of the update pass (its work
-// then spreads over that many more CUs; a node's key is folded by the last
-// of its workgroups to finish)
+// then spreads over that many more CUs; a node's key is
+// the largest of the parts its workgroups write)
 constexpr uint32_t kSplitMaxNodes = 128;
 
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
@@ -1079,13 +1078,14 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
   }
   const uint32_t nc = (uint32_t)plans.size();
-  const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
   const uint32_t helpers = alias ? 0u : fused_helpers(nc, max_nl1);
+  // fused rounds keep whole node keys (their helpers read and write l1_key)
+  const bool split = helpers == 0 && (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
   std::vector<std::pair<uint32_t, uint32_t>> used;
   uint32_t repairs = 0, seq = 0;
-  HIP_TRY(launch_runs_init(d_clouds, nc, st));
+  HIP_TRY(launch_runs_init(d_clouds, nc, split, st));
   // fused rounds: the first pick (row 0, the whole grid) by one update pass
   if (helpers) HIP_TRY(launch_update_pass(d_clouds, nc, max_nl1, st));
   std::vector<CloudStatus> pr(nc);

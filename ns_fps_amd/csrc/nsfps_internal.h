@@ -139,8 +139,8 @@ struct CloudDev {
   uint64_t *leaf_key;         // max key of the leaf
   float4 *leaf_pos;           // x, y, z, input row (bits) of that key
   uint64_t *l1_key;
-  uint64_t *l1_part;  // split update pass: kUpdateSplit partial keys per node
-  uint32_t *l1_cnt;   //   and each node's arrivals (zero between launches)
+  uint64_t *l1_part;  // split update pass: each node's key is the largest of its
+                      // kUpdateSplit parts (l1_key then zero; otherwise parts zero)
   float4 *l1_pos;
   const float4 *l1_lo;        // level-1 bounding boxes
   const float4 *l1_hi;

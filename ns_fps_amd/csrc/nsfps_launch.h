@@ -87,7 +87,9 @@ hipError_t launch_late_loop(const CloudDev *d_clouds, uint32_t nclouds, uint32_t
 constexpr uint32_t kProfWords = 64;
 
 // speculative-run engine
-hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st);
+// split: the rounds' update pass is split (node keys move into their parts)
+hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool split,
+                            hipStream_t st);
 // helpers == 0: rounds of update pass, refinements, gather pass and run; else
 // fused rounds of one cloud (refinements, gather pass, then the run with
 // `helpers` helper workgroups applying its picks), after one update pass

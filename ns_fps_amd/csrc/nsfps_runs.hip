@@ -118,6 +118,17 @@ __device__ __forceinline__ uint32_t in_box11(uint32_t cg, uint32_t c11, uint32_t
   return (uint32_t)(((t1 & t2 & kGuards) == kGuards) & !b1 & !b2);
 }
 
+// Level-1 node g's key: the largest of l1_key and the node's parts (in a call
+// whose update pass is split, l1_key is zero and the parts hold the largest
+// keys of the node's quarters; otherwise the parts are zero)
+__device__ __forceinline__ uint64_t node_key(const CloudDev &c, uint32_t g) {
+  const NSFPS_GLOBAL uint64_t *const pp = gptr(c.l1_part) + (size_t)g * kUpdateSplit;
+  uint64_t k = gptr(c.l1_key)[g];
+#pragma unroll
+  for (uint32_t s = 0; s < kUpdateSplit; ++s) k = pp[s] > k ? pp[s] : k;
+  return k;
+}
+
 // Cube overlapping the cell range [lo, hi] (packed corners).
 __device__ __forceinline__ bool cube_overlaps(uint2 cube, uint32_t lo, uint32_t hi) {
   bool ok = true;
@@ -318,7 +329,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t S = rs.s0;
   const uint32_t hsel = rs.hsel;
   const uint32_t gn = g < c.nl1 ? g : 0u;  // read unconditionally, used only if g < nl1
-  const uint64_t nkey = gptr(c.l1_key)[gn];
+  // split: a sibling workgroup may have written its part already; either value
+  // bounds this workgroup's points (distances only fall)
+  const uint64_t nkey = SPLIT == 1 ? gptr(c.l1_key)[gn] : node_key(c, gn);
   uint32_t clo, chi;
   uint64_t uta = 0, utb = 0, utc = 0, utd = 0;
   // the node's box of points (x > its hi x: no points)
@@ -524,24 +537,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const uint32_t wl = key_winner((uint32_t)(k >> 32), (uint32_t)k, true, mh);
     if (lane == 0) gptr(c.l1_key)[g] = ((uint64_t)mh << 32) | (uint32_t)s_lk[wl];
   } else if (wave == 0) {
-    // this part's largest key (keys are unique: the rank is their low word);
-    // the node's last workgroup to arrive folds the parts into its key and
-    // clears the count for the next launch
+    // this quarter's largest key (keys are unique: the rank is their low word)
     const uint64_t part = wave_max_u64(lane < kFan / SPLIT ? s_lk[lane] : 0ull);
-    if (lane == 0) {
-      NSFPS_GLOBAL uint64_t *const parts = gptr(c.l1_part) + (size_t)g * SPLIT;
-      NSFPS_GLOBAL uint32_t *const cnt = gptr(c.l1_cnt) + g;
-      __hip_atomic_store(parts + sub, part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == SPLIT - 1) {
-        uint64_t m = 0;
-        for (uint32_t s = 0; s < SPLIT; ++s) {
-          const uint64_t v = __hip_atomic_load(parts + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          m = v > m ? v : m;
-        }
-        gptr(c.l1_key)[g] = m;
-        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    if (lane == 0) gptr(c.l1_part)[(size_t)g * SPLIT + sub] = part;
   }
   NSFPS_GLOBAL uint32_t *H = hist_set(c, hsel);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
@@ -601,7 +599,7 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) s_hist[j] = 0;
   __syncthreads();
   for (uint32_t g = blockIdx.x; g < c.nl1; g += gridDim.x) {
-    if (gptr(c.l1_key)[g] < wlo) continue;
+    if (node_key(c, g) < wlo) continue;
     for (uint32_t k = 0; k < kLeavesPerWave; ++k) {
       const uint32_t leaf = g * kFan + wave * kLeavesPerWave + k;
       if (leaf >= c.nleaves || gptr(c.leaf_key)[leaf] < wlo) continue;
@@ -678,7 +676,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   if (s.state == 2) {
     uint64_t best = 0;
     for (uint32_t j = tid; j < c.nl1; j += kPassThreads) {
-      const uint64_t k = gptr(c.l1_key)[j];
+      const uint64_t k = node_key(c, j);
       best = k > best ? k : best;
     }
     best = wave_max_u64(best);
@@ -2250,12 +2248,18 @@ __global__ __launch_bounds__(kRunThreads) void k_round(const CloudDev *__restric
 
 // First round: the only pick is input row 0 (the first sample) with a cube
 // over the whole grid.
-__global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__restrict__ clouds) {
+__global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__restrict__ clouds,
+                                                           bool split) {
   const CloudDev &c = clouds[blockIdx.x];
   const uint32_t tid = threadIdx.x;
-  // the split update pass's arrival counts start at zero (each launch's last
-  // arrival of a node clears them again)
-  for (uint32_t i = tid; i < c.nl1; i += kPassThreads) gptr(c.l1_cnt)[i] = 0;
+  // split: each node's key moves into its first part (the other parts and
+  // l1_key zero); otherwise the parts are zero
+  for (uint32_t i = tid; i < c.nl1; i += kPassThreads) {
+    NSFPS_GLOBAL uint64_t *const pp = gptr(c.l1_part) + (size_t)i * kUpdateSplit;
+    const uint64_t k = gptr(c.l1_key)[i];
+    for (uint32_t s = 0; s < kUpdateSplit; ++s) pp[s] = split && s == 0 ? k : 0ull;
+    if (split) gptr(c.l1_key)[i] = 0;
+  }
   if (tid == 0) {
     NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
     rs.kref0 = ~0ull;
@@ -2287,8 +2291,9 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, hipStream_t st) {
-  k_runs_init<<<nclouds, kPassThreads, 0, st>>>(d_clouds);
+hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool split,
+                            hipStream_t st) {
+  k_runs_init<<<nclouds, kPassThreads, 0, st>>>(d_clouds, split);
   return hipGetLastError();
 }
 
