@@ -1062,9 +1062,13 @@ uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
 constexpr uint32_t kLeafBoundMaxPoints = 262144;
 // Rounds with at most this many level-1 nodes over all clouds split each
 // node's leaves over kUpdateSplit workgroups of the update pass (its work
-// then spreads over that many more CUs; a node's key is
-// the largest of the parts its workgroups write)
-constexpr uint32_t kSplitMaxNodes = 128;
+// then spreads over that many more CUs; a node's key is the largest of the
+// parts its workgroups write).  Measured per call: quickstart (3 nodes)
+// 0.97 -> 0.82 ms, 240,000-point scan 4.45 -> 4.21, 524,288-point clustered
+// cloud 7.45 -> 7.29 (at this bound; 7.45 at 128), 64 clouds of 16,384
+// points (256 nodes) unchanged; the 1M-point uniform cube (512 nodes) 7.7 ->
+// 12.3 with it.
+constexpr uint32_t kSplitMaxNodes = 256;
 
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
