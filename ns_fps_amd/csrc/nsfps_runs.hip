@@ -286,7 +286,11 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // ALIAS: cells share buckets, and a pick touches a leaf when its cube holds
 // any cell of the leaf's bucket (src/yuezu_fps.cpp:573-597 updates every point
 // of every bucket of the cube's cells); nodes are screened by the corners of
-// those cells.
+// those cells.  LB: a pick also takes part in a leaf only if its distance
+// bound to the leaf's box is below the leaf key's distance (the node test
+// again, per leaf).  SPLIT: the node's leaves are split over SPLIT
+// workgroups, each storing the largest key of its leaves as one of the
+// node's parts (node_key reads the node's key back as the largest part).
 template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT>
 __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
