@@ -360,3 +360,19 @@ def test_host_buffer_calls_across_a_workspace_release(lib):
                               case.expected), step
         if step == "before":
             lib.release_workspace()
+
+
+@pytest.mark.parametrize("n, blocks", [(700000, (16, 16, 16)),   # one cell per bucket
+                                       (320000, (15, 15, 15))])  # cells sharing buckets
+def test_split_update_pass_on_a_mid_size_cloud(yf, oracle, n, blocks):
+    """A cloud of 129 to 256 level-1 nodes: the update pass splits each node's
+    leaves over four workgroups (node keys kept as four parts); the samples
+    are the oracle's."""
+    rs = np.random.RandomState(31)
+    pts = rs.uniform(-1, 1, (n, 3)).astype(np.float32)
+    rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks)
+    got = yf.fps(pts, 8000, yf.make_range(*rng))
+    st = yf.last_stats()
+    nl1 = (st["n_leaves"] + 63) // 64
+    assert st["engine"] == "runs" and 128 < nl1 <= 256, nl1
+    assert np.array_equal(got, oracle.fps(pts, 8000, rng))
