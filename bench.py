@@ -372,8 +372,7 @@ def run_ball_query(lib, hip, steps, radius=0.05, nsample=32):
 # ------------------------------------------------------------ phase clocks
 
 RUN_PHASES = ["load", "select", "gather", "phases", "apply", "tail", "big", "rank", "picks",
-              "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total",
-              "help_tail", "help_tail_n", "help_step", "help_steps", "help_count"]
+              "rounds", "hot_sets", "phase_count", "walk", "publish", "rt_load", "rt_total"]
 PASS_COUNTERS = ["update_leaves", "update_points", "gather_leaves", "gather_points"]
 
 
@@ -397,7 +396,7 @@ def run_phases(lib, hip, w):
             hip.free(d_out)
     finally:
         del os.environ["NSFPS_PROFILE"]
-    v = dict(zip(RUN_PHASES, words[:21]))
+    v = dict(zip(RUN_PHASES, words[:16]))
     ctr = dict(zip(PASS_COUNTERS, words[24:28]))
     ctr.update(zip(["up_t_picks", "up_t_leaves", "up_t_flush", "up_groups"], words[32:36]))
     ctr.update(zip(["up_t_load", "up_t_zero", "up_t_hits", "up_t_points"], words[40:44]))
@@ -430,11 +429,6 @@ def run_phases(lib, hip, w):
             "cycles_per_round": {"load": round(cycles["load"] / rounds, 1),
                                  "tail": round(cycles["tail"] / rounds, 1)},
             "sample_ms": round(st["sample_ms"], 3), "device_ms": round(st["device_ms"], 3),
-            "helpers": {"tail_us_per_round": round(v["help_tail"] * 0.01 / max(1, v["help_tail_n"]), 2),
-                        "rounds_measured": v["help_tail_n"],
-                        "step_us": round(v["help_step"] * 0.01 / max(1, v["help_steps"]), 2),
-                        "steps": v["help_steps"],
-                        "first_count_us_total": round(v["help_count"] * 0.01, 1)},
             "passes": pass_counts(w["name"], ctr, rounds)}
 
 
@@ -546,6 +540,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=30.0,
                     help="seconds of reference CPU work per workload (default 30)")
     ap.add_argument("--all", action="store_true", help="also print a line per workload")
+    ap.add_argument("--no-contract", action="store_true",
+                    help="with --all: stop after the per-workload lines (profiler runs of one "
+                         "workload)")
     ap.add_argument("--only", default="",
                     help="with --all: comma-separated workloads instead of all six")
     ap.add_argument("--ball-query", action="store_true",
@@ -592,6 +589,8 @@ def main():
             line = workload_line(lib, hip, yf, wname, args.cpu_budget,
                                  with_cpu=not args.no_cpu_baseline)
             print(json.dumps(line), flush=True)
+        if args.no_contract:
+            return
 
     w = make_workload(args.workload)
     if len(w["clouds"]) != 1:

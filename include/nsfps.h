@@ -99,7 +99,8 @@ typedef struct {
   uint32_t lds_bytes;   /* dynamic LDS of the single-workgroup loop */
   uint64_t rounds;      /* speculative-run rounds (max over clouds; 0 for the tree loop) */
   uint32_t engine;      /* 1: speculative runs, 0: grid-wide steps + tree loop */
-  uint32_t repairs;     /* fused rounds whose update the host redid after a helper gave up */
+  uint32_t update_split; /* workgroups per level-1 node of the runs engine's update pass
+                           (1, or 4 when the call has few level-1 nodes) */
 } nsfps_stats;
 
 /* Library constants mirrored from src/yuezu_fps.h:19-50. */

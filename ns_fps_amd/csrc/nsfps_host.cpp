@@ -531,16 +531,6 @@ int key_bits_for(uint32_t T) {
 // slots: cell -> leaf becomes arithmetic, no table lookup per iteration.
 uint64_t padded_slot_limit(uint32_t n) { return std::max<uint64_t>(4ull * n, 65536ull); }
 
-// How long a helper of a fused round waits for the run before giving up, in
-// s_memrealtime ticks (100 MHz): NSFPS_HELP_WAIT_US microseconds, 20 ms by
-// default (a run takes well under 1 ms; only a run that never started, or
-// a test asking for it, reaches the bound).
-uint32_t help_wait_ticks() {
-  const char *e = getenv("NSFPS_HELP_WAIT_US");
-  uint64_t us = e ? strtoull(e, nullptr, 10) : 20000ull;
-  return (uint32_t)std::min<uint64_t>(us * 100ull, 0xffffffffull);
-}
-
 // Lays out the persistent buffers of one cloud (upper bounds: the padded /
 // dense decision is made on the device data during the build).
 void layout_cloud(Bump &bp, CloudPlan &p) {
@@ -575,8 +565,7 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.root_pos = bp.take<float4>(1);
   c.counter = bp.take<uint32_t>(1);
   c.prof = bp.take<uint64_t>(kProfWords);
-  c.hist = bp.take<uint32_t>((size_t)2 * kHists * kHistBins);
-  c.rec = bp.take<uint64_t>((size_t)kListCap * kRecWords);
+  c.hist = bp.take<uint32_t>((size_t)kHists * kHistBins);
   c.pick_p = bp.take<float4>(kListCap);
   c.pick_c = bp.take<uint2>(kListCap);
   c.list_p = bp.take<float4>(kListCap);
@@ -587,7 +576,6 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.n = n;
   c.m = p.m;
   c.r = p.rng.dev;
-  c.help_wait = help_wait_ticks();
 }
 
 void layout_scratch(Bump &bp, uint32_t n, uint32_t tmax, Scratch &s) {
@@ -1027,32 +1015,6 @@ struct RoundSchedule {
 };
 RoundSchedule g_schedule;
 
-// Helper workgroups of a fused round for a single cloud of nl1 level-1
-// nodes, when NSFPS_FUSED=1: one per node where they fit beside the run on
-// the device at once (up to fused_max_nodes_per_helper() nodes per helper),
-// else 0 (classic rounds).  Off by default: measured on the MI355X, a helper
-// owning several nodes steps slower than the run publishes (1M-point uniform
-// cube, 512 nodes over 255 helpers: a 20 us tail per round against the 14 us
-// update pass it replaces), a small cloud's update pass is shorter than the
-// helpers' tail (10,000 points, 3 nodes: 1.64 against 1.38 ms per call), and
-// on the 120,000-point scan (93 nodes, one helper each), where they once
-// gained 0.45 ms, the present run kernel leaves them no gain (4.52 ms per
-// call either way).  Several clouds always take classic rounds.
-uint32_t fused_helpers(uint32_t nclouds, uint32_t nl1) {
-  if (nclouds != 1) return 0;
-  const char *force = getenv("NSFPS_FUSED");
-  if (!(force && atoi(force) == 1) || getenv("NSFPS_NO_FUSED")) return 0;
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      fused_blocks_per_cu(&per_cu) != hipSuccess || per_cu < 1 || cus < 2)
-    return 0;
-  const uint32_t cap = (uint32_t)(cus * per_cu - 1);
-  const uint32_t h = std::min<uint32_t>(nl1, cap);
-  if (h == 0 || (nl1 + h - 1) / h > fused_max_nodes_per_helper()) return 0;
-  return h;
-}
-
 // Rounds whose clouds all have at most this many points use the update pass
 // that also bounds each pick by each leaf's box of points (the bound's extra
 // work pays where cubes are large against the leaves: sparse clouds).
@@ -1072,7 +1034,7 @@ constexpr uint32_t kSplitMaxNodes = 256;
 
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
-                        uint64_t *rounds_out, uint32_t *repairs_out) {
+                        uint64_t *rounds_out, uint32_t *split_out) {
   uint32_t max_nl1 = 1;
   bool alias = false;  // some cloud's cells share buckets
   bool leaf_bound = true;  // every cloud small enough for the leaf-box bound
@@ -1082,16 +1044,12 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
   }
   const uint32_t nc = (uint32_t)plans.size();
-  const uint32_t helpers = alias ? 0u : fused_helpers(nc, max_nl1);
-  // fused rounds keep whole node keys (their helpers read and write l1_key)
-  const bool split = helpers == 0 && (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
+  const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
+  *split_out = split ? kUpdateSplit : 1u;
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
   std::vector<std::pair<uint32_t, uint32_t>> used;
-  uint32_t repairs = 0, seq = 0;
   HIP_TRY(launch_runs_init(d_clouds, nc, split, st));
-  // fused rounds: the first pick (row 0, the whole grid) by one update pass
-  if (helpers) HIP_TRY(launch_update_pass(d_clouds, nc, max_nl1, st));
   std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
   uint32_t batch = 4, stalled = 0, passes = 0;
@@ -1101,7 +1059,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            split, helpers, &seq, st));
+                            split, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1111,7 +1069,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            split, helpers, &seq, st));
+                            split, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }
@@ -1119,21 +1077,6 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
                            st));
     HIP_TRY(hipStreamSynchronize(st));
-    // a helper that gave up waiting left its round's update undone, and every
-    // launch after it in the batch did nothing: redo that update (every pick
-    // of the run on every point; points already updated stay as they are)
-    // into a cleared histogram set, then go on
-    bool repaired = false;
-    for (uint32_t i = 0; i < nc; ++i) {
-      if (!pr[i].rs.hold || pr[i].done) continue;
-      const CloudDev &c = plans[i].dev;
-      HIP_TRY(launch_fill_u32(c.hist + (size_t)pr[i].rs.hsel * kHists * kHistBins, 0u,
-                              (uint64_t)kHists * kHistBins, st));
-      HIP_TRY(launch_update_pass(d_clouds + i, 1, std::max<uint32_t>(c.nl1, 1), st));
-      HIP_TRY(launch_fill_u32((char *)c.rs + offsetof(RunState, hold), 0u, 1, st));
-      repaired = true;
-      ++repairs;
-    }
     bool all = true;
     uint64_t samples = 0, rounds = 0;
     for (auto &q : pr) {
@@ -1152,7 +1095,6 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       rounds = std::max<uint64_t>(rounds, q.rs.rounds);
     }
     *rounds_out = rounds;
-    *repairs_out = repairs;
     if (all) {
       std::copy(shape, shape + 5, g_schedule.shape);
       g_schedule.batches = used;
@@ -1160,7 +1102,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       break;
     }
     // every round takes at least one sample of every unfinished cloud
-    stalled = samples == last_samples && !repaired ? stalled + 1 : 0;
+    stalled = samples == last_samples ? stalled + 1 : 0;
     if (stalled >= 2) return fail(NSFPS_EDEVICE, "internal: sampling made no progress");
     last_samples = samples;
     batch = std::min<uint32_t>(batch * 2, 64);
@@ -1237,7 +1179,7 @@ bool choose_runs(std::vector<CloudPlan> &plans) {
 // or the speculative-run rounds.
 nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
                            bool runs, uint64_t *rounds, uint64_t *wide_total,
-                           uint32_t *repairs) {
+                           uint32_t *update_split) {
   hipStream_t st = ws.st;
   std::vector<CloudDev> devs;
   uint32_t lds_bytes = 0;
@@ -1248,14 +1190,14 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
   *rounds = 0;
   *wide_total = 0;
-  *repairs = 0;
+  *update_split = 0;
   if (runs) {
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[3], st));
     HIP_TRY(hipMemcpyAsync(L.d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                            hipMemcpyHostToDevice, st));
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
     if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
-    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, repairs);
+    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, update_split);
   }
   if (plans.size() == 1) {
     uint32_t e = wide_iters_for(plans[0]);
@@ -1277,7 +1219,7 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
 // After sampling: lengths, the samples to the host (out_on_host) and the
 // statistics of the call (t0: host time at its start).
 nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
-                         bool runs, uint64_t rounds, uint64_t wide_total, uint32_t repairs,
+                         bool runs, uint64_t rounds, uint64_t wide_total, uint32_t update_split,
                          bool out_on_host,
                          int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
                          std::chrono::steady_clock::time_point t0) {
@@ -1334,7 +1276,7 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
   S.lds_bytes = runs ? 0 : lds_bytes;
   S.rounds = rounds;
   S.engine = runs ? 1u : 0u;
-  S.repairs = repairs;
+  S.update_split = update_split;
   return NSFPS_OK;
 }
 
@@ -1370,10 +1312,10 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, 
   if (rc) return rc;
   if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[1], st));
   uint64_t rounds = 0, wide_total = 0;
-  uint32_t repairs = 0;
-  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &repairs);
+  uint32_t update_split = 0;
+  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &update_split);
   if (rc) return rc;
-  return finish_call(plans, L, ws, runs, rounds, wide_total, repairs, out_on_host, h_out,
+  return finish_call(plans, L, ws, runs, rounds, wide_total, update_split, out_on_host, h_out,
                      out_stride, out_lens, t0);
 }
 
@@ -1832,10 +1774,10 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
     HIP_TRY(launch_init_state(c, p.d_small + 2, st));
     HIP_TRY(hipEventRecord(P.ev[1], st));
     uint64_t rounds = 0, wide_total = 0;
-    uint32_t repairs = 0;
-    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &repairs);
+    uint32_t update_split = 0;
+    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split);
     if (rc) return rc;
-    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, repairs, false, nullptr, 0,
+    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, false, nullptr, 0,
                        out_len, t0);
   });
 }

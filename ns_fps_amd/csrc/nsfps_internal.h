@@ -90,8 +90,6 @@ struct LdsPlan {
 struct RunState {
   uint64_t kref0;     // every key is <= kref0 when the update pass runs
   uint64_t bkey;      // list threshold chosen by the selection
-  uint64_t fin;       // fused rounds: (launch number << 32) | picks of the run, once it ended
-  uint64_t pub;       // fused rounds: (launch number << 32) | picks published so far
   uint32_t s0;        // bin shift of the update pass's key histogram
   uint32_t s0_next;   // bin shift proposed for the next round
   uint32_t npicks;    // picks of the last run (applied by the next update pass)
@@ -99,18 +97,8 @@ struct RunState {
   uint32_t rounds;    // rounds that ran (statistics)
   uint32_t err;       // set if a list overflowed (internal error)
   uint32_t forced;    // rounds whose threshold was forced for want of refinement passes
-  uint32_t hsel;      // the key histogram set the next selection reads (0 or 1)
-  uint32_t hacc;      // the set the helpers of a fused round count into
-  uint32_t hold;      // number of the fused launch whose helper gave up (0: none):
-                      // the launches after it in the batch do nothing
   uint32_t pad;
-  uint32_t pad2;
 };
-
-// Words of one published pick record of a fused round: x, y, z bits, cube lo
-// and hi corners, each with the launch's number in the upper half, so that a
-// reader knows the record is whole when all five numbers match.
-constexpr uint32_t kRecWords = 5;
 
 // Everything one cloud's kernels touch.  Device pointers; passed by value to
 // the grid-wide step and as an array to the single-workgroup loop.
@@ -155,7 +143,7 @@ struct CloudDev {
   uint64_t *prof;             // loop phase clocks / counters, or null
   // speculative-run engine
   RunState *rs;
-  uint32_t *hist;             // 2 sets of kHists x kHistBins (RunState::hsel picks one)
+  uint32_t *hist;             // kHists x kHistBins
   float4 *pick_p;             // kListCap: x, y, z, D of each pick of a run
   uint2 *pick_c;              // kListCap: cube lo / hi cells, 11 bits per axis with guard bits
                               // (lo, hi | guards: the run kernel's box-test form)
@@ -163,9 +151,6 @@ struct CloudDev {
   uint2 *list_r;              // kListCap: logical rank, input row
   uint32_t *list_c;           // kListCap: cell (10 bits per axis)
   uint32_t *list_al;          // kListCap x r.na: the cells of each entry's bucket
-  uint64_t *rec;              // kListCap x kRecWords: the run's picks as tagged records
-  uint32_t help_wait;         // fused rounds: s_memrealtime ticks a helper waits before giving up
-  uint32_t pad2;
 };
 
 // Argmax key: larger min-distance wins, equal distances go to the smaller

@@ -90,22 +90,13 @@ constexpr uint32_t kProfWords = 64;
 // split: the rounds' update pass is split (node keys move into their parts)
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool split,
                             hipStream_t st);
-// helpers == 0: rounds of update pass, refinements, gather pass and run; else
-// fused rounds of one cloud (refinements, gather pass, then the run with
-// `helpers` helper workgroups applying its picks), after one update pass
-// (launch_update_pass) for the first pick.
-// *seq counts the call's fused launches (each gets the next number).  alias:
-// some cloud's cells share buckets (classic rounds only).  leaf_bound: the
-// update pass also bounds each pick by each leaf's box; split: it takes
-// kUpdateSplit workgroups per level-1 node (both classic rounds only).
+// `rounds` rounds of update pass, refinement passes, gather pass and run.
+// alias: some cloud's cells share buckets.  leaf_bound: the update pass also
+// bounds each pick by each leaf's box; split: it takes kUpdateSplit
+// workgroups per level-1 node.
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, uint32_t helpers, uint32_t *seq,
-                         hipStream_t st);
-hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                              hipStream_t st);
-uint32_t fused_max_nodes_per_helper();
-hipError_t fused_blocks_per_cu(int *blocks);
+                         bool leaf_bound, bool split, hipStream_t st);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

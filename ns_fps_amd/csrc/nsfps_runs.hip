@@ -24,8 +24,11 @@
 // The first round's only pick is input row 0 with a cube covering the whole
 // grid: the reference's first full pass (src/yuezu_fps.cpp:431-438).
 //
-// The cube test compares cell coordinates, so the engine runs only when
-// bucket <-> cell is one-to-one.
+// The cube test compares cell coordinates.  Where cells share buckets (block
+// counts that are not powers of two: the Morton code is taken modulo the
+// block count, src/yuezu_fps.cpp:413, 592) a point is updated when the cube
+// holds any cell of its bucket, so every kernel tests each cell of a bucket
+// (the ALIAS variants).
 #include <hip/hip_runtime.h>
 
 #include "nsfps_device.h"
@@ -155,11 +158,10 @@ __device__ __forceinline__ uint32_t key_bin(uint64_t key, uint64_t kref, uint32_
   return b < kHistBins ? (uint32_t)b : kNone;
 }
 
-// The key histograms of set sel (kHists of kHistBins each): the update pass
-// (or a fused round's helpers) counts histogram 0 of a set, the refinement
-// passes histograms 1 and 2, and the selection reads the set RunState::hsel.
-__device__ __forceinline__ NSFPS_GLOBAL uint32_t *hist_set(const CloudDev &c, uint32_t sel) {
-  return gptr(c.hist) + (size_t)sel * kHists * kHistBins;
+// The key histograms (kHists of kHistBins each): the update pass counts
+// histogram 0, the refinement passes histograms 1 and 2.
+__device__ __forceinline__ NSFPS_GLOBAL uint32_t *hist_set(const CloudDev &c) {
+  return gptr(c.hist);
 }
 
 // Threshold selection, replayed identically by every workgroup that needs it.
@@ -234,7 +236,7 @@ __device__ Sel sel_replay(const CloudDev &c, uint32_t avail, uint32_t passes, ui
   s.total = 0;
   s.state = 0;
   s.pass = 0;
-  const uint32_t *H0 = c.hist + (size_t)rs.hsel * kHists * kHistBins;
+  const uint32_t *H0 = c.hist;
   Step st = h0 ? hist_step(*h0, s.cap, sc) : hist_step(H0, s.cap, sc);
   s.win = st.tot;
   for (uint32_t p = 0;; ++p) {
@@ -331,7 +333,6 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t npicks = min(rs.npicks, kListCap);
   const uint64_t kref = rs.kref0;
   const uint32_t S = rs.s0;
-  const uint32_t hsel = rs.hsel;
   const uint32_t gn = g < c.nl1 ? g : 0u;  // read unconditionally, used only if g < nl1
   // split: a sibling workgroup may have written its part already; either value
   // bounds this workgroup's points (distances only fall)
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const uint2 cb = gptr(c.l1_cbox)[gn];
     if (lane < kLPW * na && leaf0 + lane / na < c.nleaves)
       mal = gptr(c.leaf_al)[(size_t)leaf0 * na + lane];
-    pin_sgpr(done, npicks, kref, S, hsel, nkey, cb.x, cb.y, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y,
+    pin_sgpr(done, npicks, kref, S, nkey, cb.x, cb.y, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y,
              nhi.z);
     if (g >= c.nl1 || done || cb.x == kNone) return;  // finished, or no points
     if (PROF) uta = __builtin_amdgcn_s_memrealtime();
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     chi = cb.y;
   } else {
     // the run state and the node's record are read together, ahead of the exit
-    pin_sgpr(done, npicks, kref, S, hsel, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
+    pin_sgpr(done, npicks, kref, S, nkey, nlo.x, nlo.y, nlo.z, nhi.x, nhi.y, nhi.z);
     if (g >= c.nl1 || done || nlo.x > nhi.x) return;  // finished, or no points
     if (PROF) uta = __builtin_amdgcn_s_memrealtime();
     clo = pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y), cell_axis(c.r, 2, nlo.z));
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
     const uint64_t part = wave_max_u64(lane < kFan / SPLIT ? s_lk[lane] : 0ull);
     if (lane == 0) gptr(c.l1_part)[(size_t)g * SPLIT + sub] = part;
   }
-  NSFPS_GLOBAL uint32_t *H = hist_set(c, hsel);
+  NSFPS_GLOBAL uint32_t *H = hist_set(c);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
     const uint32_t v = s_hist[j];
     if (v) atomicAdd(&H[j], v);
@@ -595,7 +596,7 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ uint32_t s_sc[kPassWaves + 2];
   const CloudDev &c = clouds[blockIdx.y];
-  if (blockIdx.x >= c.nl1 || *gptr(c.done) || gptr(c.rs)->hold) return;
+  if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const Sel s = sel_replay(c, pass, passes, s_sc);
   if (s.state != 0 || s.pass != pass) return;
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(kPassThreads) void k_refine(const CloudDev *__restr
     }
   }
   __syncthreads();
-  NSFPS_GLOBAL uint32_t *H = hist_set(c, gptr(c.rs)->hsel) + pass * kHistBins;
+  NSFPS_GLOBAL uint32_t *H = hist_set(c) + pass * kHistBins;
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {
     const uint32_t v = s_hist[j];
     if (v) atomicAdd(&H[j], v);
@@ -646,10 +647,9 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
   const uint64_t gt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   // Reads that depend on nothing read before them go out together with the
-  // run state: both histogram sets' update-pass bins (the run state says
-  // which one the selection replays) and the first node chunk's leaf records.
-  const uint4 hA = gptr(reinterpret_cast<const uint4 *>(c.hist))[tid];
-  const uint4 hB = gptr(reinterpret_cast<const uint4 *>(c.hist + kHists * kHistBins))[tid];
+  // run state: the update pass's histogram bins and the first node chunk's
+  // leaf records.
+  const uint4 h0 = gptr(reinterpret_cast<const uint4 *>(c.hist))[tid];
   const auto leaf_of = [&](uint32_t c0, uint32_t &gq) {
     gq = c0 + (lane / kLeavesPerWave) * gridDim.x;
     return gq * kFan + wave * kLeavesPerWave + lane % kLeavesPerWave;
@@ -670,11 +670,10 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     }
   };
   read_leaf(blockIdx.x);
-  if (blockIdx.x >= c.nl1 || *gptr(c.done) || gptr(c.rs)->hold) return;
+  if (blockIdx.x >= c.nl1 || *gptr(c.done)) return;
   NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
   uint64_t gt1 = 0, gt2 = 0, gt3 = 0;
   bool forced = false;
-  const uint4 h0 = rs.hsel ? hB : hA;
   const Sel s = sel_replay(c, passes + 1, passes, s_sc, &forced, &h0);
   uint64_t bkey = s.bkey;
   if (s.state == 2) {
@@ -700,9 +699,6 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     uint32_t nx = bit_length(rs.kref0 - bkey + 1);
     nx = nx > 11u ? nx - 11u : 0u;
     rs.s0_next = nx < kMaxShift ? nx : kMaxShift;
-    // the histogram set a fused round's helpers count the next selection's
-    // keys into
-    rs.hacc = rs.hsel ^ 1u;
   }
   // Nodes in chunks of kGatherNodes; lane l of a wave holds leaf l % 4 of the
   // wave's four leaves of node l / 4 of the chunk, so one read brings in all
@@ -905,11 +901,6 @@ enum : uint32_t {
   kRpRtLoad = 14,  // s_memrealtime ticks (100 MHz) from the kernel's start to the end of the load
   kRpRtTotal = 15, //   and to the kernel's end
   kRpWords = 16,
-  // fused rounds (s_memrealtime ticks): how long the last helper of a launch
-  // outlived the run (measured by the next launch's run), launches measured,
-  // helper time in steps, helper steps, helper time in the first count, and
-  // the latest helper end / the run's end of the launch (absolute; scratch)
-  kHpTail = 16, kHpTailN, kHpStep, kHpSteps, kHpCount, kHpEndMax, kHpRunEnd,
   // words kept past the first kRpWords (local words 16.., profile words
   // 28.., after the work counters of the passes): the wait at the barrier
   // after the walk, the pass over entries whose bucket has several cells,
@@ -1013,32 +1004,15 @@ __device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, ui
   }
 }
 
-// A published pick record of a fused round (kRecWords words, every one with
-// the round's tag in its upper half; relaxed agent-scope stores, each word
-// single-copy atomic, so no fence orders them).
-__device__ __forceinline__ void put_record(NSFPS_GLOBAL uint64_t *r, uint32_t tag, uint4 xyz,
-                                           uint32_t lo_c, uint32_t hi_c) {
-  const uint64_t tg = (uint64_t)tag << 32;
-  __hip_atomic_store(r + 0, tg | xyz.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(r + 1, tg | xyz.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(r + 2, tg | xyz.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(r + 3, tg | lo_c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(r + 4, tg | hi_c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The run of one cloud by one workgroup of kRunThreads.  FUSED: the run of a
-// fused round, which also publishes every hot set's samples as tagged
-// records for the round's helpers, names its pick count at the end
-// (RunState::fin) and hands the histogram set the helpers counted into to
-// the next selection.  ALIAS: cells share buckets.  A sample then updates
+// The run of one cloud by one workgroup of kRunThreads.  ALIAS: cells share
+// buckets.  A sample then updates
 // every entry whose bucket has a cell inside its cube (src/yuezu_fps.cpp:
 // 573-597).  The walk finds entries by their own cell; the entries whose
 // bucket has further cells are few and listed apart, and after each walk
 // every one of them is tested against every sample of the hot set; the
 // phases test every cell of a hot copy's bucket.
-template <bool PROF, bool FUSED, bool ALIAS>
-__device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
-  static_assert(!(FUSED && ALIAS), "fused rounds need one cell per bucket");
+template <bool PROF, bool ALIAS>
+__device__ __forceinline__ void run_list(const CloudDev &c) {
   __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, pack11(cell)}
   __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
   __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
@@ -1087,22 +1061,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
   // every input of the run is read at once: the done flag, the run state and
   // the whole list buffer (entries at or beyond the list length are stale
   // and ignored)
-  // a fused launch after one whose helper gave up does nothing
-  const uint32_t held = FUSED ? rs.hold : 0u;
-  const uint32_t done_in = *gptr(c.done) | (held != 0u && held < seq ? 1u : 0u);
+  const uint32_t done_in = *gptr(c.done);
   const uint32_t nlist = min(rs.nlist, kListCap);
   const uint64_t bkey = rs.bkey, kref0 = rs.kref0;
-  const uint32_t tag = seq, hsel = rs.hsel;
-  if (PROF && FUSED && tid == 0) {
-    NSFPS_GLOBAL uint64_t *pw = gptr(c.prof);
-    const uint64_t he = pw[kHpEndMax], re = pw[kHpRunEnd];
-    if (he && re) {
-      pw[kHpTail] += he > re ? he - re : 0;
-      pw[kHpTailN] += 1;
-    }
-    pw[kHpEndMax] = 0;
-    pw[kHpRunEnd] = 0;
-  }
   float4 P[kOwnSlots];
   uint2 R[kOwnSlots];
   uint32_t C[kOwnSlots];
@@ -1669,7 +1630,6 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
             s_spos[my_out] = make_float4(__uint_as_float(rp.x), __uint_as_float(rp.y),
                                          __uint_as_float(rp.z), 0.f);
           }
-          if (FUSED) put_record(gptr(c.rec) + (size_t)(np + my_out) * kRecWords, tag, rp, lo_c, hi_c);
         }
         const uint32_t x0 = (lo_c & 1023u) >> gsx, x1 = (hi_c & 1023u) >> gsx;
         const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
@@ -1777,9 +1737,6 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
       NSFPS_RMARK(kRpWalk);
       __syncthreads();  // the walks' updates are in LDS
       NSFPS_RMARK(kRpWalkWait);
-      if (FUSED && tid == 0)  // the hot set's records are written (or on their way)
-        __hip_atomic_store(&rs.pub, ((uint64_t)tag << 32) | (np + npk), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
       if (ALIAS) {
         // the entries whose other cells did not fit the second index (the
         // walk reached them by their own cell alone), against every sample
@@ -1891,15 +1848,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     rs.nlist = 0;
     rs.rounds += 1;
     if (done) *gptr(c.done) = 1;
-    if (FUSED) {
-      rs.hsel = hsel ^ 1u;  // the set this round's helpers count into
-      __hip_atomic_store(&rs.fin, ((uint64_t)tag << 32) | np, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
   }
-  // the set this round's selection read is cleared for the round after next
-  // (16-byte stores: six a thread)
-  NSFPS_GLOBAL uint4 *const hz = reinterpret_cast<NSFPS_GLOBAL uint4 *>(hist_set(c, hsel));
+  // the histograms this round's selection read are cleared for the next
+  // round's update pass (16-byte stores: three a thread)
+  NSFPS_GLOBAL uint4 *const hz = reinterpret_cast<NSFPS_GLOBAL uint4 *>(hist_set(c));
   for (uint32_t j = tid; j < kHists * kHistBins / 4; j += kRunThreads) hz[j] = make_uint4(0u, 0u, 0u, 0u);
   if (PROF && tid == 0) {
     NSFPS_RMARK(kRpTail);
@@ -1909,344 +1861,15 @@ __device__ __forceinline__ void run_list(const CloudDev &c, uint32_t seq) {
     NSFPS_GLOBAL uint64_t *pw = gptr(c.prof);
     for (uint32_t i = 0; i < kRpWords; ++i) pw[i] += pf[i];
     for (uint32_t i = kRpWords; i < kRpLocal; ++i) pw[kRpExtraAt + i - kRpWords] += pf[i];
-    if (FUSED) pw[kHpRunEnd] = __builtin_amdgcn_s_memrealtime();
   }
 #undef NSFPS_RMARK
 }
 
 template <bool PROF, bool ALIAS>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  run_list<PROF, false, ALIAS>(clouds[blockIdx.x], 0u);
+  run_list<PROF, ALIAS>(clouds[blockIdx.x]);
 }
 
-
-// ------------------------------------------------------------ fused rounds
-//
-// One launch per round carries the run (workgroup 0) and helpers (workgroups
-// 1 .. H) that apply the run's picks to the points while the run goes on:
-// the work of the update pass, off the run's critical path.  Helper h owns
-// the level-1 nodes h, h + H, h + 2H, ...  The run publishes each hot set's
-// samples as tagged records (put_record); a helper reads every record that
-// is whole, applies those picks to its nodes exactly as the update pass
-// would (every point of every leaf whose cell lies in a pick's cube, the
-// leaf and level-1 keys after it), and keeps the next selection's key
-// histogram of its points current in LDS: it counts their keys inside the
-// window before the first pick, and a lowered point then leaves its old bin
-// and enters its new one.  A helper reads records up to the count the run
-// publishes after each hot set (RunState::pub); when the run has named its
-// final count (RunState::fin) and every pick is applied, it adds its
-// histogram to set RunState::hacc.  The end of the launch is the only
-// barrier.  The run never
-// waits for a helper.  A helper waits for the run at most help_wait ticks of
-// s_memrealtime in all; past that it sets RunState::hold and leaves between
-// two steps (its nodes consistent, its histogram not added): the launches
-// after it in the batch do nothing, and the host redoes the round's update
-// pass before going on.
-
-constexpr uint32_t kMaxHelpNodes = 16;                // level-1 nodes one helper owns at most
-constexpr uint32_t kHelpLeaves = kMaxHelpNodes * kFan;
-constexpr uint32_t kHelpLPW = kFan / kRunWaves;       // leaves of a node per wave
-constexpr uint32_t kHelpChunk = 1;                    // nodes whose points are read together
-static_assert(kHelpLPW * kRunWaves == kFan, "one node's leaves over the workgroup's waves");
-static_assert(kRunThreads <= 65536, "pick indices of a step fit 16 bits");
-
-// Record r of this round: true when every word carries tag.
-__device__ __forceinline__ bool get_record(const uint64_t *r, uint32_t tag, float4 &p, uint2 &cube) {
-  uint64_t w[kRecWords];
-  NSFPS_GLOBAL uint64_t *g = (NSFPS_GLOBAL uint64_t *)gptr(r);
-#pragma unroll
-  for (uint32_t k = 0; k < kRecWords; ++k)
-    w[k] = __hip_atomic_load(g + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  bool ok = true;
-#pragma unroll
-  for (uint32_t k = 0; k < kRecWords; ++k) ok &= (uint32_t)(w[k] >> 32) == tag;
-  p = make_float4(__uint_as_float((uint32_t)w[0]), __uint_as_float((uint32_t)w[1]),
-                  __uint_as_float((uint32_t)w[2]), 0.f);
-  cube = make_uint2((uint32_t)w[3], (uint32_t)w[4]);
-  return ok;
-}
-
-template <bool PROF>
-__device__ __forceinline__ void help_list(const CloudDev &c, uint32_t h, uint32_t H, uint32_t seq) {
-  __shared__ uint32_t s_hh[kHistBins];           // my points' keys in the next window
-  __shared__ uint64_t s_lk[kHelpLeaves];         // my leaves: keys,
-  __shared__ uint32_t s_lc[kHelpLeaves];         //   cells,
-  __shared__ uint2 s_ls[kHelpLeaves];            //   first slot and point count
-  __shared__ uint2 s_nb[kMaxHelpNodes];          // my nodes' cell ranges; x = kNone: no points
-  __shared__ uint16_t s_sel[kMaxHelpNodes][kRunThreads];  // picks of the step touching each node
-  __shared__ uint32_t s_nsel[kMaxHelpNodes];
-  __shared__ float4 s_bp[kRunThreads];           // the step's picks
-  __shared__ uint2 s_bc[kRunThreads];            //   and their cubes
-  __shared__ uint32_t s_ctl[3];                  // wait outcome, picks of the step, changed nodes
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  NSFPS_GLOBAL RunState &rs = *gptr(c.rs);
-  const uint32_t held = rs.hold;
-  const uint32_t stop_in = *gptr(c.done) | (held != 0u && held < seq ? 1u : 0u);
-  const uint32_t tag = seq, hacc = rs.hacc, S = rs.s0_next;
-  const uint64_t kref = rs.bkey - 1;  // every key is below the list threshold after the run
-  const uint32_t nmine = c.nl1 > h ? (c.nl1 - h + H - 1) / H : 0u;
-  if (stop_in || nmine == 0) return;
-  if (nmine > kMaxHelpNodes) {  // cannot happen: the host sizes the helpers
-    if (tid == 0) rs.err = 5;
-    return;
-  }
-  const uint64_t wlo = window_lo(kref, S);
-  const uint32_t nlv = nmine * kFan;
-  const NSFPS_GLOBAL float4 *const P4 = gptr(c.P4);
-  const NSFPS_GLOBAL uint32_t *const R = gptr(c.R);
-  for (uint32_t j = tid; j < kHistBins; j += kRunThreads) s_hh[j] = 0;
-  for (uint32_t i = tid; i < nlv; i += kRunThreads) {
-    const uint32_t leaf = (h + (i / kFan) * H) * kFan + i % kFan;
-    uint64_t k = 0;
-    uint32_t cl = 0;
-    uint2 ls = make_uint2(0u, 0u);
-    if (leaf < c.nleaves) {
-      k = gptr(c.leaf_key)[leaf];
-      cl = gptr(c.leaf_cell)[leaf];
-      ls = gptr(c.leaf_sc)[leaf];
-    }
-    s_lk[i] = k;
-    s_lc[i] = cl;
-    s_ls[i] = ls;
-  }
-  if (tid < nmine) {
-    const uint32_t g = h + tid * H;
-    const float4 nlo = gptr(c.l1_lo)[g], nhi = gptr(c.l1_hi)[g];
-    s_nb[tid] = nlo.x > nhi.x
-                    ? make_uint2(kNone, 0u)
-                    : make_uint2(pack_cell(cell_axis(c.r, 0, nlo.x), cell_axis(c.r, 1, nlo.y),
-                                           cell_axis(c.r, 2, nlo.z)),
-                                 pack_cell(cell_axis(c.r, 0, nhi.x), cell_axis(c.r, 1, nhi.y),
-                                           cell_axis(c.r, 2, nhi.z)));
-  }
-  if (tid < kMaxHelpNodes) s_nsel[tid] = 0;
-  if (tid == 0) s_ctl[2] = 0;
-  __syncthreads();
-  const uint64_t tc0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
-  uint64_t tstep = 0, nsteps = 0;
-  // the keys of my points inside the window, before any pick of the run
-  for (uint32_t lb = wave * kHelpLPW; lb < nlv; lb += kFan) {
-    float4 p[kHelpLPW];
-    uint32_t rk[kHelpLPW];
-#pragma unroll
-    for (uint32_t k = 0; k < kHelpLPW; ++k) {
-      const uint2 ls = s_ls[lb + k];
-      p[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      rk[k] = 0;
-      if (s_lk[lb + k] >= wlo && lane < ls.y) {
-        p[k] = P4[ls.x + lane];
-        rk[k] = R[ls.x + lane];
-      }
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < kHelpLPW; ++k) {
-      const uint2 ls = s_ls[lb + k];
-      if (s_lk[lb + k] >= wlo && lane < ls.y) {
-        const uint32_t b = key_bin(((uint64_t)__float_as_uint(p[k].w) << 32) | ~rk[k], kref, S);
-        if (b != kNone) atomicAdd(&s_hh[b], 1u);
-      }
-    }
-  }
-  uint32_t applied = 0;
-  bool stalled = false;  // the last step found no whole record
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  const uint64_t tcount = PROF ? t0 - tc0 : 0;
-  while (true) {
-    if (tid == 0) {
-      // wait for published picks beyond `applied`, or for the run's end with
-      // every pick applied (after a step that found no whole record, first
-      // a pause and a look at the clock)
-      uint32_t outcome, avail = applied;
-      bool pause = stalled;
-      while (true) {
-        if (pause) {
-          if (__builtin_amdgcn_s_memrealtime() - t0 > c.help_wait) {
-            outcome = 3;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-        pause = true;
-        const uint64_t f = __hip_atomic_load(&rs.fin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((uint32_t)(f >> 32) == tag && (uint32_t)f <= applied) {
-          outcome = 2;
-          break;
-        }
-        const uint64_t pb = __hip_atomic_load(&rs.pub, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((uint32_t)(pb >> 32) == tag && (uint32_t)pb > applied) {
-          outcome = 1;
-          avail = min((uint32_t)pb, kListCap);
-          break;
-        }
-      }
-      s_ctl[0] = outcome;
-      s_ctl[1] = min(avail - applied, kRunThreads);
-    }
-    __syncthreads();
-    const uint32_t outcome = s_ctl[0];
-    if (outcome == 2) break;
-    if (outcome == 3) {  // the run did not come: the host redoes this round's update
-      if (tid == 0) atomicExch(&rs.hold, seq);
-      return;
-    }
-    const uint64_t ts = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
-    // the step's picks: the published records from `applied` on, up to the
-    // first one not yet whole (a record may trail the count that names it)
-    const uint32_t navail = s_ctl[1];
-    float4 bp;
-    uint2 bc;
-    const bool ok = tid < navail &&
-                    get_record(c.rec + (size_t)(applied + tid) * kRecWords, tag, bp, bc);
-    const uint64_t bad = __ballot(!ok);
-    __syncthreads();  // every thread has read navail
-    if (bad && lane == (uint32_t)__ffsll((long long)bad) - 1) atomicMin(&s_ctl[1], tid);
-    __syncthreads();
-    const uint32_t nb = s_ctl[1];
-    if (tid < nb) {
-      s_bp[tid] = bp;
-      s_bc[tid] = bc;
-      for (uint32_t k = 0; k < nmine; ++k) {
-        const uint2 nb2 = s_nb[k];
-        if (nb2.x != kNone && cube_overlaps(bc, nb2.x, nb2.y))
-          s_sel[k][atomicAdd(&s_nsel[k], 1u)] = (uint16_t)tid;
-      }
-    }
-    __syncthreads();
-    // the leaves of the nodes with picks, kHelpChunk nodes at a time (their
-    // points read before any is processed): wave w takes leaves 8w .. 8w + 7
-    // of each node
-    for (uint32_t k0 = 0; k0 < nmine; k0 += kHelpChunk) {
-      uint32_t cell[kHelpChunk][kHelpLPW], st[kHelpChunk][kHelpLPW], cnt[kHelpChunk][kHelpLPW];
-      uint64_t okey[kHelpChunk][kHelpLPW], hm[kHelpChunk][kHelpLPW];
-      bool hit[kHelpChunk][kHelpLPW];
-      uint32_t nsel[kHelpChunk];
-#pragma unroll
-      for (uint32_t kk = 0; kk < kHelpChunk; ++kk) {
-        const uint32_t k = k0 + kk;
-        nsel[kk] = k < nmine ? s_nsel[k] : 0u;
-        const uint32_t lb = k * kFan + wave * kHelpLPW;
-#pragma unroll
-        for (uint32_t j = 0; j < kHelpLPW; ++j) {
-          hit[kk][j] = false;
-          hm[kk][j] = 0;
-          cell[kk][j] = st[kk][j] = cnt[kk][j] = 0;
-          okey[kk][j] = 0;
-          if (nsel[kk] == 0) continue;
-          cell[kk][j] = s_lc[lb + j];
-          const uint2 ls = s_ls[lb + j];
-          st[kk][j] = ls.x;
-          cnt[kk][j] = ls.y;
-          okey[kk][j] = s_lk[lb + j];
-          hm[kk][j] = __ballot(lane < nsel[kk] && cell_in(cell[kk][j], s_bc[s_sel[k][lane]]));
-          bool hh = hm[kk][j] != 0;
-          for (uint32_t cb = 64; cb < nsel[kk] && !hh; cb += 64)
-            hh = __ballot(cb + lane < nsel[kk] && cell_in(cell[kk][j], s_bc[s_sel[k][cb + lane]])) != 0;
-          hit[kk][j] = hh && cnt[kk][j] > 0;
-        }
-      }
-      float4 p[kHelpChunk][kHelpLPW];
-      uint32_t rr[kHelpChunk][kHelpLPW];  // logical ranks
-#pragma unroll
-      for (uint32_t kk = 0; kk < kHelpChunk; ++kk)
-#pragma unroll
-        for (uint32_t j = 0; j < kHelpLPW; ++j) {
-          p[kk][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-          rr[kk][j] = 0;
-          if (hit[kk][j] && lane < cnt[kk][j]) {
-            p[kk][j] = P4[st[kk][j] + lane];
-            rr[kk][j] = R[st[kk][j] + lane];
-          }
-        }
-#pragma unroll
-      for (uint32_t kk = 0; kk < kHelpChunk; ++kk) {
-        const uint32_t k = k0 + kk;
-        if (nsel[kk] == 0) continue;
-        const uint32_t lb = k * kFan + wave * kHelpLPW;
-        const uint32_t leaf0 = (h + k * H) * kFan + wave * kHelpLPW;
-        bool changed = false;
-#pragma unroll
-        for (uint32_t j = 0; j < kHelpLPW; ++j) {
-          if (!hit[kk][j]) continue;
-          const bool act = lane < cnt[kk][j];
-          const uint32_t lo = ~rr[kk][j];
-          float d = p[kk][j].w;
-          for (uint32_t cb = 0; cb < nsel[kk]; cb += 64) {
-            uint64_t m = cb == 0 ? hm[kk][j]
-                                 : __ballot(cb + lane < nsel[kk] &&
-                                            cell_in(cell[kk][j], s_bc[s_sel[k][cb + lane]]));
-            while (m) {
-              const uint32_t u = (uint32_t)__ffsll((long long)m) - 1;
-              m &= m - 1;
-              const float4 q = s_bp[s_sel[k][cb + u]];
-              const float dd = sqdist(p[kk][j].x, p[kk][j].y, p[kk][j].z, q.x, q.y, q.z);
-              d = dd < d ? dd : d;
-            }
-          }
-          const bool lowered = act && d < p[kk][j].w;
-          if (lowered) {
-            ((NSFPS_GLOBAL float *)gptr(c.P4 + st[kk][j] + lane))[3] = d;
-            const uint32_t bo = key_bin(((uint64_t)__float_as_uint(p[kk][j].w) << 32) | lo, kref, S);
-            const uint32_t bn = key_bin(((uint64_t)__float_as_uint(d) << 32) | lo, kref, S);
-            if (bo != kNone) atomicSub(&s_hh[bo], 1u);
-            if (bn != kNone) atomicAdd(&s_hh[bn], 1u);
-          }
-          if (__ballot(lowered && lo == (uint32_t)okey[kk][j])) {  // the point holding the key
-            const uint32_t hi = act ? __float_as_uint(d) : 0u;
-            uint32_t mh;
-            const uint32_t wl = key_winner(hi, lo, act, mh);
-            const uint64_t key = ((uint64_t)mh << 32) | rdlane(lo, wl);
-            if (lane == 0) {
-              s_lk[lb + j] = key;
-              gptr(c.leaf_key)[leaf0 + j] = key;
-            }
-            changed = true;
-          }
-        }
-        if (changed && lane == 0) atomicOr(&s_ctl[2], 1u << k);
-      }
-    }
-    __syncthreads();
-    // level-1 keys of the nodes whose leaf keys changed
-    const uint32_t chg = s_ctl[2];
-    for (uint32_t k = wave; k < nmine; k += kRunWaves) {
-      if (!((chg >> k) & 1u)) continue;
-      const uint64_t kk = s_lk[k * kFan + lane];
-      uint32_t mh;
-      const uint32_t wl = key_winner((uint32_t)(kk >> 32), (uint32_t)kk, true, mh);
-      if (lane == 0) gptr(c.l1_key)[h + k * H] = ((uint64_t)mh << 32) | (uint32_t)s_lk[k * kFan + wl];
-    }
-    applied += nb;
-    stalled = nb == 0;
-    __syncthreads();
-    if (tid < kMaxHelpNodes) s_nsel[tid] = 0;
-    if (tid == 0) s_ctl[2] = 0;
-    if (PROF) {
-      tstep += __builtin_amdgcn_s_memrealtime() - ts;
-      nsteps += 1;
-    }
-  }
-  NSFPS_GLOBAL uint32_t *const Hs = hist_set(c, hacc);
-  for (uint32_t j = tid; j < kHistBins; j += kRunThreads) {
-    const uint32_t v = s_hh[j];
-    if (v) atomicAdd(&Hs[j], v);
-  }
-  if (PROF && tid == 0) {
-    NSFPS_GLOBAL unsigned long long *pw = (NSFPS_GLOBAL unsigned long long *)gptr(c.prof);
-    atomicAdd(&pw[kHpStep], (unsigned long long)tstep);
-    atomicAdd(&pw[kHpSteps], (unsigned long long)nsteps);
-    atomicAdd(&pw[kHpCount], (unsigned long long)tcount);
-    atomicMax(&pw[kHpEndMax], (unsigned long long)__builtin_amdgcn_s_memrealtime());
-  }
-}
-
-// seq: the launch's number among the call's fused launches (1, 2, ...): the
-// tag of its records, and what RunState::hold compares with.
-template <bool PROF>
-__global__ __launch_bounds__(kRunThreads) void k_round(const CloudDev *__restrict__ clouds,
-                                                       uint32_t seq) {
-  if (blockIdx.x == 0) run_list<PROF, true, false>(clouds[0], seq);
-  else help_list<PROF>(clouds[0], blockIdx.x - 1, gridDim.x - 1, seq);
-}
 
 // ------------------------------------------------------------------ setup
 
@@ -2275,11 +1898,6 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
     rs.rounds = 0;
     rs.err = 0;
     rs.forced = 0;
-    rs.fin = 0;
-    rs.pub = 0;
-    rs.hsel = 0;
-    rs.hacc = 1;
-    rs.hold = 0;
     const float4 p0 = *gptr(c.root_pos);
     gptr(c.pick_p)[0] = make_float4(p0.x, p0.y, p0.z, INFINITY);
     gptr(c.pick_c)[0] = make_uint2(
@@ -2288,9 +1906,7 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
     *gptr(c.iter) = 1;
     *gptr(c.done) = c.m <= 1 ? 1u : 0u;
   }
-  for (uint32_t j = tid; j < 2 * kHists * kHistBins; j += kPassThreads) gptr(c.hist)[j] = 0;
-  // no record of an earlier call may pass for one of this call's rounds
-  for (uint32_t j = tid; j < kListCap * kRecWords; j += kPassThreads) gptr(c.rec)[j] = 0;
+  for (uint32_t j = tid; j < kHists * kHistBins; j += kPassThreads) gptr(c.hist)[j] = 0;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -2299,24 +1915,6 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
                             hipStream_t st) {
   k_runs_init<<<nclouds, kPassThreads, 0, st>>>(d_clouds, split);
   return hipGetLastError();
-}
-
-hipError_t launch_update_pass(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
-                              hipStream_t st) {
-  k_update<false, false, false, 1><<<dim3(max_nl1, nclouds), kPassThreads, 0, st>>>(d_clouds);
-  return hipGetLastError();
-}
-
-uint32_t fused_max_nodes_per_helper() { return kMaxHelpNodes; }
-
-hipError_t fused_blocks_per_cu(int *blocks) {
-  int a = 0, b = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_round<false>, kRunThreads, 0);
-  if (e != hipSuccess) return e;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_round<true>, kRunThreads, 0);
-  if (e != hipSuccess) return e;
-  *blocks = a < b ? a : b;
-  return hipSuccess;
 }
 
 // The classic round's update, gather and run kernels of one variant.
@@ -2332,27 +1930,9 @@ void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, uint32_t helpers, uint32_t *seq,
-                         hipStream_t st) {
+                         bool leaf_bound, bool split, hipStream_t st) {
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
-  if (helpers) {  // fused rounds of one cloud (one cell per bucket)
-    if (alias) return hipErrorInvalidValue;
-    for (uint32_t r = 0; r < rounds; ++r) {
-      for (uint32_t p = 1; p <= passes; ++p)
-        k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
-      if (profile)
-        k_gather<true, false><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
-      else
-        k_gather<false, false><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
-      const uint32_t q = ++*seq;
-      if (profile)
-        k_round<true><<<1 + helpers, kRunThreads, 0, st>>>(d_clouds, q);
-      else
-        k_round<false><<<1 + helpers, kRunThreads, 0, st>>>(d_clouds, q);
-    }
-    return hipGetLastError();
-  }
   using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, hipStream_t);
   constexpr uint32_t S = kUpdateSplit;
   static constexpr Launch kClassic[2][2][2][2] = {  // [profile][alias][leaf_bound][split]

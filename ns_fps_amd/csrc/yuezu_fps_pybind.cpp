@@ -284,7 +284,7 @@ py::dict last_stats_py() {
   d["samples"] = s.samples;
   d["rounds"] = s.rounds;
   d["engine"] = s.engine ? "runs" : "tree";
-  d["repairs"] = s.repairs;
+  d["update_split"] = s.update_split;
   return d;
 }
 
