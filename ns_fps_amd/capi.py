@@ -39,7 +39,8 @@ class Stats(ctypes.Structure):
                 ("wide_iters", ctypes.c_uint64), ("samples", ctypes.c_uint64),
                 ("padded", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32),
                 ("rounds", ctypes.c_uint64), ("engine", ctypes.c_uint32),
-                ("update_split", ctypes.c_uint32)]
+                ("update_split", ctypes.c_uint32),
+                ("mixed", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

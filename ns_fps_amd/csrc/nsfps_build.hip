@@ -369,6 +369,31 @@ __device__ __forceinline__ void leaf_desc_at(uint32_t b, const uint32_t *__restr
   }
 }
 
+// Mixed leaves (runs engine, one cell per bucket): leaf l holds the slots
+// 64 l .. 64 l + 63 of the logical order, whichever buckets they belong to.
+__device__ __forceinline__ void leaf_desc_mixed_at(uint32_t l, uint32_t n, uint32_t nleaves,
+                                                   float4 *__restrict__ leaf_lo,
+                                                   float4 *__restrict__ leaf_hi,
+                                                   uint32_t *__restrict__ leaf_cell,
+                                                   uint32_t *__restrict__ leaf_al,
+                                                   uint2 *__restrict__ leaf_sc) {
+  if (l >= nleaves) return;
+  const uint32_t first = l * kLeaf;
+  const uint32_t cnt = n - first < kLeaf ? n - first : kLeaf;
+  leaf_lo[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(first));
+  leaf_hi[l] = make_float4(0.f, 0.f, 0.f, __uint_as_float(cnt));
+  leaf_sc[l] = make_uint2(first, cnt);
+  leaf_cell[l] = 0;      // a leaf of several cells: its cell box is leaf_cbox
+  leaf_al[l] = kNoCell;  // one cell per bucket (r.na == 1)
+}
+
+__global__ void k_leaf_desc_mixed(uint32_t n, uint32_t nleaves, float4 *__restrict__ leaf_lo,
+                                  float4 *__restrict__ leaf_hi, uint32_t *__restrict__ leaf_cell,
+                                  uint32_t *__restrict__ leaf_al, uint2 *__restrict__ leaf_sc) {
+  leaf_desc_mixed_at(blockIdx.x * blockDim.x + threadIdx.x, n, nleaves, leaf_lo, leaf_hi, leaf_cell,
+                     leaf_al, leaf_sc);
+}
+
 __global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
                             const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
                             uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
@@ -379,13 +404,16 @@ __global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
                r, P4, leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
 }
 
-// Leaf bounding boxes and initial keys (FLT_MAX with the smallest rank of the
-// leaf); empty leaves get an empty box and key 0.  One wave per leaf.
-__device__ __forceinline__ void leaf_bbox_at(uint32_t leaf, uint32_t nleaves,
+// Leaf bounding boxes, the corners of their points' cells, and initial keys
+// (FLT_MAX with the smallest rank of the leaf); empty leaves get an empty box
+// (its cell corners lo > hi) and key 0.  One wave per leaf.  cell_axis is
+// monotone, so the cells of the box's corners bound every point's cell.
+__device__ __forceinline__ void leaf_bbox_at(uint32_t leaf, uint32_t nleaves, const RangeDev &r,
                                              const float4 *__restrict__ P4,
                                              const uint2 *__restrict__ RO,
                                              float4 *__restrict__ leaf_lo,
                                              float4 *__restrict__ leaf_hi,
+                                             uint2 *__restrict__ leaf_cbox,
                                              uint64_t *__restrict__ leaf_key,
                                              float4 *__restrict__ leaf_pos) {
   uint32_t lane = lane_id();
@@ -416,6 +444,9 @@ __device__ __forceinline__ void leaf_bbox_at(uint32_t leaf, uint32_t nleaves,
   if (lane == 0) {
     leaf_lo[leaf] = make_float4(mnx, mny, mnz, lo.w);
     leaf_hi[leaf] = make_float4(mxx, mxy, mxz, hi.w);
+    leaf_cbox[leaf] =
+        make_uint2(cell_axis(r, 0, mnx) | (cell_axis(r, 1, mny) << 10) | (cell_axis(r, 2, mnz) << 20),
+                   cell_axis(r, 0, mxx) | (cell_axis(r, 1, mxy) << 10) | (cell_axis(r, 2, mxz) << 20));
     leaf_key[leaf] = km;
   }
   if (cnt == 0) {
@@ -425,14 +456,16 @@ __device__ __forceinline__ void leaf_bbox_at(uint32_t leaf, uint32_t nleaves,
   }
 }
 
-__global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, const float4 *__restrict__ P4,
+__global__ __launch_bounds__(256) void k_leaf_bbox(uint32_t nleaves, RangeDev r,
+                                                   const float4 *__restrict__ P4,
                                                    const uint2 *__restrict__ RO,
                                                    float4 *__restrict__ leaf_lo,
                                                    float4 *__restrict__ leaf_hi,
+                                                   uint2 *__restrict__ leaf_cbox,
                                                    uint64_t *__restrict__ leaf_key,
                                                    float4 *__restrict__ leaf_pos) {
-  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
-               leaf_pos);
+  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, r, P4, RO, leaf_lo, leaf_hi, leaf_cbox,
+               leaf_key, leaf_pos);
 }
 
 // Level-1 nodes from the initial leaves: max key, its position, the union
@@ -639,16 +672,23 @@ hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t 
 }
 
 hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
-                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
-                             const RangeDev &r, const float4 *P4, const uint2 *RO,
-                             float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
-                             uint32_t *leaf_al, uint2 *leaf_sc, uint64_t *leaf_key,
-                             float4 *leaf_pos, hipStream_t st) {
-  k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
-                                            leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
+                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t mixed,
+                             uint32_t n, uint32_t nleaves, const RangeDev &r, const float4 *P4,
+                             const uint2 *RO, float4 *leaf_lo, float4 *leaf_hi,
+                             uint32_t *leaf_cell, uint32_t *leaf_al, uint2 *leaf_sc,
+                             uint2 *leaf_cbox, uint64_t *leaf_key, float4 *leaf_pos,
+                             hipStream_t st) {
+  if (mixed) {
+    if (nleaves)
+      k_leaf_desc_mixed<<<cdiv(nleaves, 256), 256, 0, st>>>(n, nleaves, leaf_lo, leaf_hi, leaf_cell,
+                                                            leaf_al, leaf_sc);
+  } else {
+    k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
+                                              leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
+  }
   if (nleaves)
-    k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, P4, RO, leaf_lo, leaf_hi, leaf_key,
-                                                  leaf_pos);
+    k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, r, P4, RO, leaf_lo, leaf_hi, leaf_cbox,
+                                                  leaf_key, leaf_pos);
   return hipGetLastError();
 }
 
@@ -701,21 +741,28 @@ __global__ void kb_gather(const BuildDev *__restrict__ bd) {
             const_cast<uint32_t *>(b.c.R), b.small + 2);
 }
 
+// thread i: cell i's table entry, and the leaves of bucket i (or, with mixed
+// leaves, leaf i)
 __global__ void kb_cells(const BuildDev *__restrict__ bd) {
   const BuildDev &b = bd[blockIdx.y];
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   cell_info_at(i, b.counts, b.lc, b.T, const_cast<uint2 *>(b.c.cell_info));
-  leaf_desc_at(i, b.counts, b.lc, b.T, b.c.padded, b.cap, b.c.lpc, b.c.r, b.c.P4,
-               const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
-               const_cast<uint32_t *>(b.c.leaf_cell), const_cast<uint32_t *>(b.c.leaf_al),
-               const_cast<uint2 *>(b.c.leaf_sc));
+  if (b.c.mixed)
+    leaf_desc_mixed_at(i, b.n, b.c.nleaves, const_cast<float4 *>(b.c.leaf_lo),
+                       const_cast<float4 *>(b.c.leaf_hi), const_cast<uint32_t *>(b.c.leaf_cell),
+                       const_cast<uint32_t *>(b.c.leaf_al), const_cast<uint2 *>(b.c.leaf_sc));
+  else
+    leaf_desc_at(i, b.counts, b.lc, b.T, b.c.padded, b.cap, b.c.lpc, b.c.r, b.c.P4,
+                 const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
+                 const_cast<uint32_t *>(b.c.leaf_cell), const_cast<uint32_t *>(b.c.leaf_al),
+                 const_cast<uint2 *>(b.c.leaf_sc));
 }
 
 __global__ __launch_bounds__(256) void kb_leaf_bbox(const BuildDev *__restrict__ bd) {
   const BuildDev &b = bd[blockIdx.y];
-  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), b.c.nleaves, b.c.P4, b.c.RO,
+  leaf_bbox_at(blockIdx.x * 4 + (threadIdx.x >> 6), b.c.nleaves, b.c.r, b.c.P4, b.c.RO,
                const_cast<float4 *>(b.c.leaf_lo), const_cast<float4 *>(b.c.leaf_hi),
-               b.c.leaf_key, b.c.leaf_pos);
+               const_cast<uint2 *>(b.c.leaf_cbox), b.c.leaf_key, b.c.leaf_pos);
 }
 
 __global__ __launch_bounds__(256) void kb_l1_init(const BuildDev *__restrict__ bd) {
@@ -745,7 +792,8 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
                                   uint32_t l1_max, hipStream_t st) {
   if (slots_max) kb_zero_slots<<<dim3(cdiv(slots_max, 256), nclouds), 256, 0, st>>>(d_bd);
   if (nmax) kb_gather<<<dim3(cdiv(nmax, 256), nclouds), 256, 0, st>>>(d_bd);
-  kb_cells<<<dim3(cdiv((uint64_t)tmax + 1, 256), nclouds), 256, 0, st>>>(d_bd);
+  const uint64_t cells_or_leaves = (uint64_t)tmax + 1 > leaves_max ? (uint64_t)tmax + 1 : leaves_max;
+  kb_cells<<<dim3(cdiv(cells_or_leaves, 256), nclouds), 256, 0, st>>>(d_bd);
   if (leaves_max) kb_leaf_bbox<<<dim3(cdiv(leaves_max, 4), nclouds), 256, 0, st>>>(d_bd);
   if (l1_max) kb_l1_init<<<dim3(cdiv(l1_max, 4), nclouds), 256, 0, st>>>(d_bd);
   kb_init_state<<<nclouds, 64, 0, st>>>(d_bd);

@@ -553,6 +553,7 @@ void layout_cloud(Bump &bp, CloudPlan &p) {
   c.leaf_sc = bp.take<uint2>(leaves);
   c.leaf_cell = bp.take<uint32_t>(leaves);
   c.leaf_al = bp.take<uint32_t>(leaves * p.rng.dev.na);
+  c.leaf_cbox = bp.take<uint2>(leaves);
   c.leaf_key = bp.take<uint64_t>(leaves);
   c.leaf_pos = bp.take<float4>(leaves);
   c.l1_key = bp.take<uint64_t>(p.l1_ub);
@@ -734,20 +735,61 @@ nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &
   return NSFPS_OK;
 }
 
-nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs) {
+// Leaves of the per-bucket layouts (a leaf holds points of one bucket):
+// padded (slot = bucket * cap + j) when that stays within the slot limit,
+// else dense.  hs: the words read back after the first build phase.
+uint64_t bucket_leaves(const CloudPlan &p, const uint32_t *hs, bool *padded, uint64_t *cap) {
+  const uint32_t n = p.n, T = p.rng.dev.T;
+  const uint32_t maxocc = hs[1], dense_leaves = hs[3];
+  *cap = (uint64_t)((maxocc + kLeaf - 1) / kLeaf) * kLeaf;
+  const uint64_t padded_slots = *cap * T;
+  *padded = getenv("NSFPS_NO_PADDED") == nullptr && *cap > 0 &&
+            padded_slots <= padded_slot_limit(n) && padded_slots <= p.slots_ub;
+  return *padded ? padded_slots / kLeaf : dense_leaves;
+}
+
+// Mixed leaves (runs of 64 slots of the logical order, possibly of several
+// buckets) for every cloud of a call, or for none: when the runs engine
+// samples them, every cloud's buckets have one cell, and the per-bucket
+// layout would fill its leaves to less than a quarter on the whole (the
+// update and gather passes work on whole leaves, so sparse buckets waste
+// their lanes; a mixed leaf instead tests each point's cell against each
+// pick's cube).  Measured on the MI355X (sampling pass per call, per-bucket
+// against mixed): 64 clouds of 16,384 points on 16^3 blocks (leaves 10 %
+// full) 2.52 -> 1.82 ms; the 1M-point uniform cube (50 %) 7.47 -> 8.10 ms
+// and the 120,000-point scan (66 %) 3.67 -> 4.66 ms, where the wider cell
+// boxes and the per-point test cost more than the lanes they fill.
+// NSFPS_MIXED=0 never takes them; NSFPS_MIXED=1 whenever allowed.
+bool mixed_wanted(const std::vector<CloudPlan> &plans, const uint32_t *hs) {
+  const char *e = getenv("NSFPS_MIXED");
+  if (e && atoi(e) == 0) return false;
+  uint64_t leaves = 0, points = 0;
+  for (size_t i = 0; i < plans.size(); ++i) {
+    const CloudPlan &p = plans[i];
+    if (p.tree || !p.rng.dev.bijective) return false;
+    bool padded;
+    uint64_t cap;
+    leaves += bucket_leaves(p, hs + 4 * i, &padded, &cap);
+    points += p.n;
+  }
+  if (e && atoi(e) == 1) return true;
+  return leaves * kLeaf > 4 * points;
+}
+
+nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs, bool mixed) {
   CloudDev &c = p.dev;
   const uint32_t n = p.n, T = p.rng.dev.T;
   if (hs[0]) return fail(NSFPS_EINVAL, "points must be finite");
-  const uint32_t maxocc = hs[1], dense_leaves = hs[3];
-  uint64_t cap = (uint64_t)((maxocc + kLeaf - 1) / kLeaf) * kLeaf;
-  uint64_t padded_slots = cap * T;
-  bool padded = getenv("NSFPS_NO_PADDED") == nullptr && cap > 0 &&
-                padded_slots <= padded_slot_limit(n) && padded_slots <= p.slots_ub;
+  bool padded;
+  uint64_t cap;
+  const uint64_t leaves = bucket_leaves(p, hs, &padded, &cap);
+  padded = padded && !mixed;
   p.cap = padded ? cap : 0;
   c.padded = padded ? 1u : 0u;
+  c.mixed = mixed ? 1u : 0u;
   c.lpc = padded ? (uint32_t)(cap / kLeaf) : 0u;
-  c.nslots = padded ? (uint32_t)padded_slots : n;
-  c.nleaves = padded ? T * c.lpc : dense_leaves;
+  c.nslots = padded ? (uint32_t)(cap * T) : n;
+  c.nleaves = mixed ? (n + kLeaf - 1) / kLeaf : (uint32_t)leaves;
   if (c.nleaves > p.leaves_ub)
     return fail(NSFPS_EDEVICE, "internal: leaf count %u exceeds bound %u", c.nleaves, p.leaves_ub);
   c.nl1 = (c.nleaves + kFan - 1) / kFan;
@@ -829,11 +871,11 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
                         (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), const_cast<uint32_t *>(c.R),
                         p.d_small + 2, st));
   HIP_TRY(launch_cell_info(p.d_counts, p.d_lc, T, p.d_cell_info, st));
-  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.nleaves,
-                            p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
+  HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.mixed, n,
+                            c.nleaves, p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
                             const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
                             const_cast<uint32_t *>(c.leaf_al), const_cast<uint2 *>(c.leaf_sc),
-                            c.leaf_key, c.leaf_pos, st));
+                            const_cast<uint2 *>(c.leaf_cbox), c.leaf_key, c.leaf_pos, st));
   HIP_TRY(launch_init_state(c, p.d_small + 2, st));
   c.lds = plan_lds(c);
   return NSFPS_OK;
@@ -916,8 +958,9 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   std::vector<uint32_t> hs(4 * nc);
   HIP_TRY(hipMemcpyAsync(hs.data(), cb.small, nc * 16, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  const bool mixed = mixed_wanted(plans, hs.data());
   for (size_t i = 0; i < nc; ++i) {
-    nsfps_status rc = decide_layout(plans[i], &hs[4 * i]);
+    nsfps_status rc = decide_layout(plans[i], &hs[4 * i], mixed);
     if (rc) return rc;
   }
   // the sub-cell sort for the tree engine, and where a bucket can fill a
@@ -1044,6 +1087,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
     leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
   }
   const uint32_t nc = (uint32_t)plans.size();
+  const bool mixed = plans[0].dev.mixed != 0;  // the same for every cloud of a call
   const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
   *split_out = split ? kUpdateSplit : 1u;
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
@@ -1059,7 +1103,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            split, st));
+                            split, mixed, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1069,7 +1113,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            split, st));
+                            split, mixed, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }
@@ -1273,6 +1317,7 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
   S.wide_iters = wide_total;
   S.samples = samples;
   S.padded = plans.size() == 1 ? plans[0].dev.padded : 0;
+  S.mixed = plans[0].dev.mixed;
   S.lds_bytes = runs ? 0 : lds_bytes;
   S.rounds = rounds;
   S.engine = runs ? 1u : 0u;

@@ -111,6 +111,10 @@ struct CloudDev {
   uint32_t phys0;    // physical slot of input row 0 (the first sample)
   uint32_t padded;   // 1: slot = bucket * cap + j, leaf = bucket * lpc + k
   uint32_t lpc;      // leaves per bucket when padded
+  uint32_t mixed;    // 1: leaf l holds slots 64 l .. 64 l + 63 of the logical order,
+                     // which may belong to several buckets (runs engine, one cell
+                     // per bucket); 0: a leaf holds points of one bucket
+  uint32_t pad0;
   RangeDev r;
   LdsPlan lds;
   const uint32_t *lut;
@@ -124,6 +128,8 @@ struct CloudDev {
   const uint2 *leaf_sc;       // first slot, point count (leaf_lo.w / leaf_hi.w packed)
   const uint32_t *leaf_cell;  // ix | iy << 10 | iz << 20
   const uint32_t *leaf_al;    // r.na per leaf: the cells of its bucket, kNoCell-padded
+  const uint2 *leaf_cbox;     // lo / hi corners of the cells of the leaf's points (10 bits
+                              // per axis; lo > hi on some axis: no points)
   uint64_t *leaf_key;         // max key of the leaf
   float4 *leaf_pos;           // x, y, z, input row (bits) of that key
   uint64_t *l1_key;

@@ -47,12 +47,15 @@ hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t 
                          const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
                          uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
                          uint32_t *R, uint32_t *phys0, hipStream_t st);
+// Leaves: per bucket (padded or dense), or with mixed = 1 runs of 64 slots
+// of the logical order; then their boxes, cell corners and initial keys.
 hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
-                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t nleaves,
-                             const RangeDev &r, const float4 *P4, const uint2 *RO,
-                             float4 *leaf_lo, float4 *leaf_hi, uint32_t *leaf_cell,
-                             uint32_t *leaf_al, uint2 *leaf_sc, uint64_t *leaf_key,
-                             float4 *leaf_pos, hipStream_t st);
+                             uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t mixed,
+                             uint32_t n, uint32_t nleaves, const RangeDev &r, const float4 *P4,
+                             const uint2 *RO, float4 *leaf_lo, float4 *leaf_hi,
+                             uint32_t *leaf_cell, uint32_t *leaf_al, uint2 *leaf_sc,
+                             uint2 *leaf_cbox, uint64_t *leaf_key, float4 *leaf_pos,
+                             hipStream_t st);
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st);
 
 // The build of many clouds, each step one launch for all of them (grid y =
@@ -93,10 +96,11 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 // `rounds` rounds of update pass, refinement passes, gather pass and run.
 // alias: some cloud's cells share buckets.  leaf_bound: the update pass also
 // bounds each pick by each leaf's box; split: it takes kUpdateSplit
-// workgroups per level-1 node.
+// workgroups per level-1 node; mixed: the clouds' leaves are runs of 64 slots
+// that may hold several buckets (never with alias).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, hipStream_t st);
+                         bool leaf_bound, bool split, bool mixed, hipStream_t st);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

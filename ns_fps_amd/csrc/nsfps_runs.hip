@@ -293,9 +293,14 @@ __device__ __forceinline__ const NSFPS_GLOBAL RunState &rstate(const CloudDev &c
 // again, per leaf).  SPLIT: the node's leaves are split over SPLIT
 // workgroups, each storing the largest key of its leaves as one of the
 // node's parts (node_key reads the node's key back as the largest part).
-template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT>
+// MIXED: a leaf is a run of 64 slots of the logical order and may hold
+// several buckets (one cell each); a pick touches the leaf when its cube
+// overlaps the leaf's cell box, and lowers a point only when the point's own
+// cell lies in the cube (the reference's rule, point by point).
+template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT, bool MIXED>
 __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60))) void k_update(
     const CloudDev *__restrict__ clouds) {
+  static_assert(!(ALIAS && MIXED), "leaves of several buckets need one cell per bucket");
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ float4 s_pp[kListCap];
   __shared__ uint2 s_pc[kListCap];  // the picks' cube corners: pack11(lo), pack11(hi) | kGuards
@@ -314,12 +319,19 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   const uint32_t leaf0 = g * kFan + sub * (kFan / SPLIT) + wave * kLPW;
   uint64_t mkey = 0;
   uint32_t mcell = 0, mst = 0, mcnt = 0;
+  uint32_t mchi = 0;  // MIXED: the leaf's cell box is mcell .. mchi
   // LB (leaf bounds): the leaf's box of points (an absent leaf's stays empty)
   constexpr bool lbound = LB;
   float4 mlo = make_float4(0.f, 0.f, 0.f, 0.f), mhi = mlo;
   if (lane < kLPW && leaf0 + lane < c.nleaves) {
     mkey = gptr(c.leaf_key)[leaf0 + lane];
-    mcell = gptr(c.leaf_cell)[leaf0 + lane];
+    if (MIXED) {
+      const uint2 cb = gptr(c.leaf_cbox)[leaf0 + lane];
+      mcell = cb.x;
+      mchi = cb.y;
+    } else {
+      mcell = gptr(c.leaf_cell)[leaf0 + lane];
+    }
     const uint2 sc = gptr(c.leaf_sc)[leaf0 + lane];
     mst = sc.x;
     mcnt = sc.y;
@@ -396,6 +408,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   // which leaves a pick touches (hm: the first 64 picks whose cube holds the
   // leaf's cell), and which must be read
   uint32_t c11[kLPW], st[kLPW], cnt[kLPW];
+  uint32_t ch11g[MIXED ? kLPW : 1];  // MIXED: pack11 of the leaf's cell box hi, with guards
   uint64_t okey[kLPW], hm[kLPW];
   bool hit[kLPW], need[kLPW];
   // pick i's cube (its s_pc record) holds (a cell of the bucket of) leaf k.
@@ -403,7 +416,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   // more here than the reads it saves on points that fill their cells.
   const auto touches_pick = [&](uint32_t k, uint2 cube) -> bool {
     uint32_t in;
-    if (!ALIAS) {
+    if (MIXED) {  // the cube overlaps the leaf's cell box (in_box11 crosswise)
+      in = in_box11(cube.y, cube.x, c11[k], ch11g[MIXED ? k : 0]);
+    } else if (!ALIAS) {
       in = in_box11(c11[k] | kGuards, c11[k], cube.x, cube.y);
     } else if (na == 2) {
       const uint32_t a0 = pack11(rdlane(mal, 2 * k)), a1 = pack11(rdlane(mal, 2 * k + 1));
@@ -426,6 +441,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
 #pragma unroll
   for (uint32_t k = 0; k < kLPW; ++k) {
     c11[k] = pack11(rdlane(mcell, k));
+    if (MIXED) ch11g[MIXED ? k : 0] = pack11(rdlane(mchi, k)) | kGuards;
     st[k] = rdlane(mst, k);
     cnt[k] = rdlane(mcnt, k);
     okey[k] = ((uint64_t)rdlane((uint32_t)(mkey >> 32), k) << 32) | rdlane((uint32_t)mkey, k);
@@ -504,6 +520,11 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
         const uint32_t lo = ~rk[k];
         float d = p[k].w;
         if (hit[k]) {
+          // MIXED: this point's own cell (pack11), the cell its bucket is
+          uint32_t pc11 = 0;
+          if (MIXED)
+            pc11 = pack11(pack_cell(cell_axis(c.r, 0, p[k].x), cell_axis(c.r, 1, p[k].y),
+                                    cell_axis(c.r, 2, p[k].z)));
           for (uint32_t cb = 0; cb < nsel; cb += 64) {
             uint64_t m = cb == 0 ? hm[k] : __ballot((cb + lane < nsel) & touches(k, cb + lane));
             while (m) {
@@ -511,7 +532,12 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
               m &= m - 1;
               const float4 q = s_pp[cb + j];
               const float dd = sqdist(p[k].x, p[k].y, p[k].z, q.x, q.y, q.z);
-              d = dd < d ? dd : d;
+              if (MIXED) {
+                const uint2 qc = s_pc[cb + j];
+                d = in_box11(pc11 | kGuards, pc11, qc.x, qc.y) && dd < d ? dd : d;
+              } else {
+                d = dd < d ? dd : d;
+              }
             }
           }
           const bool lowered = act && d < p[k].w;
@@ -635,9 +661,10 @@ __device__ __forceinline__ uint32_t bit_length(uint64_t v) { return v ? 64u - __
 // (more than kListCap keys inside the finest bin), the threshold is the
 // maximum key itself: a run of one sample.  Few workgroups, each striding over
 // the level-1 nodes; most nodes hold no key above the threshold.  PROF: counts
-// the hot leaves whose points it reads and those points.  ALIAS (cells share
-// buckets): an entry's cell is its point's own (where its cube is centred
-// when it becomes a sample), and it carries the cells of its bucket.
+// the hot leaves whose points it reads and those points.  An entry's cell is
+// its point's own (where its cube is centred when it becomes a sample).
+// ALIAS (cells share buckets): the entry also carries the cells of its
+// bucket.
 template <bool PROF, bool ALIAS>
 __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restrict__ clouds,
                                                          uint32_t passes) {
@@ -655,18 +682,17 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     return gq * kFan + wave * kLeavesPerWave + lane % kLeavesPerWave;
   };
   uint64_t lkey = 0;
-  uint32_t lst = 0, lcnt = 0, lcell = 0;
+  uint32_t lst = 0, lcnt = 0;
   const auto read_leaf = [&](uint32_t c0) {
     uint32_t gq;
     const uint32_t lf = leaf_of(c0, gq);
     lkey = 0;
-    lst = lcnt = lcell = 0;
+    lst = lcnt = 0;
     if (gq < c.nl1 && lf < c.nleaves) {
       lkey = gptr(c.leaf_key)[lf];
       const uint2 sc = gptr(c.leaf_sc)[lf];
       lst = sc.x;
       lcnt = sc.y;
-      lcell = gptr(c.leaf_cell)[lf];
     }
   };
   read_leaf(blockIdx.x);
@@ -713,7 +739,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     const uint32_t lf = leaf_of(c0, gq);
     const bool hot = lcnt != 0 && lkey >= bkey;  // an empty or absent leaf has key 0
     if (PROF) {
-      pin_vgpr(lst, lcnt, lcell, (uint32_t)hot);
+      pin_vgpr(lst, lcnt, (uint32_t)hot);
       if (!gt2) gt2 = __builtin_amdgcn_s_memrealtime();
     }
     if (tid == 0) s_cnt = 0;
@@ -729,7 +755,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     }
     float4 hp[kGatherHold];
     uint2 hr[kGatherHold];
-    uint32_t hcell[kGatherHold], hn[kGatherHold], hal[kGatherHold];
+    uint32_t hn[kGatherHold], hal[kGatherHold];
     uint64_t htk[kGatherHold];
     const uint32_t na = ALIAS ? c.r.na : 1u;
     // the held leaves' points: every lane loads, without a branch, so that
@@ -742,7 +768,6 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       const uint32_t j = have ? (uint32_t)__builtin_ctzll(rest) : 0u;
       rest &= rest - 1;
       const uint32_t st = rdlane(lst, j), cnt = have ? rdlane(lcnt, j) : 0u;
-      hcell[u] = rdlane(lcell, j);
       hn[u] = cnt;
       const uint32_t idx = lane < cnt ? st + lane : 0u;
       hp[u] = gptr(c.P4)[idx];
@@ -784,18 +809,17 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
     NSFPS_GLOBAL uint32_t *const LC = vgpr_ptr(gptr(c.list_c));
     // arguments by value: a reference into hp / hr would make those arrays
     // memory (the compiler then keeps them in LDS)
-    const auto put = [&](float4 p, uint2 ro, uint32_t cell, uint32_t al, uint64_t m) {
+    const auto put = [&](float4 p, uint2 ro, uint32_t al, uint64_t m) {
       if ((m >> lane) & 1u) {
         const uint32_t i = base + lanes_below(m);
         if (i < kListCap) {
           LP[i] = p;
           LR[i] = ro;
-          if (ALIAS) {
-            LC[i] = pack_cell(cell_axis(c.r, 0, p.x), cell_axis(c.r, 1, p.y), cell_axis(c.r, 2, p.z));
+          // the point's own cell (its bucket's, when buckets have one cell;
+          // a leaf may hold several buckets)
+          LC[i] = pack_cell(cell_axis(c.r, 0, p.x), cell_axis(c.r, 1, p.y), cell_axis(c.r, 2, p.z));
+          if (ALIAS)
             for (uint32_t a = 0; a < na; ++a) gptr(c.list_al)[(size_t)i * na + a] = rdlane(al, a);
-          } else {
-            LC[i] = cell;
-          }
         } else {
           rs.err = 1;
         }
@@ -803,7 +827,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       base += (uint32_t)__popcll(m);
     };
 #pragma unroll
-    for (uint32_t u = 0; u < kGatherHold; ++u) put(hp[u], hr[u], hcell[u], hal[u], htk[u]);
+    for (uint32_t u = 0; u < kGatherHold; ++u) put(hp[u], hr[u], hal[u], htk[u]);
     rest = later;
     while (rest) {
       const uint32_t j = (uint32_t)__builtin_ctzll(rest);
@@ -818,7 +842,7 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
       }
       if (ALIAS && lane < na) al = gptr(c.leaf_al)[(size_t)rdlane(lf, j) * na + lane];
       const bool take = lane < cnt && (((uint64_t)__float_as_uint(p.w) << 32) | ~ro.x) >= bkey;
-      put(p, ro, rdlane(lcell, j), al, __ballot(take));
+      put(p, ro, al, __ballot(take));
     }
     __syncthreads();  // s_base is read before the next chunk's claim
   }
@@ -1918,10 +1942,11 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 }
 
 // The classic round's update, gather and run kernels of one variant.
-template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT>
+template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT, bool MIXED>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
                     uint32_t passes, hipStream_t st) {
-  k_update<PROF, ALIAS, LB, SPLIT><<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
+  k_update<PROF, ALIAS, LB, SPLIT, MIXED>
+      <<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
@@ -1930,21 +1955,27 @@ void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, hipStream_t st) {
+                         bool leaf_bound, bool split, bool mixed, hipStream_t st) {
+  if (alias && mixed) return hipErrorInvalidValue;  // leaves of several buckets: one cell each
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
   using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, hipStream_t);
   constexpr uint32_t S = kUpdateSplit;
-  static constexpr Launch kClassic[2][2][2][2] = {  // [profile][alias][leaf_bound][split]
-      {{{launch_classic<false, false, false, 1>, launch_classic<false, false, false, S>},
-        {launch_classic<false, false, true, 1>, launch_classic<false, false, true, S>}},
-       {{launch_classic<false, true, false, 1>, launch_classic<false, true, false, S>},
-        {launch_classic<false, true, true, 1>, launch_classic<false, true, true, S>}}},
-      {{{launch_classic<true, false, false, 1>, launch_classic<true, false, false, S>},
-        {launch_classic<true, false, true, 1>, launch_classic<true, false, true, S>}},
-       {{launch_classic<true, true, false, 1>, launch_classic<true, true, false, S>},
-        {launch_classic<true, true, true, 1>, launch_classic<true, true, true, S>}}}};
-  const Launch classic = kClassic[profile][alias][leaf_bound][split];
+  // [profile][cells: one per leaf, shared buckets, several per leaf][leaf_bound][split]
+  static constexpr Launch kClassic[2][3][2][2] = {
+      {{{launch_classic<false, false, false, 1, false>, launch_classic<false, false, false, S, false>},
+        {launch_classic<false, false, true, 1, false>, launch_classic<false, false, true, S, false>}},
+       {{launch_classic<false, true, false, 1, false>, launch_classic<false, true, false, S, false>},
+        {launch_classic<false, true, true, 1, false>, launch_classic<false, true, true, S, false>}},
+       {{launch_classic<false, false, false, 1, true>, launch_classic<false, false, false, S, true>},
+        {launch_classic<false, false, true, 1, true>, launch_classic<false, false, true, S, true>}}},
+      {{{launch_classic<true, false, false, 1, false>, launch_classic<true, false, false, S, false>},
+        {launch_classic<true, false, true, 1, false>, launch_classic<true, false, true, S, false>}},
+       {{launch_classic<true, true, false, 1, false>, launch_classic<true, true, false, S, false>},
+        {launch_classic<true, true, true, 1, false>, launch_classic<true, true, true, S, false>}},
+       {{launch_classic<true, false, false, 1, true>, launch_classic<true, false, false, S, true>},
+        {launch_classic<true, false, true, 1, true>, launch_classic<true, false, true, S, true>}}}};
+  const Launch classic = kClassic[profile][alias ? 1 : mixed ? 2 : 0][leaf_bound][split];
   for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, st);
   return hipGetLastError();
 }

@@ -285,6 +285,7 @@ py::dict last_stats_py() {
   d["rounds"] = s.rounds;
   d["engine"] = s.engine ? "runs" : "tree";
   d["update_split"] = s.update_split;
+  d["mixed"] = s.mixed;
   return d;
 }
 

@@ -67,6 +67,23 @@ def test_workload_matches_reference_hash(yf, lib, wname):
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("mixed", ["0", "1"])
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "lidar_scan", "batched_shapes",
+                                   "clustered"])
+def test_workload_hash_in_both_leaf_layouts(yf, lib, wname, mixed, monkeypatch):
+    """Leaves of one bucket each (padded or dense) and mixed leaves (runs of 64
+    slots of the logical order, several buckets each, every point's own cell
+    tested) give the reference's samples on every workload whose buckets
+    have one cell."""
+    if wname not in GOLDEN_CONFIGS:
+        pytest.skip(f"golden hash of {wname} not generated")
+    monkeypatch.setenv("NSFPS_MIXED", mixed)
+    w, g, outs = run_workload(yf, lib, wname)
+    assert yf.last_stats()["mixed"] == int(mixed)
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
 def test_clustered_workload_matches_reference_hash(yf, lib):
     if "clustered" not in GOLDEN_CONFIGS:
         pytest.skip("golden hash for the 8,388,608-point workload not generated")
@@ -147,7 +164,7 @@ TREE = {"NSFPS_ENGINE": "tree"}
 
 
 @pytest.mark.parametrize("env", [
-    {}, {"NSFPS_NO_PADDED": "1"},
+    {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
@@ -155,8 +172,8 @@ TREE = {"NSFPS_ENGINE": "tree"}
 ], ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()) or "runs")
 def test_schedule_and_layout_do_not_change_results(yf, env, monkeypatch):
     """The engine (speculative runs, or grid-wide steps + single-workgroup
-    tree loop), where the grid-wide phase hands over, the padded or table
-    layout and the profiling build are result-invariant."""
+    tree loop), where the grid-wide phase hands over, the padded, table or
+    mixed-leaf layout and the profiling build are result-invariant."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     for name in ["testpy_10k_1k", "lattice_ties_16", "granularity_64x64x64", "boundary_aligned"]:
@@ -275,16 +292,23 @@ def test_tie_heavy_clouds_match_oracle(yf, oracle, name, pts, m, rng):
     assert np.array_equal(got, want), name
 
 
-def test_many_level1_nodes_on_the_runs_engine(yf, oracle):
-    """1M uniform points on a 128^3 grid: about 825k occupied buckets, each
-    with at least one 64-point leaf, so some 12,900 level-1 nodes, above what
-    the tree engine's single-workgroup loop holds; the runs engine samples it."""
+@pytest.mark.parametrize("mixed", ["0", "1"])
+def test_many_level1_nodes_on_the_runs_engine(yf, oracle, mixed, monkeypatch):
+    """1M uniform points on a 128^3 grid: about 825k occupied buckets.  With a
+    leaf per bucket (NSFPS_MIXED=0) that is some 12,900 level-1 nodes, above
+    what the tree engine's single-workgroup loop holds; with mixed leaves
+    (runs of 64 slots over about 50 buckets each) 16,384 leaves whose cell
+    boxes span several cells.  The runs engine samples both exactly."""
+    monkeypatch.setenv("NSFPS_MIXED", mixed)
     rs = np.random.RandomState(21)
     pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)
     rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 128, 128, 128)
     got = yf.fps(pts, 3000, yf.make_range(*rng))
     st = yf.last_stats()
-    assert st["engine"] == "runs" and st["n_leaves"] > 64 * 4096
+    assert st["engine"] == "runs" and st["mixed"] == int(mixed)
+    assert st["n_leaves"] == (16384 if mixed == "1" else st["n_leaves"])
+    if mixed == "0":
+        assert st["n_leaves"] > 64 * 4096
     assert np.array_equal(got, oracle.fps(pts, 3000, rng))
 
 
