@@ -13,15 +13,21 @@ per candidate point and 8 B per candidate 16-point leaf of every iteration,
 the per-iteration census in tests/golden/census.npz -- in the hipEvent-timed
 sample_ms of the call.
 
-Besides the steady-state time of repeated calls (ms_per_step), the line
-reports the first call of a shape (first_call_ms: no replayed round
+Besides the steady-state time of repeated calls (ms_per_step, and the
+median of the same calls, each of which returns after its stream work), the
+line reports the first call of a shape (first_call_ms: no replayed round
 schedule), the host-buffer call with its PCIe copies (e2e_ms) and the
 sampling of a prepared plan (plan_sample_ms).
 
-Prints ONE JSON line (rank 0).  With --all it first prints one line per
-workload (the five seeded benchmark workloads and the uniform cube on a 30^3
-grid, which takes the general bucket path; each with its roofline and
-reference CPU time); the contract line always comes last.
+The other four benchmark configurations (the 10,000-point quickstart, the
+120,000-point LiDAR scan, 64 batched clouds of 16,384 points with per-cloud
+compute_bbox, and the 8,388,608-point clustered cloud) each print one line
+first -- median ms per call on device-resident input, samples/s, the
+sampling pass's roofline and traffic, the reference CPU path on this host,
+bit-exactness against the reference's hashes -- and the contract line
+carries the same figures in its "configs" block.  --all adds the uniform
+cube on a 30^3 grid (the general bucket path).  The contract line always
+comes last.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 2] [--workload uniform_cube]
 """
@@ -44,6 +50,8 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 HEADLINE_METRIC = "FPS ms/call & samples/s at 1M pts -> 65,536 samples; % of HBM roofline"
 ALL_WORKLOADS = ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan", "batched_shapes",
                  "clustered"]
+# the benchmark configurations besides the headline one, in their order
+OTHER_CONFIGS = ["quickstart", "lidar_scan", "batched_shapes", "clustered"]
 
 
 def metric_for(w):
@@ -65,7 +73,8 @@ def workload_config(w, extra=None):
         "blocks": list(w["blocks"]),
         "range": None if w["range"] is None else [float(v) for v in w["range"][:6]],
         "start_index": 0,
-        "input": "device-resident float32 (N,3)" if len(P) == 1 else "host float32 (B,N,3)",
+        "input": "device-resident float32 (N,3)" if len(P) == 1 else
+                 "device-resident float32 (B,N,3)",
     }
     if extra:
         cfg.update(extra)
@@ -157,10 +166,12 @@ def run_single(lib, hip, w, steps, warmup):
         for _ in range(warmup):
             lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
         hip.synchronize()
-        stats = []
+        stats, per_call = [], []
         t0 = time.perf_counter()
         for _ in range(steps):
-            n = lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
+            tc = time.perf_counter()
+            n = lib.fps_device(d_xyz, len(P), m, w["range"], d_out)  # returns after the stream
+            per_call.append((time.perf_counter() - tc) * 1e3)
             stats.append(lib.stats())
         hip.synchronize()
         t1 = time.perf_counter()
@@ -168,7 +179,8 @@ def run_single(lib, hip, w, steps, warmup):
     finally:
         hip.free(d_xyz)
         hip.free(d_out)
-    return {"ms": (t1 - t0) * 1e3 / steps, "stats": stats, "out": out, "digest": sha_i32(out),
+    return {"ms": (t1 - t0) * 1e3 / steps, "median_ms": statistics.median(per_call),
+            "stats": stats, "out": out, "digest": sha_i32(out),
             "first_ms": first_ms, "first_stats": first_stats}
 
 
@@ -214,18 +226,49 @@ def run_plan(lib, hip, w, steps):
             "plan_sample_ms": round((t1 - t0) * 1e3 / steps, 3), "digest": sha_i32(out)}
 
 
-def run_batched(yf, w, steps, warmup):
+def run_batched(lib, hip, w, steps, warmup):
+    """Device-resident clouds (B, N, 3) through nsfps_fps_batched_device:
+    per-cloud compute_bbox (range=None) on the device, build and sampling of
+    every cloud, the samples in device memory."""
+    P = np.ascontiguousarray(np.stack(w["clouds"]))
+    B, n, m = P.shape[0], P.shape[1], int(w["n_samples"])
+    d_xyz, d_out = hip.upload(P), hip.malloc(B * m * 4)
+    try:
+        # a call of another shape first, so that the timed first call replays
+        # no round schedule
+        lib.fps_batched_device(d_xyz, B, n, m - 1, d_out, w["range"], w["blocks"])
+        t = time.perf_counter()
+        lib.fps_batched_device(d_xyz, B, n, m, d_out, w["range"], w["blocks"])
+        first_ms = (time.perf_counter() - t) * 1e3
+        for _ in range(warmup):
+            lib.fps_batched_device(d_xyz, B, n, m, d_out, w["range"], w["blocks"])
+        stats, per_call = [], []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tc = time.perf_counter()
+            lens = lib.fps_batched_device(d_xyz, B, n, m, d_out, w["range"], w["blocks"])
+            per_call.append((time.perf_counter() - tc) * 1e3)
+            stats.append(lib.stats())
+        t1 = time.perf_counter()
+        out = hip.download(d_out, B * m, np.int32).reshape(B, m)
+    finally:
+        hip.free(d_xyz)
+        hip.free(d_out)
+    digests = [sha_i32(out[b, :lens[b]]) for b in range(B)]
+    return {"ms": (t1 - t0) * 1e3 / steps, "median_ms": statistics.median(per_call),
+            "stats": stats, "lens": lens, "digests": digests, "first_ms": first_ms}
+
+
+def run_batched_host(yf, w, reps=3):
+    """The same clouds as host arrays through the module's fps_batched (copies
+    to and from the device included)."""
     P = np.stack(w["clouds"])
-    for _ in range(warmup):
-        yf.fps_batched(P, w["n_samples"], None, *w["blocks"])
-    stats = []
-    t0 = time.perf_counter()
-    for _ in range(steps):
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
         idx, lens = yf.fps_batched(P, w["n_samples"], None, *w["blocks"])
-        stats.append(yf.last_stats())
-    t1 = time.perf_counter()
-    digests = [sha_i32(idx[b, :lens[b]]) for b in range(len(lens))]
-    return (t1 - t0) * 1e3 / steps, stats, digests
+        times.append((time.perf_counter() - t) * 1e3)
+    return statistics.median(times), [sha_i32(idx[b, :lens[b]]) for b in range(len(lens))]
 
 
 # ------------------------------------------------------------- CPU baseline
@@ -380,15 +423,19 @@ def run_phases(lib, hip, w):
     """One call with NSFPS_PROFILE=1: the run kernel's phase clocks summed over
     rounds (s_memtime cycles of wave 0 between its barriers, and s_memrealtime
     ticks of 10 ns for the load and the whole kernel), per round and per hot
-    set."""
+    set.  Batched clouds: one call of all of them, the counters of cloud 0
+    (every kernel adds to its own cloud's words)."""
     os.environ["NSFPS_PROFILE"] = "1"
     try:
-        P = w["clouds"][0]
-        m = int(w["n_samples"])
+        P = np.ascontiguousarray(np.stack(w["clouds"]))
+        B, n, m = P.shape[0], P.shape[1], int(w["n_samples"])
         d_xyz = hip.upload(P)
-        d_out = hip.malloc(m * 4)
+        d_out = hip.malloc(B * m * 4)
         try:
-            lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
+            if B == 1:
+                lib.fps_device(d_xyz, n, m, w["range"], d_out)
+            else:
+                lib.fps_batched_device(d_xyz, B, n, m, d_out, w["range"], w["blocks"])
             st = lib.stats()
             words = lib.loop_profile()
         finally:
@@ -486,47 +533,73 @@ def pass_counts(wname, ctr, rounds):
 
 # --------------------------------------------------------------------- lines
 
-def workload_line(lib, hip, yf, wname, budget_s, with_cpu=True):
-    """One informational line per workload: time per call, samples/s,
-    roofline of the sampling pass and the reference's CPU time."""
+def workload_line(lib, hip, yf, wname, budget_s, steps, warmup, with_cpu=True):
+    """One line per workload: median ms per call on device-resident input,
+    samples/s, the sampling pass's roofline (with the committed traffic
+    profile), the reference's CPU time on this host, bit-exactness."""
     from ns_fps_amd.workloads import make_workload
     w = make_workload(wname)
     g = golden_hashes(wname)
     if len(w["clouds"]) == 1:
-        steps = 1 if wname == "clustered" else 5
-        r = run_single(lib, hip, w, steps, 0 if wname == "clustered" else 1)
+        big = wname == "clustered"
+        r = run_single(lib, hip, w, min(steps, 5) if big else steps, min(warmup, 1) if big else warmup)
         s = r["stats"][-1]
         exact = g is not None and r["digest"] == g["output_sha256"][0]
-        line = {"workload": wname, "metric": metric_for(w), "ms_per_call": round(r["ms"], 3),
-                "first_call_ms": round(r["first_ms"], 3),
+        samples = len(r["out"])
+        line = {"workload": wname, "metric": metric_for(w),
+                "ms_per_call": round(r["median_ms"], 3), "ms_mean": round(r["ms"], 3),
+                "calls": len(r["stats"]), "first_call_ms": round(r["first_ms"], 3),
                 "device_ms": round(s["device_ms"], 3), "build_ms": round(s["build_ms"], 3),
                 "sample_ms": round(s["sample_ms"], 3), "rounds": int(s["rounds"]),
-                "samples_per_s": round(len(r["out"]) / (r["ms"] / 1e3), 1), "bit_exact": exact}
-        if wname != "clustered":
+                "samples_per_s": round(samples / (r["median_ms"] / 1e3), 1), "bit_exact": exact}
+        if not big:
             e2e, dg = run_host_buffers(lib, w)
             line["e2e_ms"] = round(e2e, 3)
             line["e2e_bit_exact"] = g is not None and dg == g["output_sha256"][0]
-        sample_ms = statistics.mean(x["sample_ms"] for x in r["stats"])
         engine = "runs" if s["engine"] else "tree"
     else:
-        ms, st, dgs = run_batched(yf, w, 3, 1)
-        s = st[-1]
-        exact = g is not None and dgs == g["output_sha256"]
-        line = {"workload": wname, "metric": metric_for(w), "ms_per_call": round(ms, 3),
+        r = run_batched(lib, hip, w, steps, warmup)
+        s = r["stats"][-1]
+        exact = g is not None and r["digests"] == g["output_sha256"]
+        samples = int(sum(r["lens"]))
+        e2e, dg = run_batched_host(yf, w)
+        line = {"workload": wname, "metric": metric_for(w),
+                "ms_per_call": round(r["median_ms"], 3), "ms_mean": round(r["ms"], 3),
+                "calls": len(r["stats"]), "first_call_ms": round(r["first_ms"], 3),
                 "device_ms": round(s["device_ms"], 3), "build_ms": round(s["build_ms"], 3),
-                "sample_ms": round(s["sample_ms"], 3), "e2e_ms": round(s["e2e_ms"], 3),
-                "rounds": int(s["rounds"]),
-                "samples_per_s": round(s["samples"] / (ms / 1e3), 1), "bit_exact": exact,
-                "input": "host float32 (B,N,3); e2e includes the bounds on the host and the copies"}
-        sample_ms = statistics.mean(x["sample_ms"] for x in st)
-        engine = s["engine"]
-    line["roofline"] = roofline_of(wname, sample_ms, engine)
+                "sample_ms": round(s["sample_ms"], 3), "rounds": int(s["rounds"]),
+                "samples_per_s": round(samples / (r["median_ms"] / 1e3), 1), "bit_exact": exact,
+                "input": "device-resident float32 (B,N,3); range=None: per-cloud compute_bbox "
+                         "on the device",
+                "e2e_ms": round(e2e, 3),
+                "e2e_bit_exact": g is not None and dg == g["output_sha256"],
+                "e2e_input": "host float32 (B,N,3) through the module's fps_batched"}
+        engine = "runs" if s["engine"] else "tree"
+    line["mixed_leaves"] = bool(s.get("mixed", 0))
+    line["roofline"] = roofline_of(wname, statistics.mean(x["sample_ms"] for x in r["stats"]),
+                                   engine)
     if with_cpu:
         line["cpu_baseline"] = cpu_baseline(w, budget_s)
         cb = line["cpu_baseline"]
         if cb.get("ms_per_call"):
             line["speedup_vs_cpu_baseline"] = round(cb["ms_per_call"] / line["ms_per_call"], 1)
     return line
+
+
+def config_summary(line):
+    """The compact form of a workload line carried in the contract line."""
+    rf = line.get("roofline") or {}
+    cb = line.get("cpu_baseline") or {}
+    out = {"ms_per_call": line["ms_per_call"], "samples_per_s": line["samples_per_s"],
+           "sample_ms": line["sample_ms"], "bit_exact": line["bit_exact"],
+           "roofline": {k: rf.get(k) for k in ("achieved", "frac", "traffic")} if rf else None}
+    if cb:
+        out["cpu_baseline"] = {"ms_per_call": cb.get("ms_per_call"), "ms_sample": cb.get("ms_sample"),
+                               "samples_per_s": cb.get("value"), "kind": cb.get("kind"),
+                               "cores": cb.get("cores"), "sample": cb.get("sample")}
+        if line.get("speedup_vs_cpu_baseline"):
+            out["speedup_vs_cpu_baseline"] = line["speedup_vs_cpu_baseline"]
+    return out
 
 
 def main():
@@ -539,12 +612,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=30.0,
                     help="seconds of reference CPU work per workload (default 30)")
-    ap.add_argument("--all", action="store_true", help="also print a line per workload")
+    ap.add_argument("--all", action="store_true",
+                    help="also print the uniform cube on a 30^3 grid (the general bucket path) "
+                         "among the per-workload lines")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-workload lines (the contract line alone)")
     ap.add_argument("--no-contract", action="store_true",
-                    help="with --all: stop after the per-workload lines (profiler runs of one "
-                         "workload)")
+                    help="stop after the per-workload lines (profiler runs of one workload)")
     ap.add_argument("--only", default="",
-                    help="with --all: comma-separated workloads instead of all six")
+                    help="comma-separated workloads for the per-workload lines instead of the "
+                         "benchmark configurations")
     ap.add_argument("--ball-query", action="store_true",
                     help="time only the grouping step after FPS (ball query) and print its line")
     ap.add_argument("--phases", action="store_true",
@@ -583,14 +660,17 @@ def main():
         print(json.dumps(run_phases(lib, hip, make_workload(args.workload))), flush=True)
         return
 
-    if args.all:
-        names = [n for n in args.only.split(",") if n] or ALL_WORKLOADS
+    configs = {}
+    if not args.no_configs:
+        names = [n for n in args.only.split(",") if n] or (
+            OTHER_CONFIGS + (["uniform_cube_30"] if args.all else []))
         for wname in names:
-            line = workload_line(lib, hip, yf, wname, args.cpu_budget,
+            line = workload_line(lib, hip, yf, wname, args.cpu_budget, args.steps, args.warmup,
                                  with_cpu=not args.no_cpu_baseline)
             print(json.dumps(line), flush=True)
-        if args.no_contract:
-            return
+            configs[wname] = config_summary(line)
+    if args.no_contract:
+        return
 
     w = make_workload(args.workload)
     if len(w["clouds"]) != 1:
@@ -598,6 +678,7 @@ def main():
         sys.exit(2)
     r = run_single(lib, hip, w, args.steps, args.warmup)
     stats = r["stats"]
+    configs_done = dict(configs)
     g = golden_hashes(args.workload)
     exact = g is not None and r["digest"] == g["output_sha256"][0] and len(r["out"]) == g["lengths"][0]
     sample_ms = statistics.mean(s["sample_ms"] for s in stats)
@@ -612,6 +693,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["ms"], 3),
+        "ms_median": round(r["median_ms"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -637,6 +719,9 @@ def main():
         cb = cpu_baseline(w, args.cpu_budget)
         cb.update(naive_baselines(w))
         line["cpu_baseline"] = cb
+    # the other benchmark configurations, measured above in this run
+    if configs_done:
+        line["configs"] = configs_done
     print(json.dumps(line), flush=True)
 
 

@@ -130,6 +130,18 @@ nsfps_status nsfps_range_derive(const nsfps_range *range, nsfps_range_info *info
 nsfps_status nsfps_bbox(const float *xyz, uint64_t n, uint32_t x_blocks,
                         uint32_t y_blocks, uint32_t z_blocks, nsfps_range *out);
 
+/* compute_bbox of device-resident points (d_xyz, n x 3 float32) on the
+ * device: the same bounds as nsfps_bbox over the finite points (minimum and
+ * maximum do not depend on the order; +-0 differ only before the -/+ 1e-6),
+ * and, when info is non-NULL, the range's derived fields as the sampling
+ * calls derive them on the device (nsfps_range_derive gives the same bits on
+ * the host).  This is the range nsfps_fps, nsfps_fps_bbox and the batched
+ * calls use when they are given none.  stream: a hipStream_t (NULL = default
+ * stream); the call returns after the stream work completes. */
+nsfps_status nsfps_bbox_device(const float *d_xyz, uint64_t n, uint32_t x_blocks,
+                               uint32_t y_blocks, uint32_t z_blocks, nsfps_range *out,
+                               nsfps_range_info *info, void *stream);
+
 /* FPS of one cloud.  xyz: host pointer, n x 3 float32, C order.  range == NULL
  * selects compute_bbox with the default 16^3 blocks.  out: host buffer of at
  * least n_samples int32 entries; *out_len receives the sample count (smaller
@@ -144,13 +156,26 @@ nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples,
                             uint32_t z_blocks, int32_t *out, uint64_t *out_len);
 
 /* B independent clouds of n points each (xyz: B x n x 3, host).  ranges: B
- * ranges, or NULL for a per-cloud compute_bbox with blocks3 (NULL -> 16^3).
- * out: B x n_samples int32 (row b holds cloud b's samples; entries past
- * out_lens[b] are unspecified); out_lens: B. */
+ * ranges, or NULL for a per-cloud compute_bbox with blocks3 (NULL -> 16^3),
+ * found on the device.  out: B x n_samples int32 (row b holds cloud b's
+ * samples; entries past out_lens[b] are unspecified); out_lens: B.  The
+ * reference samples one cloud per call (yuezu_fps, src/yuezu_fps.cpp:676-730,
+ * with compute_bbox for range=None, yuezu_fps/yuezu_fps_pybind.cpp:74-76);
+ * this is B such calls in one. */
 nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n,
                                uint64_t n_samples, const nsfps_range *ranges,
                                const uint32_t *blocks3, int32_t *out,
                                uint64_t *out_lens);
+
+/* nsfps_fps_batched on device memory: d_xyz (B x n x 3 float32) and d_out
+ * (B x n_samples int32, row b holding cloud b's samples) are device
+ * pointers; ranges, blocks3 and out_lens are host memory as in
+ * nsfps_fps_batched.  stream is a hipStream_t (NULL = default stream); the
+ * call returns after the stream work completes. */
+nsfps_status nsfps_fps_batched_device(const float *d_xyz, uint64_t batch, uint64_t n,
+                                      uint64_t n_samples, const nsfps_range *ranges,
+                                      const uint32_t *blocks3, int32_t *d_out,
+                                      uint64_t *out_lens, void *stream);
 
 /* FPS of one cloud whose points already live in device memory (d_xyz, n x 3
  * float32) writing device memory (d_out, n_samples int32).  stream is a

@@ -109,6 +109,32 @@ class Lib:
                                                out.ctypes.data_as(_vp), lens.ctypes.data_as(_vp)))
         return [out[b, :int(lens[b])].copy() for b in range(B)]
 
+    def fps_batched_device(self, d_xyz, batch, n, n_samples, d_out, ranges=None,
+                           blocks=(16, 16, 16), stream=None):
+        """nsfps_fps_batched_device: batch clouds of n points at d_xyz (device),
+        samples into d_out (device, batch x n_samples int32).  Returns the
+        per-cloud sample counts."""
+        lens = np.zeros(batch, np.uint64)
+        rs = None
+        if ranges is not None:
+            rs = (Range * batch)(*[Range.of(r) for r in ranges])
+        b3 = (ctypes.c_uint32 * 3)(*blocks)
+        self._check(self.lib.nsfps_fps_batched_device(_vp(d_xyz), _u64(batch), _u64(n),
+                                                      _u64(int(n_samples)), rs, b3, _vp(d_out),
+                                                      lens.ctypes.data_as(_vp), _vp(stream)))
+        return [int(v) for v in lens]
+
+    def bbox_device(self, d_xyz, n, blocks=(16, 16, 16), stream=None):
+        """nsfps_bbox_device: compute_bbox of device-resident points, found on
+        the device.  Returns (range tuple, nsfps_range_info bytes)."""
+        r = Range()
+        info = (ctypes.c_char * 256)()
+        self._check(self.lib.nsfps_bbox_device(_vp(d_xyz), _u64(n),
+                                               *[ctypes.c_uint32(b) for b in blocks],
+                                               ctypes.byref(r), info, _vp(stream)))
+        return ((r.min_x, r.max_x, r.min_y, r.max_y, r.min_z, r.max_z,
+                 r.x_blocks, r.y_blocks, r.z_blocks), bytes(info))
+
     def fps_device(self, d_xyz, n, n_samples, rng, d_out, stream=None):
         n_out = _u64()
         self._check(self.lib.nsfps_fps_device(_vp(d_xyz), _u64(n), _u64(int(n_samples)),

@@ -43,6 +43,115 @@ __device__ __forceinline__ void cell_keys_at(uint32_t i, const float *__restrict
   if (counts) atomicAdd(&counts[b], 1u);  // null: counted from the sorted buckets instead
 }
 
+// The same from a range in device memory (computed on the device from the
+// points' bounds, before the host knows it).
+__global__ void k_cell_keys_dr(const float *__restrict__ xyz, uint32_t n,
+                               const RangeDev *__restrict__ rp, const uint32_t *__restrict__ lut,
+                               uint32_t *__restrict__ bucket, uint32_t *__restrict__ fine,
+                               uint32_t *__restrict__ counts, uint32_t *__restrict__ bad) {
+  const RangeDev r = *rp;
+  cell_keys_at(blockIdx.x * blockDim.x + threadIdx.x, xyz, n, r, lut, bucket, fine, counts, bad);
+}
+
+// --- compute_bbox on the device (src/yuezu_fps.cpp:643-670) ---------------
+//
+// The reference keeps a running (v < mn ? v : mn) and (mx < v ? v : mx) from
+// point 0 and uses only min - BOUNDARY_EPS and max + BOUNDARY_EPS.  Minimum
+// and maximum of finite values do not depend on the order (a zero's sign is
+// the only order-dependent bit, and +-0 - 1e-6 and +-0 + 1e-6 do not keep
+// it), so per-cloud atomics on order-preserving integers give the same
+// bounds.  Non-finite points are skipped here; the cell-key pass flags them
+// and the call is refused.
+
+// ord_lo[3 b + a] / ord_hi[3 b + a]: ord_of(min) / ord_of(max) of axis a of
+// cloud b over its finite points (ord_lo starts at 0xffffffff, ord_hi at 0).
+// Grid (workgroups per cloud, clouds); the clouds lie one after another.
+__global__ __launch_bounds__(256) void k_cloud_bounds(const float *__restrict__ xyz,
+                                                      uint32_t n_per,
+                                                      uint32_t *__restrict__ ord_lo,
+                                                      uint32_t *__restrict__ ord_hi) {
+  const uint32_t b = blockIdx.y;
+  const float *const c = xyz + (size_t)b * n_per * 3;
+  uint32_t lo[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, hi[3] = {0u, 0u, 0u};
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n_per; i += gridDim.x * blockDim.x) {
+    const float v[3] = {c[3 * (size_t)i], c[3 * (size_t)i + 1], c[3 * (size_t)i + 2]};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      if (!isfinite(v[a])) continue;
+      const uint32_t o = ord_of(v[a]);
+      lo[a] = lo[a] < o ? lo[a] : o;
+      hi[a] = hi[a] > o ? hi[a] : o;
+    }
+  }
+  // one atomic per value and workgroup (contended atomics on one address
+  // serialise)
+  __shared__ uint32_t s_b[4][6];
+  const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const uint32_t l = wave_min_u32(lo[a]), h = wave_max_u32(hi[a]);
+    if ((threadIdx.x & 63u) == 0) {
+      s_b[wave][a] = l;
+      s_b[wave][3 + a] = h;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const uint32_t a = threadIdx.x;
+    uint32_t v = s_b[0][a];
+    for (uint32_t w = 1; w < 4; ++w) v = a < 3 ? min(v, s_b[w][a]) : max(v, s_b[w][a]);
+    if (a < 3) atomicMin(&ord_lo[3 * b + a], v);
+    else atomicMax(&ord_hi[3 * b + a - 3], v);
+  }
+}
+
+// The range of cloud blockIdx.x from its bounds: min - 1e-6 and max + 1e-6
+// per axis (an axis without a finite point gets 0 +- 1e-6), then make_range's
+// derivation (src/yuezu_fps.cpp:136-161) in the host's fp32 operations:
+// block size (max - min) / blocks, inv_bs = 1 / block size, the clamp bound
+// max - 1e-6, and the cube thresholds.  tmpl holds the fields that depend on
+// the block counts alone.  out[b] gets the range, bounds[6 b ..] its min x,
+// max x, min y, max y, min z, max z; with bd, bd[b].c.r gets it too.  One
+// wave per cloud: lane 3 k + a searches threshold k of axis a.
+__global__ __launch_bounds__(64) void k_range_of_bounds(const uint32_t *__restrict__ ord_lo,
+                                                        const uint32_t *__restrict__ ord_hi,
+                                                        RangeDev tmpl, RangeDev *__restrict__ out,
+                                                        float *__restrict__ bounds,
+                                                        BuildDev *__restrict__ bd) {
+  const uint32_t b = blockIdx.x, lane = threadIdx.x;
+  constexpr float kEps = 1e-6f;  // BOUNDARY_EPS, src/yuezu_fps.h:43-45
+  float mn[3], mx[3], bs[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const uint32_t lo = ord_lo[3 * b + a], hi = ord_hi[3 * b + a];
+    const bool any = lo <= hi;
+    mn[a] = (any ? float_of(lo) : 0.f) - kEps;
+    mx[a] = (any ? float_of(hi) : 0.f) + kEps;
+    bs[a] = (mx[a] - mn[a]) / (float)tmpl.blocks[a];
+  }
+  __shared__ float s_thr[3][kCubeThr];
+  if (lane < 3 * kCubeThr) {
+    const uint32_t a = lane % 3, k = lane / 3;
+    s_thr[a][k] = cube_threshold_dev(bs[a], tmpl.blocks[a], k + 1);
+  }
+  __syncthreads();
+  if (lane != 0) return;
+  RangeDev r = tmpl;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    r.mn[a] = mn[a];
+    r.hiclamp[a] = mx[a] - kEps;
+    r.bsize[a] = bs[a];
+    r.inv_bs[a] = 1.0f / bs[a];
+#pragma unroll
+    for (uint32_t k = 0; k < kCubeThr; ++k) r.cube_thr[a][k] = s_thr[a][k];
+    bounds[6 * b + 2 * a] = mn[a];
+    bounds[6 * b + 2 * a + 1] = mx[a];
+  }
+  out[b] = r;
+  if (bd) bd[b].c.r = r;
+}
+
 // Bucket populations from the buckets sorted: each bucket's points are one
 // run; the run's first element adds -(its position) and its last element
 // adds its position + 1, so every bucket takes at most two atomics, never
@@ -594,6 +703,30 @@ hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, con
 }
 
 uint32_t scan_tmp_len(uint32_t len) { return cdiv(len, kScanChunk) + 1; }
+
+hipError_t launch_cell_keys_dr(const float *xyz, uint32_t n, const RangeDev *d_range,
+                               const uint32_t *lut, uint32_t *bucket, uint32_t *fine,
+                               uint32_t *counts, uint32_t *bad, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  k_cell_keys_dr<<<cdiv(n, 256), 256, 0, st>>>(xyz, n, d_range, lut, bucket, fine, counts, bad);
+  return hipGetLastError();
+}
+
+hipError_t launch_device_ranges(const float *xyz, uint32_t n_per, uint32_t nclouds,
+                                const RangeDev &tmpl, uint32_t *ord, RangeDev *out,
+                                float *bounds, BuildDev *bd, hipStream_t st) {
+  if (nclouds == 0) return hipSuccess;
+  const hipError_t e = launch_fill_u32(ord, 0xffffffffu, 3ull * nclouds, st);
+  if (e != hipSuccess) return e;
+  const hipError_t e2 = launch_fill_u32(ord + 3ull * nclouds, 0u, 3ull * nclouds, st);
+  if (e2 != hipSuccess) return e2;
+  // about 64 points per thread, at most 64 workgroups per cloud
+  const uint32_t per = n_per ? cdiv(n_per, 256 * 64) : 1;
+  k_cloud_bounds<<<dim3(per < 64 ? per : 64, nclouds), 256, 0, st>>>(xyz, n_per, ord,
+                                                                      ord + 3ull * nclouds);
+  k_range_of_bounds<<<nclouds, 64, 0, st>>>(ord, ord + 3ull * nclouds, tmpl, out, bounds, bd);
+  return hipGetLastError();
+}
 
 hipError_t launch_scan(uint32_t *data, uint32_t len, uint32_t *tmp, hipStream_t st) {
   if (len <= kScanSingleMax) {

@@ -168,6 +168,35 @@ __device__ __forceinline__ int cube_half(float D, float bs, uint32_t blocks) {
   return (int)f;
 }
 
+// Order-preserving map of floats to unsigned integers (finite values), and
+// back: atomicMin / atomicMax on the integers give the floats' minimum and
+// maximum in any order of arrival.
+__device__ __forceinline__ uint32_t ord_of(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float float_of(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+// Smallest D >= 0 whose clipped cube half-width, min(cube_half(D), blocks -
+// 1), is at least k1 (INFINITY when none is): the half-width is monotone in D
+// and non-negative floats order like their bit patterns, so a binary search
+// over the bits finds it.  The host derives the same table with the same
+// arithmetic (correctly rounded sqrtf and division).
+__device__ __forceinline__ float cube_threshold_dev(float bs, uint32_t blocks, uint32_t k1) {
+  if (k1 > blocks - 1) return INFINITY;
+  uint32_t lo = 0, hi = 0x7f800000u;  // +inf: half-width blocks - 1 >= k1
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    const int h = cube_half(__uint_as_float(mid), bs, blocks);
+    const uint32_t hc = (uint32_t)h < blocks - 1 ? (uint32_t)h : blocks - 1;
+    if (hc >= k1) hi = mid;
+    else lo = mid + 1;
+  }
+  return __uint_as_float(lo);
+}
+
 struct Cube {
   int lo[3], hi[3];
 };

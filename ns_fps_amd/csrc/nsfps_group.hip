@@ -89,15 +89,6 @@ __global__ __launch_bounds__(256) void k_ball_query(const float *__restrict__ xy
 
 // ---- grid path
 
-// Order-preserving map of floats to unsigned integers (finite values).
-__device__ __forceinline__ uint32_t ord_of(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float float_of(uint32_t o) {
-  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-}
-
 // bnd[0..2]: ord(min) per axis (start 0xffffffff), bnd[3..5]: ord(max) (start 0),
 // over the finite points
 __global__ __launch_bounds__(256) void k_bq_bounds(const float *__restrict__ xyz, uint32_t n,

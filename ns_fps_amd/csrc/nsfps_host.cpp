@@ -105,7 +105,12 @@ uint32_t cube_half_host(float D, float bs, uint32_t blocks) {
 // Smallest D >= 0 whose half-width is at least k1 (INFINITY when none is).
 // The half-width is monotone in D (sqrtf, division by a positive value and
 // ceilf are monotone), and non-negative floats order like their bit
-// patterns, so a binary search over the bits finds the first one.
+// patterns, so the answer is the first bit pattern where the predicate
+// turns true.  It lies within a few ulps of (k1 - 1 ... k1) * bs squared:
+// the walk starts at the estimate and steps one ulp at a time, checking the
+// predicate on both sides of the boundary it stops at; a binary search over
+// the bits settles the rare case the walk does not (the same answer: the
+// predicate is monotone).
 float cube_threshold(float bs, uint32_t blocks, uint32_t k1) {
   if (k1 > blocks - 1) return INFINITY;
   auto as_float = [](uint32_t u) {
@@ -113,26 +118,51 @@ float cube_threshold(float bs, uint32_t blocks, uint32_t k1) {
     memcpy(&f, &u, 4);
     return f;
   };
+  auto as_bits = [](float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+  };
+  auto at_least = [&](uint32_t u) { return cube_half_host(as_float(u), bs, blocks) >= k1; };
+  const float est = ((float)(k1 - 1) * bs) * ((float)(k1 - 1) * bs);
+  if (std::isfinite(est) && est >= 0.0f) {
+    uint32_t u = as_bits(est);
+    constexpr int kWalk = 64;
+    bool found = false;
+    if (at_least(u)) {
+      for (int i = 0; i < kWalk; ++i) {
+        if (u == 0 || !at_least(u - 1)) {
+          found = true;
+          break;
+        }
+        --u;
+      }
+    } else {
+      for (int i = 0; i < kWalk && u < 0x7f800000u; ++i) {
+        ++u;
+        if (at_least(u)) {
+          found = true;
+          break;
+        }
+      }
+    }
+    if (found) return as_float(u);
+  }
   uint32_t lo = 0, hi = 0x7f800000u;  // +inf: half-width blocks - 1 >= k1
   while (lo < hi) {
     const uint32_t mid = lo + (hi - lo) / 2;
-    if (cube_half_host(as_float(mid), bs, blocks) >= k1) hi = mid;
+    if (at_least(mid)) hi = mid;
     else lo = mid + 1;
   }
   return as_float(lo);
 }
 
-// make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
-// _compute_bit_positions/_generate_morton_lut (:52-97).
-void derive(const nsfps_range &r, HostRange &h) {
-  h.prim = r;
-  const float mn[3] = {r.min_x, r.min_y, r.min_z};
-  const float mx[3] = {r.max_x, r.max_y, r.max_z};
-  const uint32_t bl[3] = {r.x_blocks, r.y_blocks, r.z_blocks};
+// The make_range fields that depend on the block counts alone
+// (src/yuezu_fps.cpp:45-97, 136-161): bits, Morton bit positions and LUTs,
+// bucket count, and how many cells a bucket holds.
+void derive_blocks(const uint32_t bl[3], HostRange &h) {
   uint32_t tb = 0;
   for (int a = 0; a < 3; ++a) {
-    h.info.inv_bs[a] = 1.0f / ((mx[a] - mn[a]) / (float)bl[a]);
-    h.info.block_size[a] = (mx[a] - mn[a]) / (float)bl[a];
     h.info.bits[a] = calc_bits(bl[a]);
     tb += h.info.bits[a];
   }
@@ -162,10 +192,6 @@ void derive(const nsfps_range &r, HostRange &h) {
   bool bij = true;
   uint32_t off = 0;
   for (int a = 0; a < 3; ++a) {
-    d.mn[a] = mn[a];
-    d.hiclamp[a] = mx[a] - kBoundaryEps;
-    d.inv_bs[a] = h.info.inv_bs[a];
-    d.bsize[a] = h.info.block_size[a];
     d.blocks[a] = bl[a];
     d.lut_off[a] = off;
     off += 1u << h.info.bits[a];
@@ -197,13 +223,39 @@ void derive(const nsfps_range &r, HostRange &h) {
     }
     d.na = na;
   }
+}
+
+// The fp32 fields of make_range (src/yuezu_fps.cpp:136-161): block size,
+// inv_bs = 1.0f / ((max - min) / blocks), the clamp bound max - 1e-6, and
+// the cube half-width thresholds.  The block counts are derived already.
+void derive_floats(const nsfps_range &r, HostRange &h) {
+  h.prim = r;
+  const float mn[3] = {r.min_x, r.min_y, r.min_z};
+  const float mx[3] = {r.max_x, r.max_y, r.max_z};
+  RangeDev &d = h.dev;
+  for (int a = 0; a < 3; ++a) {
+    h.info.inv_bs[a] = 1.0f / ((mx[a] - mn[a]) / (float)d.blocks[a]);
+    h.info.block_size[a] = (mx[a] - mn[a]) / (float)d.blocks[a];
+    d.mn[a] = mn[a];
+    d.hiclamp[a] = mx[a] - kBoundaryEps;
+    d.inv_bs[a] = h.info.inv_bs[a];
+    d.bsize[a] = h.info.block_size[a];
+  }
   static_assert(kCubeThr == NSFPS_CUBE_THRESHOLDS, "threshold count");
   for (int a = 0; a < 3; ++a)
     for (uint32_t k = 0; k < kCubeThr; ++k) {
-      const float t = cube_threshold(h.info.block_size[a], bl[a], k + 1);
+      const float t = cube_threshold(h.info.block_size[a], d.blocks[a], k + 1);
       h.info.cube_thr[a][k] = t;
       d.cube_thr[a][k] = t;
     }
+}
+
+// make_range derivation (src/yuezu_fps.cpp:136-161) plus the LUTs of
+// _compute_bit_positions/_generate_morton_lut (:52-97).
+void derive(const nsfps_range &r, HostRange &h) {
+  const uint32_t bl[3] = {r.x_blocks, r.y_blocks, r.z_blocks};
+  derive_blocks(bl, h);
+  derive_floats(r, h);
 }
 
 // compute_bbox (src/yuezu_fps.cpp:648-670) keeps, per axis, the running
@@ -513,6 +565,9 @@ struct CloudPlan {
   uint32_t *d_bucket = nullptr, *d_fine = nullptr;  // per point: bucket, sub-cell code
   uint64_t cap = 0;                // slots per bucket in the padded layout
   bool tree = false;               // sampled by the tree engine (its loop holds level 1 in LDS)
+  // the range is compute_bbox of the points with rng's block counts, found on
+  // the device by the build (rng holds the block-count fields until then)
+  bool bbox_dev = false;
   std::vector<uint32_t> lut_host;  // source of an asynchronous copy: lives until the sync
 };
 
@@ -640,6 +695,11 @@ LdsPlan plan_lds(const CloudDev &c) {
 struct CallBuffers {
   float *xyz_stage = nullptr;
   uint32_t *counts = nullptr, *small = nullptr, *bucket = nullptr, *fine = nullptr;
+  // ranges found on the device: bounds as order-preserving integers (6 per
+  // cloud), the ranges, and their bounds as floats (6 per cloud)
+  uint32_t *ord = nullptr;
+  RangeDev *drng = nullptr;
+  float *dbounds = nullptr;
   BuildDev *bd = nullptr;  // per-cloud parameters of the many-cloud build steps
   int32_t *out = nullptr;  // every cloud's samples, m entries per cloud
   size_t n_total = 0, counts_total = 0;
@@ -659,6 +719,9 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   cb.bucket = bp.take<uint32_t>(cb.n_total);
   cb.fine = bp.take<uint32_t>(cb.n_total);
   cb.bd = bp.take<BuildDev>(plans.size());
+  cb.ord = bp.take<uint32_t>(6 * plans.size());
+  cb.drng = bp.take<RangeDev>(plans.size());
+  cb.dbounds = bp.take<float>(6 * plans.size());
   // the clouds' outputs back to back, rows of m entries: one read-back
   size_t outs = 0;
   for (auto &p : plans) outs += p.m;
@@ -708,7 +771,7 @@ nsfps_status sort_logical(const uint32_t *bucket, uint32_t n_per, uint32_t nclou
 // buckets in *keys) and the bucket populations are counted from that order,
 // not by an atomic per point (contended where points crowd into few buckets).
 nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &s, hipStream_t st,
-                          bool sorted = false, uint32_t **keys = nullptr,
+                          const RangeDev *d_range, bool sorted = false, uint32_t **keys = nullptr,
                           uint32_t **lorig = nullptr) {
   const uint32_t T = p.rng.dev.T;
   if (lut_of) {
@@ -721,8 +784,12 @@ nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &
     HIP_TRY(hipMemcpyAsync(p.d_lut, lut.data(), lut.size() * 4, hipMemcpyHostToDevice, st));
   }
   const float *xyz = p.h_xyz ? p.d_xyz_stage : p.d_xyz_in;
-  HIP_TRY(launch_cell_keys(xyz, p.n, p.rng.dev, p.d_lut, p.d_bucket, p.d_fine,
-                           sorted ? nullptr : p.d_counts, p.d_small, st));
+  if (p.bbox_dev)  // the range is in device memory, found from the points' bounds
+    HIP_TRY(launch_cell_keys_dr(xyz, p.n, d_range, p.d_lut, p.d_bucket, p.d_fine,
+                                sorted ? nullptr : p.d_counts, p.d_small, st));
+  else
+    HIP_TRY(launch_cell_keys(xyz, p.n, p.rng.dev, p.d_lut, p.d_bucket, p.d_fine,
+                             sorted ? nullptr : p.d_counts, p.d_small, st));
   if (sorted) {
     nsfps_status rc = sort_logical(p.d_bucket, p.n, 1, 0, std::max(1, key_bits_for(T)), s, st,
                                    keys, lorig);
@@ -915,6 +982,35 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   const bool together = sort_together(plans, &cbits, &bbits);
   const bool many = together && tmax <= kManyMaxBuckets;
   bd.assign(many ? nc : 0, BuildDev{});
+  // compute_bbox on the device for the clouds that ask for it: one launch
+  // when they all do and lie one after another, else one per cloud.  With
+  // d_bd each range also goes into the cloud's build parameters.
+  const auto xyz_of = [&](size_t i) {
+    return plans[i].h_xyz ? (const float *)plans[i].d_xyz_stage : plans[i].d_xyz_in;
+  };
+  bool any_dev = false, one_launch = true;
+  for (size_t i = 0; i < nc; ++i) {
+    any_dev = any_dev || plans[i].bbox_dev;
+    one_launch = one_launch && plans[i].bbox_dev && plans[i].n == plans[0].n &&
+                 xyz_of(i) == xyz_of(0) + i * (size_t)plans[0].n * 3;
+  }
+  const auto device_ranges = [&](BuildDev *d_bd) -> nsfps_status {
+    if (one_launch) {
+      HIP_TRY(launch_device_ranges(xyz_of(0), plans[0].n, (uint32_t)nc, plans[0].rng.dev, cb.ord,
+                                   cb.drng, cb.dbounds, d_bd, st));
+      return NSFPS_OK;
+    }
+    for (size_t i = 0; i < nc; ++i)
+      if (plans[i].bbox_dev)
+        HIP_TRY(launch_device_ranges(xyz_of(i), plans[i].n, 1, plans[i].rng.dev, cb.ord + 6 * i,
+                                     cb.drng + i, cb.dbounds + 6 * i, d_bd ? d_bd + i : nullptr,
+                                     st));
+    return NSFPS_OK;
+  };
+  if (any_dev && !many) {
+    const nsfps_status rc = device_ranges(nullptr);
+    if (rc) return rc;
+  }
   uint32_t *keys1 = nullptr, *lorig1 = nullptr;  // one cloud: its sort by bucket
   for (size_t i = 0; i < nc; ++i) {
     const CloudPlan *lut_of = nullptr;
@@ -948,16 +1044,47 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     }
     // one cloud: sorted by bucket before the layout is decided (the sort's
     // scratch buffers then stay untouched until its finish)
-    nsfps_status rc = build_phase1(plans[i], lut_of, s, st, nc == 1, &keys1, &lorig1);
+    nsfps_status rc = build_phase1(plans[i], lut_of, s, st, cb.drng + i, nc == 1, &keys1, &lorig1);
     if (rc) return rc;
   }
   if (many) {
     HIP_TRY(hipMemcpyAsync(cb.bd, bd.data(), nc * sizeof(BuildDev), hipMemcpyHostToDevice, st));
+    if (any_dev) {
+      const nsfps_status rc = device_ranges(cb.bd);
+      if (rc) return rc;
+    }
     HIP_TRY(launch_build_first_many(cb.bd, (uint32_t)nc, nmax, tmax, st));
   }
   std::vector<uint32_t> hs(4 * nc);
+  std::vector<float> hb(any_dev ? 6 * nc : 0);
+  std::vector<RangeDev> hr(any_dev ? nc : 0);
   HIP_TRY(hipMemcpyAsync(hs.data(), cb.small, nc * 16, hipMemcpyDeviceToHost, st));
+  if (any_dev) {
+    HIP_TRY(hipMemcpyAsync(hb.data(), cb.dbounds, hb.size() * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(hr.data(), cb.drng, nc * sizeof(RangeDev), hipMemcpyDeviceToHost, st));
+  }
   HIP_TRY(hipStreamSynchronize(st));
+  for (size_t i = 0; i < nc; ++i)
+    if (hs[4 * i]) return fail(NSFPS_EINVAL, "points must be finite");
+  // the ranges found on the device: checked as a range given by the caller
+  // would be, and kept for the rest of the build and the sampling
+  for (size_t i = 0; i < nc && any_dev; ++i) {
+    CloudPlan &p = plans[i];
+    if (!p.bbox_dev) continue;
+    const float *b6 = &hb[6 * i];
+    nsfps_range prim{b6[0], b6[1], b6[2], b6[3], b6[4], b6[5], p.rng.dev.blocks[0],
+                     p.rng.dev.blocks[1], p.rng.dev.blocks[2]};
+    const nsfps_status rc = check_range(prim);
+    if (rc) return rc;
+    p.rng.prim = prim;
+    p.rng.dev = hr[i];
+    for (int a = 0; a < 3; ++a) {
+      p.rng.info.inv_bs[a] = hr[i].inv_bs[a];
+      p.rng.info.block_size[a] = hr[i].bsize[a];
+      for (uint32_t k = 0; k < kCubeThr; ++k) p.rng.info.cube_thr[a][k] = hr[i].cube_thr[a][k];
+    }
+    p.dev.r = hr[i];
+  }
   const bool mixed = mixed_wanted(plans, hs.data());
   for (size_t i = 0; i < nc; ++i) {
     nsfps_status rc = decide_layout(plans[i], &hs[4 * i], mixed);
@@ -1163,6 +1290,7 @@ struct Ws {
   size_t cap = 0;
   hipStream_t st = nullptr;
   const hipEvent_t *ev = nullptr;
+  bool st_used = false;  // work of the call was enqueued on st
 };
 
 // Where one call's buffers live: per cloud (layout_cloud), for the call
@@ -1327,10 +1455,27 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
 
 // One call from start to end over workspace ws: layout, build, sampling,
 // results.  ws.base == null takes the calling thread's device arena.
+// layout_out: where the call's buffers lie, for callers that copy from them.
+// A call that fails after enqueuing work waits for its stream before
+// returning, so that no kernel of it still runs when the next call reuses the
+// workspace (the wait's own status is ignored: the first error is reported).
+nsfps_status run_clouds_once(std::vector<CloudPlan> &plans, Ws &ws, bool out_on_host,
+                             int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
+                             CallLayout &L);
+
 nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, int32_t *h_out,
-                        uint64_t out_stride, uint64_t *out_lens) {
-  auto t0 = std::chrono::steady_clock::now();
+                        uint64_t out_stride, uint64_t *out_lens, CallLayout *layout_out = nullptr) {
   CallLayout L;
+  const nsfps_status rc = run_clouds_once(plans, ws, out_on_host, h_out, out_stride, out_lens, L);
+  if (rc && ws.st_used) (void)hipStreamSynchronize(ws.st);
+  if (layout_out) *layout_out = L;
+  return rc;
+}
+
+nsfps_status run_clouds_once(std::vector<CloudPlan> &plans, Ws &ws, bool out_on_host,
+                             int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
+                             CallLayout &L) {
+  auto t0 = std::chrono::steady_clock::now();
   const size_t need = measure_call(plans, L);
   if (!ws.base) {
     Arena *ap = nullptr;
@@ -1351,6 +1496,7 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, 
   layout_all(bp, plans, L);
   const bool runs = choose_runs(plans);
   hipStream_t st = ws.st;
+  ws.st_used = true;
   if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[0], st));
   std::vector<BuildDev> bd_host;  // lives until the stream is synchronised below
   nsfps_status rc = build_clouds(plans, L.cb, L.sc, bd_host, st);
@@ -1514,52 +1660,103 @@ nsfps_status nsfps_bbox(const float *xyz, uint64_t n, uint32_t xb, uint32_t yb, 
   });
 }
 
-static nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m,
-                                    const nsfps_range *range, int32_t *out, uint64_t *out_len) {
+namespace {
+
+// The range of a call without one: compute_bbox of the points with these
+// block counts (found on the device by the build).  Checks the block counts
+// as check_range would, on placeholder bounds.
+nsfps_status check_blocks(const uint32_t bl[3]) {
+  const nsfps_range r{0.f, 1.f, 0.f, 1.f, 0.f, 1.f, bl[0], bl[1], bl[2]};
+  return check_range(r);
+}
+
+// Clouds of one call, each with range[b] (or, range == null, compute_bbox
+// of its points with block counts bl on the device).  The block-count part
+// of the derivation is shared by clouds with the same counts.
+nsfps_status plan_clouds(std::vector<CloudPlan> &plans, uint64_t n, uint64_t m,
+                         const nsfps_range *ranges, const uint32_t bl[3]) {
+  for (size_t b = 0; b < plans.size(); ++b) {
+    CloudPlan &p = plans[b];
+    p.n = (uint32_t)n;
+    p.m = (uint32_t)m;
+    const uint32_t mine[3] = {ranges ? ranges[b].x_blocks : bl[0],
+                              ranges ? ranges[b].y_blocks : bl[1],
+                              ranges ? ranges[b].z_blocks : bl[2]};
+    const HostRange &prev = plans[b ? b - 1 : 0].rng;
+    if (b > 0 && prev.dev.blocks[0] == mine[0] && prev.dev.blocks[1] == mine[1] &&
+        prev.dev.blocks[2] == mine[2])
+      p.rng = prev;  // the LUTs and the other block-count fields
+    else
+      derive_blocks(mine, p.rng);
+    if (ranges) derive_floats(ranges[b], p.rng);
+    p.bbox_dev = ranges == nullptr;
+  }
+  return NSFPS_OK;
+}
+
+// nsfps_fps / nsfps_fps_bbox: range, or (range == null) compute_bbox with
+// block counts bl.
+nsfps_status fps_host_common(const float *xyz, uint64_t n, uint64_t m, const nsfps_range *range,
+                             const uint32_t bl[3], int32_t *out, uint64_t *out_len) {
   reset_stats();
   if (!out_len || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
   if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
-  nsfps_range r = *range;
-  nsfps_status rc = check_range(r);
+  if (!range && n == 0) {  // compute_bbox of no points: nothing to sample
+    *out_len = 0;
+    return NSFPS_OK;
+  }
+  nsfps_status rc = range ? check_range(*range) : check_blocks(bl);
   if (rc) return rc;
   if (trivial(n, m, out, out_len)) return NSFPS_OK;
   std::lock_guard<std::mutex> lk(g_mu);
   std::vector<CloudPlan> plans(1);
-  CloudPlan &p = plans[0];
-  p.n = (uint32_t)n;
-  p.m = (uint32_t)m;
-  derive(r, p.rng);
-  p.h_xyz = xyz;
+  rc = plan_clouds(plans, n, m, range, bl);
+  if (rc) return rc;
+  plans[0].h_xyz = xyz;
   return run_clouds(plans, Ws{}, true, out, 0, out_len);
 }
+
+// Argument checks of the batched calls; *blocks gets the block counts of a
+// call without ranges.
+nsfps_status check_batched(const float *xyz, uint64_t batch, uint64_t n, uint64_t m,
+                           const nsfps_range *ranges, const uint32_t *blocks3, const void *out,
+                           const uint64_t *out_lens, uint32_t blocks[3]) {
+  if (!out_lens || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
+  if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+  if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
+  if (m && batch * m > 0x7fffffffull)
+    return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 samples per call");
+  blocks[0] = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
+  blocks[1] = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
+  blocks[2] = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
+  if (ranges) {
+    for (uint64_t b = 0; b < batch; ++b) {
+      const nsfps_status rc = check_range(ranges[b]);
+      if (rc) return rc;
+    }
+  } else if (n) {
+    const nsfps_status rc = check_blocks(blocks);
+    if (rc) return rc;
+  }
+  return NSFPS_OK;
+}
+
+}  // namespace
 
 nsfps_status nsfps_fps(const float *xyz, uint64_t n, uint64_t n_samples, const nsfps_range *range,
                        int32_t *out, uint64_t *out_len) {
   return guarded([&]() -> nsfps_status {
-    nsfps_range r;
-    if (range) {
-      r = *range;
-    } else {
-      if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
-      bbox_of(xyz, n, r);
-      if (n) r.x_blocks = r.y_blocks = r.z_blocks = NSFPS_DEFAULT_X_BLOCKS;
-    }
-    return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+    const uint32_t bl[3] = {NSFPS_DEFAULT_X_BLOCKS, NSFPS_DEFAULT_Y_BLOCKS,
+                            NSFPS_DEFAULT_Z_BLOCKS};
+    return fps_host_common(xyz, n, n_samples, range, bl, out, out_len);
   });
 }
 
 nsfps_status nsfps_fps_bbox(const float *xyz, uint64_t n, uint64_t n_samples, uint32_t xb,
                             uint32_t yb, uint32_t zb, int32_t *out, uint64_t *out_len) {
   return guarded([&]() -> nsfps_status {
-    if (n && !xyz) return fail(NSFPS_EINVAL, "null pointer");
-    nsfps_range r;
-    bbox_of(xyz, n, r);
-    if (n) {
-      r.x_blocks = xb;
-      r.y_blocks = yb;
-      r.z_blocks = zb;
-    }
-    return fps_host_common(xyz, n, n_samples, &r, out, out_len);
+    const uint32_t bl[3] = {xb, yb, zb};
+    return fps_host_common(xyz, n, n_samples, nullptr, bl, out, out_len);
   });
 }
 
@@ -1569,41 +1766,113 @@ nsfps_status nsfps_fps_batched(const float *xyz, uint64_t batch, uint64_t n, uin
   return guarded([&]() -> nsfps_status {
     reset_stats();
     if (batch == 0) return NSFPS_OK;
-    if (!out_lens || (m && !out) || (n && !xyz)) return fail(NSFPS_EINVAL, "null pointer");
-    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
-    if (batch > 65535) return fail(NSFPS_EUNSUPPORTED, "at most 65535 clouds per call");
-    std::vector<nsfps_range> rs(batch);
-    if (!ranges) bboxes(xyz, batch, n, rs.data());
-    for (uint64_t b = 0; b < batch; ++b) {
-      if (ranges) {
-        rs[b] = ranges[b];
-      } else if (n) {
-        rs[b].x_blocks = blocks3 ? blocks3[0] : NSFPS_DEFAULT_X_BLOCKS;
-        rs[b].y_blocks = blocks3 ? blocks3[1] : NSFPS_DEFAULT_Y_BLOCKS;
-        rs[b].z_blocks = blocks3 ? blocks3[2] : NSFPS_DEFAULT_Z_BLOCKS;
+    uint32_t bl[3];
+    nsfps_status rc = check_batched(xyz, batch, n, m, ranges, blocks3, out, out_lens, bl);
+    if (rc) return rc;
+    // every cloud has n points and m samples: all are trivial, or none
+    uint64_t len = 0;
+    if (trivial(n, m, out, &len)) {
+      for (uint64_t b = 0; b < batch; ++b) {
+        if (b) trivial(n, m, out + b * m, &len);
+        out_lens[b] = len;
       }
-      nsfps_status rc = check_range(rs[b]);
-      if (rc) return rc;
+      return NSFPS_OK;
     }
-    bool all_trivial = true;
-    for (uint64_t b = 0; b < batch; ++b) {
-      uint64_t len = 0;
-      if (!trivial(n, m, out + b * m, &len)) {
-        all_trivial = false;
-        break;
-      }
-      out_lens[b] = len;
-    }
-    if (all_trivial) return NSFPS_OK;
     std::lock_guard<std::mutex> lk(g_mu);
     std::vector<CloudPlan> plans(batch);
-    for (uint64_t b = 0; b < batch; ++b) {
-      plans[b].n = (uint32_t)n;
-      plans[b].m = (uint32_t)m;
-      derive(rs[b], plans[b].rng);
-      plans[b].h_xyz = xyz + b * n * 3;
-    }
+    rc = plan_clouds(plans, n, m, ranges, bl);
+    if (rc) return rc;
+    for (uint64_t b = 0; b < batch; ++b) plans[b].h_xyz = xyz + b * n * 3;
     return run_clouds(plans, Ws{}, true, out, m, out_lens);
+  });
+}
+
+nsfps_status nsfps_fps_batched_device(const float *d_xyz, uint64_t batch, uint64_t n, uint64_t m,
+                                      const nsfps_range *ranges, const uint32_t *blocks3,
+                                      int32_t *d_out, uint64_t *out_lens, void *stream) {
+  return guarded([&]() -> nsfps_status {
+    reset_stats();
+    if (batch == 0) return NSFPS_OK;
+    uint32_t bl[3];
+    nsfps_status rc = check_batched(d_xyz, batch, n, m, ranges, blocks3, d_out, out_lens, bl);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    hipStream_t st = (hipStream_t)stream;
+    uint64_t len = 0;
+    std::vector<int32_t> one((size_t)std::max<uint64_t>(std::min(n, m), 1));
+    if (trivial(n, m, one.data(), &len)) {  // the same rows for every cloud
+      for (uint64_t b = 0; b < batch; ++b) {
+        out_lens[b] = len;
+        if (len)
+          HIP_TRY(hipMemcpyAsync(d_out + b * m, one.data(), len * 4, hipMemcpyHostToDevice, st));
+      }
+      HIP_TRY(hipStreamSynchronize(st));
+      return NSFPS_OK;
+    }
+    std::vector<CloudPlan> plans(batch);
+    rc = plan_clouds(plans, n, m, ranges, bl);
+    if (rc) return rc;
+    for (uint64_t b = 0; b < batch; ++b) plans[b].d_xyz_in = d_xyz + b * n * 3;
+    Ws ws;
+    ws.st = st;
+    CallLayout L;
+    rc = run_clouds(plans, ws, false, nullptr, 0, out_lens, &L);
+    if (rc) return rc;
+    // the clouds' rows of m entries lie back to back in the call's output
+    HIP_TRY(hipMemcpyAsync(d_out, L.cb.out, batch * m * 4, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return NSFPS_OK;
+  });
+}
+
+nsfps_status nsfps_bbox_device(const float *d_xyz, uint64_t n, uint32_t xb, uint32_t yb,
+                               uint32_t zb, nsfps_range *out, nsfps_range_info *info,
+                               void *stream) {
+  return guarded([&]() -> nsfps_status {
+    if (!out || (n && !d_xyz)) return fail(NSFPS_EINVAL, "null pointer");
+    if (n > 0x7fffffffull) return fail(NSFPS_EUNSUPPORTED, "at most 2^31-1 points per cloud");
+    const uint32_t bl[3] = {xb, yb, zb};
+    HostRange h;
+    if (n == 0) {  // compute_bbox of no points, as nsfps_bbox gives it
+      bbox_of(d_xyz, 0, *out);
+      derive(*out, h);
+      if (info) *info = h.info;
+      return NSFPS_OK;
+    }
+    nsfps_status rc = check_blocks(bl);
+    if (rc) return rc;
+    derive_blocks(bl, h);
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    rc = arena_for_device(&ap);
+    if (rc) return rc;
+    Bump meas(nullptr);
+    meas.take<uint32_t>(6);
+    meas.take<RangeDev>(1);
+    meas.take<float>(6);
+    rc = arena_reserve(*ap, meas.off);
+    if (rc) return rc;
+    Bump bp(ap->base);
+    uint32_t *ord = bp.take<uint32_t>(6);
+    RangeDev *drng = bp.take<RangeDev>(1);
+    float *dbounds = bp.take<float>(6);
+    hipStream_t st = (hipStream_t)stream;
+    HIP_TRY(launch_device_ranges(d_xyz, (uint32_t)n, 1, h.dev, ord, drng, dbounds, nullptr, st));
+    float b6[6];
+    RangeDev r;
+    HIP_TRY(hipMemcpyAsync(b6, dbounds, sizeof(b6), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&r, drng, sizeof(r), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    *out = nsfps_range{b6[0], b6[1], b6[2], b6[3], b6[4], b6[5], xb, yb, zb};
+    if (info) {
+      for (int a = 0; a < 3; ++a) {
+        h.info.inv_bs[a] = r.inv_bs[a];
+        h.info.block_size[a] = r.bsize[a];
+        for (uint32_t k = 0; k < kCubeThr; ++k) h.info.cube_thr[a][k] = r.cube_thr[a][k];
+      }
+      *info = h.info;
+    }
+    return NSFPS_OK;
   });
 }
 

@@ -19,6 +19,10 @@ hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t 
 hipError_t launch_cell_keys(const float *xyz, uint32_t n, const RangeDev &r, const uint32_t *lut,
                             uint32_t *bucket, uint32_t *fine, uint32_t *counts, uint32_t *bad,
                             hipStream_t st);
+// k_cell_keys with the range in device memory (d_range).
+hipError_t launch_cell_keys_dr(const float *xyz, uint32_t n, const RangeDev *d_range,
+                               const uint32_t *lut, uint32_t *bucket, uint32_t *fine,
+                               uint32_t *counts, uint32_t *bad, hipStream_t st);
 // bucket populations into zeroed counts from n sorted bucket keys
 hipError_t launch_seg_counts(const uint32_t *keys, uint32_t n, uint32_t *counts, hipStream_t st);
 // exclusive scan in place, data[len] = total; tmp holds scan_tmp_len(len) words
@@ -82,6 +86,15 @@ hipError_t launch_build_first_many(const BuildDev *d_bd, uint32_t nclouds, uint3
 hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32_t nmax,
                                   uint32_t tmax, uint32_t slots_max, uint32_t leaves_max,
                                   uint32_t l1_max, hipStream_t st);
+
+// compute_bbox of nclouds clouds of n_per points stored one after another
+// (xyz, device) and the ranges of those bounds: out[b] (tmpl's block-count
+// fields, the bounds' fp32 fields), bounds[6 b ..] (min x, max x, min y,
+// max y, min z, max z), and bd[b].c.r when bd is non-null.  ord: 6 nclouds
+// words of workspace.
+hipError_t launch_device_ranges(const float *xyz, uint32_t n_per, uint32_t nclouds,
+                                const RangeDev &tmpl, uint32_t *ord, RangeDev *out,
+                                float *bounds, BuildDev *bd, hipStream_t st);
 
 // sampling
 hipError_t launch_wide_steps(const CloudDev &c, uint32_t steps, uint32_t grid, hipStream_t st);
