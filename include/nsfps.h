@@ -118,6 +118,14 @@ const char *nsfps_version(void);
 /* Number of visible HIP devices (0 when none); never fails. */
 int nsfps_device_count(void);
 
+/* Prepares the current device for the library's calls: loads its kernels
+ * (the runtime loads code on a kernel's first use) and creates the stream and
+ * events the host-buffer calls use.  No counterpart in the reference (a CPU
+ * library).  Optional: the first call on a device does the same; calling
+ * this first keeps that one-time work (tens of milliseconds) out of the
+ * first call.  NSFPS_EDEVICE when no device is visible. */
+nsfps_status nsfps_init_device(void);
+
 /* Derived fields and Morton LUTs of a range.  luts receives the x, y and z
  * LUTs back to back (2^bits[0] + 2^bits[1] + 2^bits[2] entries) when non-NULL
  * and lut_cap is large enough.  Replaces make_range()/make_uniform_range()'s

@@ -679,6 +679,7 @@ __global__ void k_fill_u32(uint32_t *__restrict__ p, uint32_t value, uint64_t wo
 
 // ---------------------------------------------------------------- launchers
 
+
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
 hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t st) {
@@ -931,6 +932,16 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
   if (l1_max) kb_l1_init<<<dim3(cdiv(l1_max, 4), nclouds), 256, 0, st>>>(d_bd);
   kb_init_state<<<nclouds, 64, 0, st>>>(d_bd);
   return hipGetLastError();
+}
+
+hipError_t preload_build_kernels() {
+  return func_attributes(k_cell_keys_dr, k_cloud_bounds, k_range_of_bounds, k_seg_counts,
+                         k_cell_keys, k_radix_hist, k_scan_excl, k_scan_sums, k_scan_apply,
+                         k_radix_scatter, k_cloud_keys, k_key2, k_leaf_counts, k_cell_info,
+                         k_gather, k_leaf_desc_mixed, k_leaf_desc, k_leaf_bbox, k_l1_init,
+                         k_init_state, k_fill_u32, kb_cell_keys, kb_leaf_counts, kb_scans,
+                         kb_zero_slots, kb_gather, kb_cells, kb_leaf_bbox, kb_l1_init,
+                         kb_init_state);
 }
 
 }  // namespace nsfps

@@ -306,6 +306,11 @@ __global__ __launch_bounds__(256) void k_bq_query(const float4 *__restrict__ spt
 
 }  // namespace
 
+hipError_t preload_group_kernels() {
+  return func_attributes(k_gather_points, k_ball_query, k_bq_bounds, k_bq_grid, k_bq_keys,
+                         k_bq_cells, k_bq_query);
+}
+
 hipError_t launch_gather_points(const float *xyz, uint32_t n, const int32_t *idx, uint32_t m,
                                 float *out, uint32_t *bad, hipStream_t st) {
   if (m == 0) return hipSuccess;

@@ -450,6 +450,20 @@ struct Bump {
   }
 };
 
+// Once per device (the current one), before its first call: the library's
+// kernels are loaded, so that loading them does not fall inside a call.
+bool g_kernels_loaded[16];
+
+nsfps_status prepare_device(int dev) {
+  if (dev < 0 || dev >= 16) return fail(NSFPS_EDEVICE, "device ordinal %d out of range", dev);
+  if (g_kernels_loaded[dev]) return NSFPS_OK;
+  HIP_TRY(preload_build_kernels());
+  HIP_TRY(preload_runs_kernels());
+  HIP_TRY(preload_group_kernels());
+  g_kernels_loaded[dev] = true;
+  return NSFPS_OK;
+}
+
 nsfps_status arena_for_device(Arena **out) {
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
@@ -457,6 +471,8 @@ nsfps_status arena_for_device(Arena **out) {
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
   if (dev < 0 || dev >= 16) return fail(NSFPS_EDEVICE, "device ordinal %d out of range", dev);
+  nsfps_status rc = prepare_device(dev);
+  if (rc) return rc;
   Arena &a = g_arena[dev];
   if (!a.stream) {
     HIP_TRY(hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking));
@@ -1574,6 +1590,8 @@ nsfps_status scratch_for_device(void **out) {
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
   if (dev < 0 || dev >= 16) return fail(NSFPS_EDEVICE, "device ordinal %d out of range", dev);
+  const nsfps_status rc = prepare_device(dev);
+  if (rc) return rc;
   if (!g_scratch_ptr[dev]) {
     void *p = nullptr;
     HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
@@ -1617,6 +1635,14 @@ extern "C" {
 const char *nsfps_last_error(void) { return g_err.c_str(); }
 
 const char *nsfps_version(void) { return "nsfps 0.1.0 (gfx950)"; }
+
+nsfps_status nsfps_init_device(void) {
+  return guarded([&]() -> nsfps_status {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Arena *ap = nullptr;
+    return arena_for_device(&ap);
+  });
+}
 
 int nsfps_device_count(void) {
   int n = 0;
@@ -1983,6 +2009,8 @@ nsfps_status nsfps_plan_create(const float *xyz, uint64_t n, const nsfps_range *
     auto plan = std::make_unique<nsfps_plan_s>();
     PlanImpl &P = plan->impl;
     HIP_TRY(hipGetDevice(&P.device));
+    rc = prepare_device(P.device);
+    if (rc) return rc;
     P.plans.resize(1);
     CloudPlan &p = P.plans[0];
     p.n = (uint32_t)n;

@@ -10,6 +10,26 @@
 
 namespace nsfps {
 
+// Loads the kernels of one translation unit on the current device.  The
+// runtime loads a code object, and resolves a kernel in it, when the kernel
+// is first used; done at device set-up, that work stays out of the first
+// call's device time.
+hipError_t preload_build_kernels();
+hipError_t preload_runs_kernels();
+hipError_t preload_group_kernels();
+
+// hipFuncGetAttributes on every kernel given (it loads the kernel's code
+// object and resolves the kernel); the first error is returned.
+template <typename... K>
+hipError_t func_attributes(K... kernels) {
+  hipError_t e = hipSuccess;
+  hipFuncAttributes a;
+  ((e = e == hipSuccess ? hipFuncGetAttributes(&a, reinterpret_cast<const void *>(kernels)) : e),
+   ...);
+  return e;
+}
+
+
 // words 32-bit words at p set to value
 hipError_t launch_fill_u32(void *p, uint32_t value, uint64_t words, hipStream_t st);
 

@@ -1935,6 +1935,19 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
 
 // ---------------------------------------------------------------- launchers
 
+// The variants a call without profiling may launch.
+hipError_t preload_runs_kernels() {
+  constexpr uint32_t S = kUpdateSplit;
+  return func_attributes(
+      k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>, k_run<false, false>,
+      k_run<false, true>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
+      k_update<false, false, true, 1, false>, k_update<false, false, true, S, false>,
+      k_update<false, true, false, 1, false>, k_update<false, true, false, S, false>,
+      k_update<false, true, true, 1, false>, k_update<false, true, true, S, false>,
+      k_update<false, false, false, 1, true>, k_update<false, false, false, S, true>,
+      k_update<false, false, true, 1, true>, k_update<false, false, true, S, true>);
+}
+
 hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool split,
                             hipStream_t st) {
   k_runs_init<<<nclouds, kPassThreads, 0, st>>>(d_clouds, split);
