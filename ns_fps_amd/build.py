@@ -6,7 +6,13 @@
   reference's own import path (``import yuezu_fps.yuezu_fps_module as yf``),
   linked against libnsfps.so with an $ORIGIN-relative rpath.
 
-Run ``python -m ns_fps_amd.build`` (or ``__graft_entry__.build()``).
+* ``_build/sanitize/`` -- the same two, host code built with AddressSanitizer
+  and UndefinedBehaviorSanitizer (device code as usual), for
+  ``python -m ns_fps_amd.sanitize``, which runs the CPU tests of the host
+  library under them.
+
+Run ``python -m ns_fps_amd.build`` (or ``__graft_entry__.build()``);
+``python -m ns_fps_amd.build sanitize`` builds the sanitized pair.
 """
 
 import os
@@ -87,35 +93,59 @@ def module_path():
     return os.path.join(MODULE_DIR, "yuezu_fps_module" + suffix)
 
 
-def build_lib():
+SAN_DIR = os.path.join(ROOT, "_build", "sanitize")
+# host code only: each -fsanitize= right after -Xarch_host, device code unsanitized
+SAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all",
+                  "-fno-gpu-sanitize", "-g"]
+
+
+def build_lib(out=LIB, extra=()):
     srcs = [os.path.join(CSRC, f) for f in SOURCES]
-    tmp = LIB + ".tmp"
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
     with tempfile.TemporaryDirectory(prefix="nsfps_build_") as td:
         # -save-temps keeps each translation unit's gfx950 assembly in td
-        _run([HIPCC, *DEVICE_FLAGS, "-save-temps", "-shared", "-I", INCLUDE, "-I", CSRC, *srcs,
-              "-o", tmp], cwd=td)
+        _run([HIPCC, *DEVICE_FLAGS, *extra, "-save-temps", "-shared", "-I", INCLUDE, "-I", CSRC,
+              *srcs, "-o", tmp], cwd=td)
         check_no_packed_fp32(td)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
-def build_module():
+def build_module(out=None, lib_dir=HERE, cxx="g++", extra=()):
     import pybind11
-    os.makedirs(MODULE_DIR, exist_ok=True)
-    out = module_path()
+    out = out or module_path()
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
     pyinc = sysconfig.get_paths()["include"]
-    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", *extra,
           "-I", INCLUDE, "-I", pybind11.get_include(), "-I", pyinc,
           os.path.join(CSRC, "yuezu_fps_pybind.cpp"),
-          "-L", HERE, "-lnsfps", "-Wl,-rpath,$ORIGIN/../ns_fps_amd", "-o", tmp])
+          "-L", lib_dir, "-lnsfps", "-Wl,-rpath,$ORIGIN/../ns_fps_amd", "-o", tmp])
     os.replace(tmp, out)
-    # an older build placed the module inside the package: remove it so that
-    # only one copy of the bindings exists
-    old = os.path.join(HERE, os.path.basename(out))
-    if os.path.exists(old):
-        os.remove(old)
+    if out == module_path():
+        # an older build placed the module inside the package: remove it so
+        # that only one copy of the bindings exists
+        old = os.path.join(HERE, os.path.basename(out))
+        if os.path.exists(old):
+            os.remove(old)
     return out
+
+
+def build_sanitized():
+    """libnsfps.so and the module with ASan + UBSan host code, under
+    _build/sanitize/ (ns_fps_amd/ and yuezu_fps/, as in the tree).  Both use
+    clang's sanitizer runtime, which the process preloads."""
+    lib = build_lib(os.path.join(SAN_DIR, "ns_fps_amd", "libnsfps.so"), SAN_HOST_FLAGS)
+    clangxx = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "llvm", "bin", "clang++")
+    if not os.path.exists(clangxx):
+        clangxx = "/opt/rocm/llvm/bin/clang++"
+    mod = build_module(os.path.join(SAN_DIR, "yuezu_fps", os.path.basename(module_path())),
+                       os.path.dirname(lib), clangxx,
+                       ["-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                        "-fno-omit-frame-pointer", "-shared-libasan", "-g"])
+    return lib, mod
 
 
 def build_all():
@@ -126,4 +156,5 @@ def build_all():
 if __name__ == "__main__":
     what = sys.argv[1:] or ["all"]
     for w in what:
-        {"lib": build_lib, "module": build_module, "all": build_all}[w]()
+        {"lib": build_lib, "module": build_module, "all": build_all,
+         "sanitize": build_sanitized}[w]()

@@ -13,7 +13,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libnsfps.so")
+# NSFPS_LIB names another build of the library (the sanitized one, say)
+LIB_PATH = os.environ.get("NSFPS_LIB") or os.path.join(HERE, "libnsfps.so")
 
 NSFPS_OK, NSFPS_EINVAL, NSFPS_EDEVICE, NSFPS_ENOMEM, NSFPS_EUNSUPPORTED = range(5)
 

@@ -51,12 +51,60 @@ nsfps_status fail(nsfps_status s, const char *fmt, ...) {
   return s;
 }
 
-#define HIP_TRY(expr)                                                                    \
-  do {                                                                                   \
-    hipError_t e_ = (expr);                                                              \
-    if (e_ != hipSuccess)                                                                \
+// ----------------------------------------------------- failure injection
+//
+// NSFPS_INJECT=<kind>:<n> makes the n-th HIP operation of that kind in a
+// call fail inside the library, without reaching the runtime: kind is alloc
+// (device or pinned allocation, reported as out of memory), launch (a kernel
+// launch or kernel load), copy (a memory copy), sync (a wait for a stream or
+// event) or any.  Every entry point reads the variable when it starts, so
+// each call gets its own countdown and a call after the variable is removed
+// runs normally.  The error paths this reaches (status, message, the
+// workspace left usable, the stream drained) are tested on the GPU.
+enum InjectKind : int { kInjNone = 0, kInjAlloc, kInjLaunch, kInjCopy, kInjSync, kInjAny };
+thread_local int g_inj_kind = kInjNone;
+thread_local uint64_t g_inj_left = 0;
+
+void arm_injection() {
+  g_inj_kind = kInjNone;
+  const char *e = getenv("NSFPS_INJECT");
+  if (!e || !*e) return;
+  static const char *const names[] = {"", "alloc", "launch", "copy", "sync", "any"};
+  const char *colon = strchr(e, ':');
+  const size_t len = colon ? (size_t)(colon - e) : strlen(e);
+  for (int k = kInjAlloc; k <= kInjAny; ++k)
+    if (strlen(names[k]) == len && strncmp(e, names[k], len) == 0) g_inj_kind = k;
+  const unsigned long long n = colon ? strtoull(colon + 1, nullptr, 10) : 1ull;
+  g_inj_left = n ? n : 1;
+}
+
+// The kind of HIP operation an expression performs, from its text.
+int op_kind(const char *expr) {
+  const auto starts = [&](const char *p) { return strncmp(expr, p, strlen(p)) == 0; };
+  if (starts("hipMalloc") || starts("hipHostMalloc")) return kInjAlloc;
+  if (starts("launch_") || starts("preload_")) return kInjLaunch;
+  if (starts("hipMemcpy")) return kInjCopy;
+  if (starts("hipStreamSynchronize") || starts("hipEventSynchronize")) return kInjSync;
+  return kInjAny;  // other runtime calls fail only under "any"
+}
+
+// hipSuccess, or the injected failure when this operation is the one armed.
+hipError_t injected(int kind) {
+  if (g_inj_kind == kInjNone || (g_inj_kind != kInjAny && g_inj_kind != kind)) return hipSuccess;
+  if (--g_inj_left) return hipSuccess;
+  g_inj_kind = kInjNone;
+  return kind == kInjAlloc ? hipErrorOutOfMemory : hipErrorLaunchFailure;
+}
+
+#define HIP_TRY(expr)                                                                        \
+  do {                                                                                       \
+    hipError_t e_ = g_inj_kind ? injected(op_kind(#expr)) : hipSuccess;                      \
+    const bool inj_ = e_ != hipSuccess;                                                      \
+    if (!inj_) e_ = (expr);                                                                  \
+    if (e_ != hipSuccess)                                                                    \
       return fail(e_ == hipErrorOutOfMemory ? NSFPS_ENOMEM : NSFPS_EDEVICE, "%s: %s (%s:%d)", \
-                  #expr, hipGetErrorString(e_), __FILE__, __LINE__);                     \
+                  #expr, inj_ ? "injected failure (NSFPS_INJECT)" : hipGetErrorString(e_),   \
+                  __FILE__, __LINE__);                                                       \
   } while (0)
 
 // ---------------------------------------------------------------- range ----
@@ -492,10 +540,12 @@ nsfps_status arena_reserve(Arena &a, size_t bytes) {
     a.cap = 0;
   }
   size_t want = bytes + bytes / 8 + (1u << 20);
-  hipError_t e = hipMalloc(&a.base, want);
+  const hipError_t inj = injected(kInjAlloc);
+  hipError_t e = inj != hipSuccess ? inj : hipMalloc(&a.base, want);
   if (e != hipSuccess) {
     a.base = nullptr;
-    return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", want, hipGetErrorString(e));
+    return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", want,
+                inj != hipSuccess ? "injected failure (NSFPS_INJECT)" : hipGetErrorString(e));
   }
   a.cap = want;
   return NSFPS_OK;
@@ -532,7 +582,8 @@ nsfps_status upload_host(const std::vector<HostUp> &ups, hipStream_t st) {
     ps.p = nullptr;
     ps.cap = 0;
     const size_t want = total + total / 8 + (1u << 20);
-    if (hipHostMalloc(reinterpret_cast<void **>(&ps.p), want, hipHostMallocDefault) != hipSuccess) {
+    if (injected(kInjAlloc) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void **>(&ps.p), want, hipHostMallocDefault) != hipSuccess) {
       ps.p = nullptr;
       (void)hipGetLastError();
       for (const auto &u : ups)
@@ -742,6 +793,7 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   size_t outs = 0;
   for (auto &p : plans) outs += p.m;
   cb.out = bp.take<int32_t>(outs);
+  if (!bp.base) return;  // measuring: no buffer to hand out
   size_t o_stage = 0, o_n = 0, o_c = 0, o_out = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
     CloudPlan &p = plans[i];
@@ -1618,6 +1670,7 @@ namespace {
 template <class F>
 nsfps_status guarded(F &&f) {
   try {
+    arm_injection();
     return f();
   } catch (const std::bad_alloc &) {
     return fail(NSFPS_ENOMEM, "host allocation failed");
@@ -2031,10 +2084,12 @@ nsfps_status nsfps_plan_create(const float *xyz, uint64_t n, const nsfps_range *
     snap.take<uint64_t>(pb.leaves_ub);
     snap.take<float4>(pb.leaves_ub);
     const size_t total = snap.off + 256;
-    hipError_t e = hipMalloc(&P.mem, total);
+    const hipError_t inj = injected(kInjAlloc);
+    hipError_t e = inj != hipSuccess ? inj : hipMalloc(&P.mem, total);
     if (e != hipSuccess) {
       P.mem = nullptr;
-      return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", total, hipGetErrorString(e));
+      return fail(NSFPS_ENOMEM, "hipMalloc(%zu) failed: %s", total,
+                  inj != hipSuccess ? "injected failure (NSFPS_INJECT)" : hipGetErrorString(e));
     }
     P.cap = total;
     for (auto &ev : P.ev) HIP_TRY(hipEventCreate(&ev));
@@ -2107,20 +2162,29 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
     ws.st = st;
     ws.ev = P.ev;
     CloudDev &c = p.dev;
-    HIP_TRY(hipEventRecord(P.ev[0], st));
-    HIP_TRY(hipMemcpyAsync(c.P4, P.p4_0, (size_t)c.nslots * sizeof(float4),
-                           hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipMemcpyAsync(c.leaf_key, P.lk_0, (size_t)c.nleaves * 8, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipMemcpyAsync(c.leaf_pos, P.lp_0, (size_t)c.nleaves * sizeof(float4),
-                           hipMemcpyDeviceToDevice, st));
-    HIP_TRY(launch_init_state(c, p.d_small + 2, st));
-    HIP_TRY(hipEventRecord(P.ev[1], st));
-    uint64_t rounds = 0, wide_total = 0;
-    uint32_t update_split = 0;
-    nsfps_status rc = sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split);
-    if (rc) return rc;
-    return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, false, nullptr, 0,
-                       out_len, t0);
+    // the restore and the sampling; a failure after work was enqueued waits
+    // for the stream before returning, as run_clouds does
+    const auto body = [&]() -> nsfps_status {
+      HIP_TRY(hipEventRecord(P.ev[0], st));
+      HIP_TRY(hipMemcpyAsync(c.P4, P.p4_0, (size_t)c.nslots * sizeof(float4),
+                             hipMemcpyDeviceToDevice, st));
+      HIP_TRY(hipMemcpyAsync(c.leaf_key, P.lk_0, (size_t)c.nleaves * 8, hipMemcpyDeviceToDevice,
+                             st));
+      HIP_TRY(hipMemcpyAsync(c.leaf_pos, P.lp_0, (size_t)c.nleaves * sizeof(float4),
+                             hipMemcpyDeviceToDevice, st));
+      HIP_TRY(launch_init_state(c, p.d_small + 2, st));
+      HIP_TRY(hipEventRecord(P.ev[1], st));
+      uint64_t rounds = 0, wide_total = 0;
+      uint32_t update_split = 0;
+      const nsfps_status rc =
+          sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split);
+      if (rc) return rc;
+      return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, false,
+                         nullptr, 0, out_len, t0);
+    };
+    const nsfps_status rc = body();
+    if (rc) (void)hipStreamSynchronize(st);
+    return rc;
   });
 }
 

@@ -30,6 +30,23 @@ def oracle():
     return Oracle()
 
 
+def _module_override():
+    """NSFPS_MODULE names another build of the module (the sanitized one): it
+    is imported under the module's own name, so every import of it gets it."""
+    path = os.environ.get("NSFPS_MODULE")
+    if not path or "yuezu_fps.yuezu_fps_module" in sys.modules:
+        return
+    import importlib.util
+    import yuezu_fps  # noqa: F401  (the package the module belongs to)
+    spec = importlib.util.spec_from_file_location("yuezu_fps.yuezu_fps_module", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    sys.modules["yuezu_fps.yuezu_fps_module"] = mod
+
+
+_module_override()
+
+
 @pytest.fixture(scope="session")
 def yf():
     import yuezu_fps.yuezu_fps_module as m
@@ -38,8 +55,8 @@ def yf():
 
 @pytest.fixture(scope="session")
 def capi():
-    lib = ctypes.CDLL(os.path.join(ROOT, "ns_fps_amd", "libnsfps.so"))
-    return lib
+    from ns_fps_amd.capi import LIB_PATH
+    return ctypes.CDLL(LIB_PATH)
 
 
 class GoldenCase:

@@ -25,7 +25,8 @@ def test_more_than_one_gpu_is_refused():
 
 def test_no_device_is_an_error_not_a_fallback():
     import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "ns_fps_amd", "libnsfps.so"))
+    from ns_fps_amd.capi import LIB_PATH
+    lib = ctypes.CDLL(LIB_PATH)
     if lib.nsfps_device_count() > 0:
         import pytest
         pytest.skip("a HIP device is visible")
