@@ -194,19 +194,24 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t n_samples
                               uint64_t *out_len, void *stream);
 
 /* nsfps_fps_device without any device allocation.  No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The call's whole workspace (cell keys, sorts, slots, leaves,
- * tree and sampling state) lives in a static device array of
- * nsfps_noalloc_scratch_bytes() bytes (64 MiB) per device, held until the
- * process ends; a cloud whose layout needs more (about 400,000 points on
- * grids of up to 2^16 blocks) fails with NSFPS_EUNSUPPORTED and a message
- * giving both sizes.  Same arguments, samples and guards as nsfps_fps_device;
- * no hipMalloc, hipFree, stream or event creation, and no memset nodes (fill
- * kernels clear what must start at zero).  The array keeps the last call's
- * contents; calls are serialised by the library's lock, and a call on one
- * device must not overlap another use of that device's array (the library
- * makes none).  Statistics report e2e_ms only (no device events). */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  The call's whole
+ * workspace (cell keys, sorts, slots, leaves, tree and sampling state) lives
+ * in a static device array of nsfps_noalloc_scratch_bytes() bytes (64 MiB)
+ * per device, reserved on every device by the library's code object in each
+ * process that loads the library, whether or not this call is used, and
+ * held until the process ends.  A cloud whose layout needs more fails with
+ * NSFPS_EUNSUPPORTED and a message giving both sizes: measured limits are
+ * 450,736 points on a 32^3 grid, 460,416 on 16^3 and 428,160 on 64x64x16.
+ * Same arguments, samples and guards as nsfps_fps_device; no hipMalloc,
+ * hipFree, stream or event creation, and no memset nodes (fill kernels clear
+ * what must start at zero).  Like every call here it cannot be captured into
+ * a HIP graph (it reads results back between batches of rounds and waits for
+ * the stream): on a capturing stream it returns NSFPS_EUNSUPPORTED before
+ * enqueuing anything.  The array keeps the last call's contents; calls are
+ * serialised by the library's lock, and a call on one device must not
+ * overlap another use of that device's array (the library makes none).
+ * Statistics report e2e_ms only (no device events). */
 nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t n_samples,
                                       const nsfps_range *range, int32_t *d_out,
                                       uint64_t *out_len, void *stream);

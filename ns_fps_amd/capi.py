@@ -261,3 +261,24 @@ class Hip:
 
     def synchronize(self):
         self._ck(self.rt.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def stream_create(self):
+        s = _vp()
+        self._ck(self.rt.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def stream_destroy(self, s):
+        self._ck(self.rt.hipStreamDestroy(_vp(s)), "hipStreamDestroy")
+
+    def begin_capture(self, s, mode=2):
+        """hipStreamBeginCapture (mode 2: hipStreamCaptureModeRelaxed)."""
+        self._ck(self.rt.hipStreamBeginCapture(_vp(s), ctypes.c_int(mode)), "hipStreamBeginCapture")
+
+    def end_capture(self, s):
+        """hipStreamEndCapture; the graph is destroyed at once (nothing here
+        launches one).  Returns the status of the end."""
+        g = _vp()
+        rc = self.rt.hipStreamEndCapture(_vp(s), ctypes.byref(g))
+        if g.value:
+            self.rt.hipGraphDestroy(g)
+        return rc

@@ -1599,6 +1599,21 @@ bool trivial(uint64_t n, uint64_t m, int32_t *out, uint64_t *len) {
 
 void reset_stats() { memset(&g_stats, 0, sizeof(g_stats)); }
 
+// A call on a caller's stream cannot be captured into a HIP graph: between
+// batches of rounds it reads each cloud's status back and waits for the
+// stream, and it returns after the stream work completes.  Refused before
+// anything is enqueued, so the capture is left as it was.
+nsfps_status check_not_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(NSFPS_EUNSUPPORTED,
+                "the stream is being captured into a HIP graph: the call cannot be captured (it "
+                "reads each cloud's status back between batches of rounds and waits for the "
+                "stream)");
+  return NSFPS_OK;
+}
+
 // A cloud built once and sampled many times (nsfps_plan_*): its own device
 // memory holds the call layout and a copy of the arrays sampling changes
 // (the points' min-distances, the leaf keys and winners), taken after the
@@ -1877,6 +1892,8 @@ nsfps_status nsfps_fps_batched_device(const float *d_xyz, uint64_t batch, uint64
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
     hipStream_t st = (hipStream_t)stream;
+    rc = check_not_capturing(st);
+    if (rc) return rc;
     uint64_t len = 0;
     std::vector<int32_t> one((size_t)std::max<uint64_t>(std::min(n, m), 1));
     if (trivial(n, m, one.data(), &len)) {  // the same rows for every cloud
@@ -1922,6 +1939,8 @@ nsfps_status nsfps_bbox_device(const float *d_xyz, uint64_t n, uint32_t xb, uint
     if (rc) return rc;
     derive_blocks(bl, h);
     std::lock_guard<std::mutex> lk(g_mu);
+    rc = check_not_capturing((hipStream_t)stream);
+    if (rc) return rc;
     Arena *ap = nullptr;
     rc = arena_for_device(&ap);
     if (rc) return rc;
@@ -1966,6 +1985,8 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const 
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
     hipStream_t st = (hipStream_t)stream;
+    rc = check_not_capturing(st);
+    if (rc) return rc;
     if (n == 0 || m == 0 || m >= n || m == 1) {
       std::vector<int32_t> tmp((size_t)std::min<uint64_t>(std::max<uint64_t>(n, 1), m ? m : 1));
       trivial(n, m, tmp.data(), out_len);
@@ -2006,6 +2027,8 @@ nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t m
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
       return fail(NSFPS_EDEVICE, "no HIP device available (nsfps has no CPU path)");
     hipStream_t st = (hipStream_t)stream;
+    rc = check_not_capturing(st);
+    if (rc) return rc;
     void *ws_base = nullptr;
     rc = scratch_for_device(&ws_base);
     if (rc) return rc;
@@ -2132,6 +2155,8 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
       return fail(NSFPS_EINVAL, "the plan was created on device %d, the current device is %d",
                   P.device, dev);
     hipStream_t st = (hipStream_t)stream;
+    nsfps_status rc0 = check_not_capturing(st);
+    if (rc0) return rc0;
     CloudPlan &p = P.plans[0];
     const uint64_t n = p.n;
     if (n == 0 || m == 0 || m >= n || m == 1) {
@@ -2233,6 +2258,8 @@ nsfps_status nsfps_gather_points_device(const float *d_xyz, uint64_t n, const in
     nsfps_status rc = check_group(n, m, 0);
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
+    rc = check_not_capturing((hipStream_t)stream);
+    if (rc) return rc;
     Arena *ap = nullptr;
     rc = arena_for_device(&ap);
     if (rc) return rc;
@@ -2369,6 +2396,8 @@ nsfps_status nsfps_ball_query_device(const float *d_xyz, uint64_t n, const float
     rc = check_group(n, m, nsample);
     if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
+    rc = check_not_capturing((hipStream_t)stream);
+    if (rc) return rc;
     Arena *ap = nullptr;
     rc = arena_for_device(&ap);
     if (rc) return rc;

@@ -123,12 +123,19 @@ __device__ __forceinline__ uint32_t in_box11(uint32_t cg, uint32_t c11, uint32_t
 
 // Level-1 node g's key: the largest of l1_key and the node's parts (in a call
 // whose update pass is split, l1_key is zero and the parts hold the largest
-// keys of the node's quarters; otherwise the parts are zero)
+// keys of the node's quarters; otherwise the parts are zero).  In the split
+// update pass a workgroup reads its siblings' parts while they may write
+// them: the parts are read and written as relaxed agent-scope atomics (each
+// 64-bit word whole, no order needed: either value of a part bounds its
+// quarter's points, distances only falling).
 __device__ __forceinline__ uint64_t node_key(const CloudDev &c, uint32_t g) {
-  const NSFPS_GLOBAL uint64_t *const pp = gptr(c.l1_part) + (size_t)g * kUpdateSplit;
+  NSFPS_GLOBAL uint64_t *const pp = gptr(c.l1_part) + (size_t)g * kUpdateSplit;
   uint64_t k = gptr(c.l1_key)[g];
 #pragma unroll
-  for (uint32_t s = 0; s < kUpdateSplit; ++s) k = pp[s] > k ? pp[s] : k;
+  for (uint32_t s = 0; s < kUpdateSplit; ++s) {
+    const uint64_t v = __hip_atomic_load(pp + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    k = v > k ? v : k;
+  }
   return k;
 }
 
@@ -570,7 +577,9 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
   } else if (wave == 0) {
     // this quarter's largest key (keys are unique: the rank is their low word)
     const uint64_t part = wave_max_u64(lane < kFan / SPLIT ? s_lk[lane] : 0ull);
-    if (lane == 0) gptr(c.l1_part)[(size_t)g * SPLIT + sub] = part;
+    if (lane == 0)
+      __hip_atomic_store(gptr(c.l1_part) + (size_t)g * SPLIT + sub, part, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
   NSFPS_GLOBAL uint32_t *H = hist_set(c);
   for (uint32_t j = tid; j < kHistBins; j += kPassThreads) {

@@ -386,12 +386,15 @@ def test_host_buffer_calls_across_a_workspace_release(lib):
             lib.release_workspace()
 
 
-@pytest.mark.parametrize("n, blocks", [(700000, (16, 16, 16)),   # one cell per bucket
-                                       (320000, (15, 15, 15))])  # cells sharing buckets
+@pytest.mark.parametrize("n, blocks", [
+    (700000, (16, 16, 16)),  # one cell per bucket
+    (320000, (15, 15, 15)),  # cells sharing buckets
+    (200000, (24, 24, 24)),  # cells sharing buckets, at most 262,144 points: leaf-box bound too
+])
 def test_split_update_pass_on_a_mid_size_cloud(yf, oracle, n, blocks):
     """A cloud of 129 to 256 level-1 nodes: the update pass splits each node's
-    leaves over four workgroups (node keys kept as four parts); the samples
-    are the oracle's."""
+    leaves over four workgroups (node keys kept as four parts; the call's
+    statistics say so); the samples are the oracle's."""
     rs = np.random.RandomState(31)
     pts = rs.uniform(-1, 1, (n, 3)).astype(np.float32)
     rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks)
@@ -399,4 +402,14 @@ def test_split_update_pass_on_a_mid_size_cloud(yf, oracle, n, blocks):
     st = yf.last_stats()
     nl1 = (st["n_leaves"] + 63) // 64
     assert st["engine"] == "runs" and 128 < nl1 <= 256, nl1
+    assert st["update_split"] == 4, st["update_split"]
     assert np.array_equal(got, oracle.fps(pts, 8000, rng))
+
+
+def test_whole_node_update_pass_is_reported(yf):
+    """Above 256 level-1 nodes in all, each node takes one workgroup."""
+    rs = np.random.RandomState(32)
+    pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)
+    yf.fps(pts, 200, yf.make_range(-1, 1, -1, 1, -1, 1, 32, 32, 32))
+    st = yf.last_stats()
+    assert (st["n_leaves"] + 63) // 64 > 256 and st["update_split"] == 1
