@@ -100,7 +100,9 @@ hipError_t injected(int kind) {
   do {                                                                                       \
     hipError_t e_ = g_inj_kind ? injected(op_kind(#expr)) : hipSuccess;                      \
     const bool inj_ = e_ != hipSuccess;                                                      \
-    if (!inj_) e_ = (expr);                                                                  \
+    if (!inj_) {                                                                             \
+      e_ = (expr);                                                                           \
+    }                                                                                        \
     if (e_ != hipSuccess)                                                                    \
       return fail(e_ == hipErrorOutOfMemory ? NSFPS_ENOMEM : NSFPS_EDEVICE, "%s: %s (%s:%d)", \
                   #expr, inj_ ? "injected failure (NSFPS_INJECT)" : hipGetErrorString(e_),   \

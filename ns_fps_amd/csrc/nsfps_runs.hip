@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kPassThreads, 2) __attribute__((amdgpu_num_sgpr(60)
       return !lbound ||
              !(box_bound(q.x, q.y, q.z, blo.x, blo.y, blo.z, bhi.x, bhi.y, bhi.z) >= lmax);
     };
-    hm[k] = __ballot(in0 & touches_pick(k, pc0) & may_lower(pp0));
+    hm[k] = __ballot((uint32_t)in0 & (uint32_t)touches_pick(k, pc0) & (uint32_t)may_lower(pp0));
     bool h = hm[k] != 0;
     for (uint32_t cb = 64; cb < nsel && !h; cb += 64)
       h = __ballot((cb + lane < nsel) && touches(k, cb + lane) && may_lower(s_pp[cb + lane])) != 0;
