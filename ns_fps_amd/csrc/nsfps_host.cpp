@@ -784,13 +784,15 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   }
   cb.xyz_stage = stage ? bp.take<float>(stage) : nullptr;
   cb.counts = bp.take<uint32_t>(cb.counts_total);
+  // small, drng and dbounds one after another: the build reads them back
+  // in one copy
   cb.small = bp.take<uint32_t>(4 * plans.size());
+  cb.drng = bp.take<RangeDev>(plans.size());
+  cb.dbounds = bp.take<float>(6 * plans.size());
   cb.bucket = bp.take<uint32_t>(cb.n_total);
   cb.fine = bp.take<uint32_t>(cb.n_total);
   cb.bd = bp.take<BuildDev>(plans.size());
   cb.ord = bp.take<uint32_t>(6 * plans.size());
-  cb.drng = bp.take<RangeDev>(plans.size());
-  cb.dbounds = bp.take<float>(6 * plans.size());
   // the clouds' outputs back to back, rows of m entries: one read-back
   size_t outs = 0;
   for (auto &p : plans) outs += p.m;
@@ -1128,12 +1130,19 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   std::vector<uint32_t> hs(4 * nc);
   std::vector<float> hb(any_dev ? 6 * nc : 0);
   std::vector<RangeDev> hr(any_dev ? nc : 0);
-  HIP_TRY(hipMemcpyAsync(hs.data(), cb.small, nc * 16, hipMemcpyDeviceToHost, st));
-  if (any_dev) {
-    HIP_TRY(hipMemcpyAsync(hb.data(), cb.dbounds, hb.size() * 4, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(hr.data(), cb.drng, nc * sizeof(RangeDev), hipMemcpyDeviceToHost, st));
+  {  // one read-back: the build stats, and the ranges found on the device
+    const char *const at = reinterpret_cast<const char *>(cb.small);
+    const size_t o_r = reinterpret_cast<const char *>(cb.drng) - at;
+    const size_t o_b = reinterpret_cast<const char *>(cb.dbounds) - at;
+    std::vector<char> rb(any_dev ? o_b + hb.size() * 4 : nc * 16);
+    HIP_TRY(hipMemcpyAsync(rb.data(), at, rb.size(), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    std::memcpy(hs.data(), rb.data(), nc * 16);
+    if (any_dev) {
+      std::memcpy(hr.data(), rb.data() + o_r, nc * sizeof(RangeDev));
+      std::memcpy(hb.data(), rb.data() + o_b, hb.size() * 4);
+    }
   }
-  HIP_TRY(hipStreamSynchronize(st));
   for (size_t i = 0; i < nc; ++i)
     if (hs[4 * i]) return fail(NSFPS_EINVAL, "points must be finite");
   // the ranges found on the device: checked as a range given by the caller
@@ -1960,9 +1969,14 @@ nsfps_status nsfps_bbox_device(const float *d_xyz, uint64_t n, uint32_t xb, uint
     HIP_TRY(launch_device_ranges(d_xyz, (uint32_t)n, 1, h.dev, ord, drng, dbounds, nullptr, st));
     float b6[6];
     RangeDev r;
-    HIP_TRY(hipMemcpyAsync(b6, dbounds, sizeof(b6), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(&r, drng, sizeof(r), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    {  // one read-back: the range, then its bounds
+      const size_t o_b = reinterpret_cast<char *>(dbounds) - reinterpret_cast<char *>(drng);
+      std::vector<char> rb(o_b + sizeof(b6));
+      HIP_TRY(hipMemcpyAsync(rb.data(), drng, rb.size(), hipMemcpyDeviceToHost, st));
+      HIP_TRY(hipStreamSynchronize(st));
+      std::memcpy(&r, rb.data(), sizeof(r));
+      std::memcpy(b6, rb.data() + o_b, sizeof(b6));
+    }
     *out = nsfps_range{b6[0], b6[1], b6[2], b6[3], b6[4], b6[5], xb, yb, zb};
     if (info) {
       for (int a = 0; a < 3; ++a) {
