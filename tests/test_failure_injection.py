@@ -160,6 +160,23 @@ def test_plan_failures(lib, hip, monkeypatch):
         hip.free(d_out)
 
 
+def test_staged_host_copies_fail_cleanly(lib, oracle, monkeypatch):
+    """A host input of 4 MB or more is copied into the pinned stage by the
+    host pool's threads and sent in one DMA; a result of 256 KB or more comes
+    back through the stage and the pool's threads copy it out.  Every copy of
+    such a call fails in turn; the call after each failure returns the
+    oracle's samples."""
+    rs = np.random.RandomState(41)
+    pts = rs.uniform(-1, 1, (1 << 20, 3)).astype(np.float32)  # 12 MB in, 256 KB out
+    rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, 32, 32, 32)
+    want = oracle.fps(pts, 65536, rng)
+
+    def check(got):
+        assert np.array_equal(got, want)
+    check(lib.fps(pts, 65536, rng))
+    assert sweep(lib, monkeypatch, "copy", lambda: lib.fps(pts, 65536, rng), check) >= 3
+
+
 def test_unarmed_or_unknown_injection_changes_nothing(lib, monkeypatch):
     for spec in ["", "nothing:1", "launch:100000"]:
         monkeypatch.setenv("NSFPS_INJECT", spec)
