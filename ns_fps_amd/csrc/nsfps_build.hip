@@ -338,6 +338,97 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(
   }
 }
 
+// The logical sort of clouds of at most kSegSortMax points, one 1024-thread
+// workgroup per cloud: cloud s is bucket[s * n_per .., + n_per), sorted by
+// bucket with rows in input order inside a bucket.  keys_out[s * n_per + p]
+// gets (s << key_shift) | bucket and vals_out the row s * n_per + r: what
+// the radix sort over (cloud, bucket) keys writes.  An element is packed as
+// (bucket << 14) | r, 16 of them per lane in registers (lane l of wave w
+// holds r = 1024 w + 64 i + l); each pass of 8 bucket bits ranks them with
+// the ballots of k_radix_scatter (a wave's elements in order, the wave's
+// running count per digit in LDS), offsets digit by digit and then wave by
+// wave, and scatters into LDS, or into keys_out / vals_out after the last
+// pass.  Three global passes over the 64 clouds of 16,384 points took 96 us.
+constexpr uint32_t kSegSortMax = kSegSortMaxPoints;
+constexpr int kSegWaves = 16, kSegRounds = 16;  // 16 waves x 16 rounds x 64 lanes
+static_assert(kSegWaves * kSegRounds * 64 == (int)kSegSortMax, "one element per lane and round");
+
+__global__ __launch_bounds__(1024) void k_seg_sort(const uint32_t *__restrict__ bucket,
+                                                   uint32_t n_per, int bits, int key_shift,
+                                                   uint32_t *__restrict__ keys_out,
+                                                   uint32_t *__restrict__ vals_out) {
+  __shared__ uint32_t s_el[kSegSortMax];
+  __shared__ uint32_t wcnt[kSegWaves][256];
+  __shared__ uint32_t wsum[kSegWaves];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const size_t base = (size_t)blockIdx.x * n_per;
+  const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+  uint32_t el[kSegRounds];
+#pragma unroll
+  for (int r = 0; r < kSegRounds; ++r) {
+    const uint32_t e = wave * (64u * kSegRounds) + 64u * r + lane;
+    el[r] = e < n_per ? (bucket[base + e] << 14) | e : 0u;
+  }
+  for (int shift = 0; shift < bits; shift += 8) {
+    for (uint32_t i = tid; i < kSegWaves * 256u; i += 1024u) (&wcnt[0][0])[i] = 0u;
+    __syncthreads();
+    uint32_t rnk[kSegRounds];
+#pragma unroll
+    for (int r = 0; r < kSegRounds; ++r) {
+      const bool valid = wave * (64u * kSegRounds) + 64u * r + lane < n_per;
+      const uint32_t d = (el[r] >> (14 + shift)) & 255u;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const uint64_t m = __ballot((d >> b) & 1u);
+        peers &= ((d >> b) & 1u) ? m : ~m;
+      }
+      const uint32_t before = (uint32_t)__popcll(peers & lt);
+      const uint32_t baseq = valid ? wcnt[wave][d] : 0u;
+      rnk[r] = baseq + before;
+      // all lanes read their base before a leader writes (in-order LDS, one wave)
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      if (valid && before == 0) wcnt[wave][d] = baseq + (uint32_t)__popcll(peers);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+    __syncthreads();
+    // digit d's first position, then each wave's within the digit
+    uint32_t tot = 0;
+    if (tid < 256u)
+      for (int w = 0; w < kSegWaves; ++w) tot += wcnt[w][tid];
+    uint32_t all;
+    const uint32_t first = block_excl_scan<kSegWaves>(tot, wsum, &all);
+    if (tid < 256u) {
+      uint32_t at = first;
+      for (int w = 0; w < kSegWaves; ++w) {
+        const uint32_t c = wcnt[w][tid];
+        wcnt[w][tid] = at;
+        at += c;
+      }
+    }
+    __syncthreads();
+    const bool last = shift + 8 >= bits;
+#pragma unroll
+    for (int r = 0; r < kSegRounds; ++r) {
+      if (wave * (64u * kSegRounds) + 64u * r + lane >= n_per) continue;
+      const uint32_t pos = wcnt[wave][(el[r] >> (14 + shift)) & 255u] + rnk[r];
+      if (last) {
+        keys_out[base + pos] = ((uint32_t)blockIdx.x << key_shift) | (el[r] >> 14);
+        vals_out[base + pos] = (uint32_t)base + (el[r] & 0x3fffu);
+      } else {
+        s_el[pos] = el[r];
+      }
+    }
+    if (last) break;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSegRounds; ++r) {
+      const uint32_t e = wave * (64u * kSegRounds) + 64u * r + lane;
+      el[r] = e < n_per ? s_el[e] : 0u;
+    }
+  }
+}
+
 // Sort key of the clouds of a call sorted together: cloud index above the
 // bucket (every cloud has n_per points, stored one cloud after another).
 __global__ void k_cloud_keys(const uint32_t *__restrict__ bucket, uint32_t total, uint32_t n_per,
@@ -773,6 +864,18 @@ hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
   return hipGetLastError();
 }
 
+hipError_t launch_seg_sort(const uint32_t *bucket, uint32_t n_per, uint32_t nclouds,
+                           int bucket_bits, uint32_t *keys_out, uint32_t *vals_out,
+                           hipStream_t st) {
+  // rows in 14 bits, bucket above them; the cloud index above the bucket in
+  // the keys written
+  if (n_per > kSegSortMax || bucket_bits <= 0 || bucket_bits > 18 || nclouds == 0)
+    return hipErrorInvalidValue;
+  k_seg_sort<<<nclouds, 1024, 0, st>>>(bucket, n_per, bucket_bits, bucket_bits, keys_out,
+                                       vals_out);
+  return hipGetLastError();
+}
+
 hipError_t launch_cloud_keys(const uint32_t *bucket, uint32_t total, uint32_t n_per,
                              int bucket_bits, uint32_t *key, hipStream_t st) {
   k_cloud_keys<<<cdiv(total, 256), 256, 0, st>>>(bucket, total, n_per, bucket_bits, key);
@@ -969,7 +1072,7 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
 hipError_t preload_build_kernels() {
   return func_attributes(k_cell_keys_dr, k_cloud_bounds, k_range_of_bounds, k_seg_counts,
                          k_cell_keys, k_radix_hist, k_scan_excl, k_scan_sums, k_scan_apply,
-                         k_radix_scatter, k_cloud_keys, k_key2, k_leaf_counts, k_cell_info,
+                         k_radix_scatter, k_seg_sort, k_cloud_keys, k_key2, k_leaf_counts, k_cell_info,
                          k_gather, k_leaf_desc_mixed, k_leaf_desc, k_leaf_bbox, k_l1_init,
                          k_init_state, k_fill_u32, kb_cell_keys_lds<true>,
                          kb_cell_keys_lds<false>, kb_leaf_counts, kb_scans,

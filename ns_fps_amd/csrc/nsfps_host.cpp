@@ -1018,6 +1018,14 @@ nsfps_status sort_logical(const uint32_t *bucket, uint32_t n_per, uint32_t nclou
                           int cloud_bits, int bucket_bits, const Scratch &s, hipStream_t st,
                           uint32_t **keys, uint32_t **lorig) {
   const uint32_t total = n_per * nclouds;
+  // clouds of at most 16,384 points: one workgroup sorts each in LDS
+  // (NSFPS_GLOBAL_SORT=1: always the radix sort over all clouds)
+  if (n_per <= kSegSortMaxPoints && bucket_bits <= 18 && !getenv("NSFPS_GLOBAL_SORT")) {
+    HIP_TRY(launch_seg_sort(bucket, n_per, nclouds, bucket_bits, s.kB, s.vB, st));
+    *keys = s.kB;
+    *lorig = s.vB;
+    return NSFPS_OK;
+  }
   if (nclouds == 1)
     HIP_TRY(hipMemcpyAsync(s.kA, bucket, (size_t)total * 4, hipMemcpyDeviceToDevice, st));
   else

@@ -56,6 +56,14 @@ hipError_t launch_radix_sort(uint32_t *keys, uint32_t *vals, uint32_t *keys_tmp,
                              hipStream_t st);
 // sort key (cloud << bucket_bits) | bucket of clouds of n_per points stored
 // one after another
+constexpr uint32_t kSegSortMaxPoints = 16384;
+// The logical sort of nclouds clouds of n_per <= 16,384 points each (cloud
+// s's buckets at bucket + s * n_per), one workgroup per cloud: the keys
+// ((s << bucket_bits) | bucket) and rows the radix sort over (cloud, bucket)
+// keys writes.  bucket_bits <= 18.
+hipError_t launch_seg_sort(const uint32_t *bucket, uint32_t n_per, uint32_t nclouds,
+                           int bucket_bits, uint32_t *keys_out, uint32_t *vals_out,
+                           hipStream_t st);
 hipError_t launch_cloud_keys(const uint32_t *bucket, uint32_t total, uint32_t n_per,
                              int bucket_bits, uint32_t *key, hipStream_t st);
 hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint32_t *fine,

@@ -84,6 +84,21 @@ def test_workload_hash_in_both_leaf_layouts(yf, lib, wname, mixed, monkeypatch):
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("wname", ["quickstart", "batched_shapes"])
+def test_workload_hash_with_either_logical_sort(yf, lib, wname, monkeypatch):
+    """Clouds of at most 16,384 points are sorted by bucket in one workgroup
+    each, in LDS; NSFPS_GLOBAL_SORT=1 takes the radix sort over all clouds
+    instead.  Both give the reference's samples."""
+    for env in ("1", None):
+        if env:
+            monkeypatch.setenv("NSFPS_GLOBAL_SORT", env)
+        else:
+            monkeypatch.delenv("NSFPS_GLOBAL_SORT", raising=False)
+        w, g, outs = run_workload(yf, lib, wname)
+        assert [len(o) for o in outs] == g["lengths"], env
+        assert [sha256_i32(o) for o in outs] == g["output_sha256"], env
+
+
 def test_clustered_workload_matches_reference_hash(yf, lib):
     if "clustered" not in GOLDEN_CONFIGS:
         pytest.skip("golden hash for the 8,388,608-point workload not generated")
@@ -165,7 +180,7 @@ TREE = {"NSFPS_ENGINE": "tree"}
 
 @pytest.mark.parametrize("env", [
     {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
-    {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
+    {"NSFPS_GLOBAL_SORT": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
     {**TREE, "NSFPS_LATE_THREADS": "1024"},
