@@ -160,6 +160,25 @@ def test_batched_mixed_grids_and_many_clouds(yf, oracle):
         assert np.array_equal(idx[b, :lens[b]], oracle.fps(many[b], 64, None, (16, 16, 16))), b
 
 
+def test_batched_clouds_above_one_workgroup(yf, oracle):
+    """Clouds of more than 16,384 points in one batched call.  Without ranges
+    (16^3 blocks) their bucket populations are counted by several workgroups
+    per cloud, each adding its nonzero bins, and the clouds are sorted
+    together by the radix sort over (cloud, bucket) keys; with a 32^3 range
+    (32,768 buckets) each cloud is built on its own."""
+    rs = np.random.RandomState(12)
+    clouds = rs.randn(3, 40000, 3).astype(np.float32)
+    clouds[1] *= 20
+    clouds[2, 5000:9000] = clouds[2, :4000]  # duplicates
+    idx, lens = yf.fps_batched(clouds, 1500)
+    for b in range(3):
+        assert np.array_equal(idx[b, :lens[b]], oracle.fps(clouds[b], 1500, None, (16, 16, 16))), b
+    rng = (-80.0, 80.0, -80.0, 80.0, -80.0, 80.0, 32, 32, 32)
+    idx, lens = yf.fps_batched(clouds, 1500, [yf.make_range(*rng)] * 3)
+    for b in range(3):
+        assert np.array_equal(idx[b, :lens[b]], oracle.fps(clouds[b], 1500, rng)), b
+
+
 def test_device_pointer_entry_point(lib):
     from ns_fps_amd.capi import Hip
     hip = Hip()
