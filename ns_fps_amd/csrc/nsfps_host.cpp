@@ -482,6 +482,8 @@ struct Arena {
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   int device = -1;
   PinStage pin;
+  char *rb = nullptr;  // pinned buffer of the small read-backs the host waits for
+  size_t rb_cap = 0;
 };
 
 std::mutex g_mu;
@@ -675,6 +677,49 @@ nsfps_status download_host(void *dst, const void *src, size_t bytes, hipStream_t
   return NSFPS_OK;
 }
 
+// The allocation-free entry point's call: nothing may be allocated, so the
+// read-backs below take their pinned buffer only if an earlier call made it.
+bool g_call_no_alloc = false;
+
+// A small read-back the host waits for (build stats, the clouds' statuses):
+// one DMA into a pinned buffer kept per device, then the wait.  A pageable
+// destination made the runtime stage the copy, and the host waited 15-40 us
+// longer per read-back.  Without the buffer the copy is made directly.
+nsfps_status readback(void *dst, const void *src, size_t bytes, hipStream_t st) {
+  Arena *ap = nullptr;
+  if (g_call_no_alloc) {  // the arena as it is: nothing is created or grown
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev >= 0 && dev < 16) ap = &g_arena[dev];
+  } else {
+    const nsfps_status rc = arena_for_device(&ap);
+    if (rc) return rc;
+  }
+  if (ap && ap->rb_cap < bytes && !g_call_no_alloc) {
+    if (ap->rb) HIP_TRY(hipHostFree(ap->rb));
+    ap->rb = nullptr;
+    ap->rb_cap = 0;
+    const size_t want = std::max<size_t>(bytes, size_t(64) << 10);
+    if (injected(kInjAlloc) == hipSuccess &&
+        hipHostMalloc(reinterpret_cast<void **>(&ap->rb), want, hipHostMallocDefault) ==
+            hipSuccess) {
+      ap->rb_cap = want;
+    } else {
+      ap->rb = nullptr;
+      (void)hipGetLastError();
+    }
+  }
+  if (!ap || ap->rb_cap < bytes) {
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return NSFPS_OK;
+  }
+  HIP_TRY(hipMemcpyAsync(ap->rb, src, bytes, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  std::memcpy(dst, ap->rb, bytes);
+  return NSFPS_OK;
+}
+
 // ------------------------------------------------------------ one cloud ----
 
 // Per-cloud words the host polls between batches of rounds, contiguous over
@@ -689,6 +734,7 @@ struct CloudPlan {
   HostRange rng;
   const float *d_xyz_in = nullptr;  // device input, or null to stage h_xyz
   const float *h_xyz = nullptr;
+  int32_t *d_out_user = nullptr;  // the caller's device buffer for the samples, or null
   CloudDev dev{};
   uint32_t slots_ub = 0, leaves_ub = 0, l1_ub = 0;
   // build-time buffers
@@ -876,7 +922,9 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
     p.d_bucket = cb.bucket + o_n;
     p.d_fine = cb.fine + o_n;
     o_n += p.n;
-    p.dev.out = cb.out + o_out;
+    // the samples go to the caller's device buffer when there is one (no copy
+    // after the sampling), else into the call's rows
+    p.dev.out = p.d_out_user ? p.d_out_user : cb.out + o_out;
     o_out += p.m;
   }
 }
@@ -1208,8 +1256,8 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     const size_t o_r = reinterpret_cast<const char *>(cb.drng) - at;
     const size_t o_b = reinterpret_cast<const char *>(cb.dbounds) - at;
     std::vector<char> rb(any_dev ? o_b + hb.size() * 4 : nc * 16);
-    HIP_TRY(hipMemcpyAsync(rb.data(), at, rb.size(), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    const nsfps_status rc = readback(rb.data(), at, rb.size(), st);
+    if (rc) return rc;
     std::memcpy(hs.data(), rb.data(), nc * 16);
     if (any_dev) {
       std::memcpy(hr.data(), rb.data() + o_r, nc * sizeof(RangeDev));
@@ -1354,9 +1402,12 @@ constexpr uint32_t kLeafBoundMaxPoints = 262144;
 // 12.3 with it.
 constexpr uint32_t kSplitMaxNodes = 256;
 
+// ev_end (or null) is recorded after each batch's launches, before its status
+// read-back; fin gets the clouds' statuses after the last batch.
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
-                        uint64_t *rounds_out, uint32_t *split_out) {
+                        uint64_t *rounds_out, uint32_t *split_out, hipEvent_t ev_end,
+                        std::vector<CloudStatus> &fin) {
   uint32_t max_nl1 = 1;
   bool alias = false;  // some cloud's cells share buckets
   bool leaf_bound = true;  // every cloud small enough for the leaf-box bound
@@ -1397,9 +1448,11 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       used.emplace_back(batch, passes);
     }
     launched = false;
-    HIP_TRY(hipMemcpyAsync(pr.data(), d_status, nc * sizeof(CloudStatus), hipMemcpyDeviceToHost,
-                           st));
-    HIP_TRY(hipStreamSynchronize(st));
+    if (ev_end) HIP_TRY(hipEventRecord(ev_end, st));
+    {
+      const nsfps_status rc = readback(pr.data(), d_status, nc * sizeof(CloudStatus), st);
+      if (rc) return rc;
+    }
     bool all = true;
     uint64_t samples = 0, rounds = 0;
     for (auto &q : pr) {
@@ -1422,6 +1475,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       std::copy(shape, shape + 5, g_schedule.shape);
       g_schedule.batches = used;
       g_schedule.rounds = rounds;
+      fin = pr;
       break;
     }
     // every round takes at least one sample of every unfinished cloud
@@ -1501,9 +1555,10 @@ bool choose_runs(std::vector<CloudPlan> &plans) {
 // Samples the built clouds (descriptors in plans[i].dev): grid-wide steps for
 // the first iterations of a single cloud on the tree engine, then its loop;
 // or the speculative-run rounds.
+// fin: the runs engine's final statuses (left empty by the tree engine)
 nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
                            bool runs, uint64_t *rounds, uint64_t *wide_total,
-                           uint32_t *update_split) {
+                           uint32_t *update_split, std::vector<CloudStatus> &fin) {
   hipStream_t st = ws.st;
   std::vector<CloudDev> devs;
   uint32_t lds_bytes = 0;
@@ -1521,7 +1576,8 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
                            hipMemcpyHostToDevice, st));
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
     if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
-    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, update_split);
+    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, update_split,
+                      ws.ev ? ws.ev[2] : nullptr, fin);
   }
   if (plans.size() == 1) {
     uint32_t e = wide_iters_for(plans[0]);
@@ -1542,17 +1598,20 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
 
 // After sampling: lengths, the samples to the host (out_on_host) and the
 // statistics of the call (t0: host time at its start).
+// fin: the clouds' final statuses when the sampling read them back already
+// (the runs engine's last batch), else empty.
 nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
                          bool runs, uint64_t rounds, uint64_t wide_total, uint32_t update_split,
-                         bool out_on_host,
+                         std::vector<CloudStatus> &fin, bool out_on_host,
                          int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
                          std::chrono::steady_clock::time_point t0) {
   hipStream_t st = ws.st;
-  if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[2], st));
-  std::vector<CloudStatus> fin(plans.size());
-  HIP_TRY(hipMemcpyAsync(fin.data(), L.d_status, fin.size() * sizeof(CloudStatus),
-                         hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  if (fin.size() != plans.size()) {
+    if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[2], st));
+    fin.assign(plans.size(), CloudStatus{});
+    const nsfps_status rc = readback(fin.data(), L.d_status, fin.size() * sizeof(CloudStatus), st);
+    if (rc) return rc;
+  }
   uint64_t samples = 0, leaves = 0, points = 0;
   uint32_t maxlen = 0, lds_bytes = 0;
   for (size_t i = 0; i < plans.size(); ++i) {
@@ -1609,7 +1668,6 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
 
 // One call from start to end over workspace ws: layout, build, sampling,
 // results.  ws.base == null takes the calling thread's device arena.
-// layout_out: where the call's buffers lie, for callers that copy from them.
 // A call that fails after enqueuing work waits for its stream before
 // returning, so that no kernel of it still runs when the next call reuses the
 // workspace (the wait's own status is ignored: the first error is reported).
@@ -1618,11 +1676,10 @@ nsfps_status run_clouds_once(std::vector<CloudPlan> &plans, Ws &ws, bool out_on_
                              CallLayout &L);
 
 nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, int32_t *h_out,
-                        uint64_t out_stride, uint64_t *out_lens, CallLayout *layout_out = nullptr) {
+                        uint64_t out_stride, uint64_t *out_lens) {
   CallLayout L;
   const nsfps_status rc = run_clouds_once(plans, ws, out_on_host, h_out, out_stride, out_lens, L);
   if (rc && ws.st_used) (void)hipStreamSynchronize(ws.st);
-  if (layout_out) *layout_out = L;
   return rc;
 }
 
@@ -1658,9 +1715,10 @@ nsfps_status run_clouds_once(std::vector<CloudPlan> &plans, Ws &ws, bool out_on_
   if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[1], st));
   uint64_t rounds = 0, wide_total = 0;
   uint32_t update_split = 0;
-  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &update_split);
+  std::vector<CloudStatus> fin;
+  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &update_split, fin);
   if (rc) return rc;
-  return finish_call(plans, L, ws, runs, rounds, wide_total, update_split, out_on_host, h_out,
+  return finish_call(plans, L, ws, runs, rounds, wide_total, update_split, fin, out_on_host, h_out,
                      out_stride, out_lens, t0);
 }
 
@@ -1994,16 +2052,13 @@ nsfps_status nsfps_fps_batched_device(const float *d_xyz, uint64_t batch, uint64
     std::vector<CloudPlan> plans(batch);
     rc = plan_clouds(plans, n, m, ranges, bl);
     if (rc) return rc;
-    for (uint64_t b = 0; b < batch; ++b) plans[b].d_xyz_in = d_xyz + b * n * 3;
+    for (uint64_t b = 0; b < batch; ++b) {
+      plans[b].d_xyz_in = d_xyz + b * n * 3;
+      plans[b].d_out_user = d_out + b * m;  // row b of the caller's buffer
+    }
     Ws ws;
     ws.st = st;
-    CallLayout L;
-    rc = run_clouds(plans, ws, false, nullptr, 0, out_lens, &L);
-    if (rc) return rc;
-    // the clouds' rows of m entries lie back to back in the call's output
-    HIP_TRY(hipMemcpyAsync(d_out, L.cb.out, batch * m * 4, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipStreamSynchronize(st));
-    return NSFPS_OK;
+    return run_clouds(plans, ws, false, nullptr, 0, out_lens);
   });
 }
 
@@ -2093,13 +2148,10 @@ nsfps_status nsfps_fps_device(const float *d_xyz, uint64_t n, uint64_t m, const 
     p.m = (uint32_t)m;
     derive(*range, p.rng);
     p.d_xyz_in = d_xyz;
+    p.d_out_user = d_out;
     Ws ws;
     ws.st = st;
-    rc = run_clouds(plans, ws, false, nullptr, 0, out_len);
-    if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipStreamSynchronize(st));
-    return NSFPS_OK;
+    return run_clouds(plans, ws, false, nullptr, 0, out_len);
   });
 }
 
@@ -2123,6 +2175,10 @@ nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t m
     void *ws_base = nullptr;
     rc = scratch_for_device(&ws_base);
     if (rc) return rc;
+    struct NoAlloc {  // for this call only, whichever way it returns
+      NoAlloc() { g_call_no_alloc = true; }
+      ~NoAlloc() { g_call_no_alloc = false; }
+    } no_alloc;
     if (n == 0 || m == 0 || m >= n || m == 1) {
       int32_t first[1] = {0};
       std::vector<int32_t> tmp;
@@ -2146,15 +2202,12 @@ nsfps_status nsfps_fps_device_noalloc(const float *d_xyz, uint64_t n, uint64_t m
     p.m = (uint32_t)m;
     derive(*range, p.rng);
     p.d_xyz_in = d_xyz;
+    p.d_out_user = d_out;
     Ws ws;
     ws.base = (char *)ws_base;
     ws.cap = kScratchBytes;
     ws.st = st;
-    rc = run_clouds(plans, ws, false, nullptr, 0, out_len);
-    if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(d_out, p.dev.out, (size_t)*out_len * 4, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipStreamSynchronize(st));
-    return NSFPS_OK;
+    return run_clouds(plans, ws, false, nullptr, 0, out_len);
   });
 }
 
@@ -2292,10 +2345,11 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
       HIP_TRY(hipEventRecord(P.ev[1], st));
       uint64_t rounds = 0, wide_total = 0;
       uint32_t update_split = 0;
+      std::vector<CloudStatus> fin;
       const nsfps_status rc =
-          sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split);
+          sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split, fin);
       if (rc) return rc;
-      return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, false,
+      return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, fin, false,
                          nullptr, 0, out_len, t0);
     };
     const nsfps_status rc = body();
@@ -2553,6 +2607,11 @@ void nsfps_release_workspace(void) {
       a.pin.p = nullptr;
       a.pin.cap = 0;
       a.pin.pending = false;
+    }
+    if (a.rb) {
+      (void)hipHostFree(a.rb);
+      a.rb = nullptr;
+      a.rb_cap = 0;
     }
   }
 }
