@@ -72,6 +72,11 @@ class Lib:
     def device_count(self):
         return self.lib.nsfps_device_count()
 
+    def init_device(self):
+        """nsfps_init_device: the current device's one-time set-up, ahead of
+        its first call."""
+        self._check(self.lib.nsfps_init_device())
+
     def fps(self, points, n_samples, rng=None):
         p = np.ascontiguousarray(points, dtype=np.float32)
         out = np.zeros(max(int(n_samples), 1), np.int32)
