@@ -910,7 +910,11 @@ constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
 // hot set, the copies left over going back to the next selection: ranking
 // them again in further phases measured slower (uniform cube 8.36 ms per call
 // at 12, 8.26 at 32, 8.20 at 48, 8.09 at kHot; LiDAR scan 5.38 / 5.26 / 5.19 /
-// 5.14 ms).
+// 5.14 ms).  Measured again on the later kernels, further phases at 32 gain
+// only where phases accept few samples (quickstart, about 20 of 64: 0.711
+// against 0.732 ms) and lose elsewhere (uniform cube 8.02 against 7.70 ms,
+// clustered cloud 73.5 against 69.8); allowing them only after a phase of at
+// most 24 samples still cost the uniform cube 3 % and the clustered cloud 4 %.
 constexpr uint32_t kPhaseMin = kHot;
 // Cubes over more coarse rows, or with more list entries in one lane's rows,
 // are applied by every thread to its own entries instead of walked.  Rows
