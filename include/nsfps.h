@@ -119,11 +119,13 @@ const char *nsfps_version(void);
 int nsfps_device_count(void);
 
 /* Prepares the current device for the library's calls: loads its kernels
- * (the runtime loads code on a kernel's first use) and creates the stream and
- * events the host-buffer calls use.  No counterpart in the reference (a CPU
- * library).  Optional: the first call on a device does the same; calling
- * this first keeps that one-time work (tens of milliseconds) out of the
- * first call.  NSFPS_EDEVICE when no device is visible. */
+ * (the runtime loads code on a kernel's first use), creates the stream and
+ * events the host-buffer calls use, and makes one copy each way through a
+ * pinned buffer (the runtime sets its copy path up on first use).  No
+ * counterpart in the reference (a CPU library).  Optional: the first call on
+ * a device does the same; calling this first keeps that one-time work (tens
+ * of milliseconds, most of it the runtime's own start) out of the first
+ * call.  NSFPS_EDEVICE when no device is visible. */
 nsfps_status nsfps_init_device(void);
 
 /* Derived fields and Morton LUTs of a range.  luts receives the x, y and z
