@@ -490,12 +490,6 @@ __device__ __forceinline__ void cell_info_at(uint32_t b, const uint32_t *__restr
   info[b] = make_uint2(cell_start[b], cell_leaf[b]);
 }
 
-__global__ void k_cell_info(const uint32_t *__restrict__ cell_start,
-                            const uint32_t *__restrict__ cell_leaf, uint32_t T,
-                            uint2 *__restrict__ info) {
-  cell_info_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, info);
-}
-
 // Gather into physical slots; min-distance starts at FLT_MAX
 // (src/yuezu_fps.cpp:215-223).  Dense: slot = physical position p.  Padded:
 // slot = bucket * cap + (p - first position of the bucket).
@@ -588,21 +582,24 @@ __device__ __forceinline__ void leaf_desc_mixed_at(uint32_t l, uint32_t n, uint3
   leaf_al[l] = kNoCell;  // one cell per bucket (r.na == 1)
 }
 
-__global__ void k_leaf_desc_mixed(uint32_t n, uint32_t nleaves, float4 *__restrict__ leaf_lo,
-                                  float4 *__restrict__ leaf_hi, uint32_t *__restrict__ leaf_cell,
-                                  uint32_t *__restrict__ leaf_al, uint2 *__restrict__ leaf_sc) {
-  leaf_desc_mixed_at(blockIdx.x * blockDim.x + threadIdx.x, n, nleaves, leaf_lo, leaf_hi, leaf_cell,
-                     leaf_al, leaf_sc);
-}
-
-__global__ void k_leaf_desc(const uint32_t *__restrict__ cell_start,
-                            const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
-                            uint32_t cap, uint32_t lpc, RangeDev r, const float4 *__restrict__ P4,
-                            float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
-                            uint32_t *__restrict__ leaf_cell, uint32_t *__restrict__ leaf_al,
-                            uint2 *__restrict__ leaf_sc) {
-  leaf_desc_at(blockIdx.x * blockDim.x + threadIdx.x, cell_start, cell_leaf, T, padded, cap, lpc,
-               r, P4, leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
+// One cloud's cell table and leaf descriptors in one launch: thread i
+// writes cell i's table entry and the leaves of bucket i (with mixed leaves,
+// leaf i).  Two launches before; the small clouds' build waits on each
+// launch's host time.
+__global__ void k_cells(const uint32_t *__restrict__ cell_start,
+                        const uint32_t *__restrict__ cell_leaf, uint32_t T, uint32_t padded,
+                        uint32_t cap, uint32_t lpc, uint32_t mixed, uint32_t n, uint32_t nleaves,
+                        RangeDev r, const float4 *__restrict__ P4, uint2 *__restrict__ info,
+                        float4 *__restrict__ leaf_lo, float4 *__restrict__ leaf_hi,
+                        uint32_t *__restrict__ leaf_cell, uint32_t *__restrict__ leaf_al,
+                        uint2 *__restrict__ leaf_sc) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  cell_info_at(i, cell_start, cell_leaf, T, info);
+  if (mixed)
+    leaf_desc_mixed_at(i, n, nleaves, leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
+  else
+    leaf_desc_at(i, cell_start, cell_leaf, T, padded, cap, lpc, r, P4, leaf_lo, leaf_hi, leaf_cell,
+                 leaf_al, leaf_sc);
 }
 
 // Leaf bounding boxes, the corners of their points' cells, and initial keys
@@ -733,21 +730,6 @@ __device__ __forceinline__ void l1_init_at(uint32_t g, uint32_t nleaves, uint32_
   }
 }
 
-__global__ __launch_bounds__(256) void k_l1_init(uint32_t nleaves, uint32_t nl1,
-                                                 const uint64_t *__restrict__ leaf_key,
-                                                 const float4 *__restrict__ leaf_pos,
-                                                 const float4 *__restrict__ leaf_lo,
-                                                 const float4 *__restrict__ leaf_hi,
-                                                 uint64_t *__restrict__ l1_key,
-                                                 float4 *__restrict__ l1_pos,
-                                                 const uint32_t *__restrict__ leaf_al,
-                                                 uint32_t na,
-                                                 float4 *__restrict__ l1_lo,
-                                                 float4 *__restrict__ l1_hi,
-                                                 uint2 *__restrict__ l1_cbox) {
-  l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), nleaves, nl1, leaf_key, leaf_pos, leaf_lo,
-             leaf_hi, leaf_al, na, l1_key, l1_pos, l1_lo, l1_hi, l1_cbox);
-}
 
 __device__ __forceinline__ void init_state_of(const CloudDev &c, const uint32_t *phys0) {
   *c.iter = 0;
@@ -759,6 +741,17 @@ __device__ __forceinline__ void init_state_of(const CloudDev &c, const uint32_t 
 
 __global__ void k_init_state(CloudDev c, const uint32_t *__restrict__ phys0) {
   if (threadIdx.x == 0 && blockIdx.x == 0) init_state_of(c, phys0);
+}
+
+// One cloud's level-1 nodes (a wave each), and its run state (block 0,
+// thread 0: it reads none of the nodes).
+__global__ __launch_bounds__(256) void k_l1_init_state(CloudDev c,
+                                                       const uint32_t *__restrict__ phys0) {
+  l1_init_at(blockIdx.x * 4 + (threadIdx.x >> 6), c.nleaves, c.nl1, c.leaf_key, c.leaf_pos,
+             c.leaf_lo, c.leaf_hi, c.leaf_al, c.r.na, c.l1_key, c.l1_pos,
+             const_cast<float4 *>(c.l1_lo), const_cast<float4 *>(c.l1_hi),
+             const_cast<uint2 *>(c.l1_cbox));
+  if (blockIdx.x == 0 && threadIdx.x == 0) init_state_of(c, phys0);
 }
 
 // Fills 32-bit words (clears flags, counters and tables with a kernel, not a
@@ -896,12 +889,6 @@ hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, 
   return hipGetLastError();
 }
 
-hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
-                            uint2 *info, hipStream_t st) {
-  k_cell_info<<<cdiv((uint64_t)T + 1, 256), 256, 0, st>>>(cell_start, cell_leaf, T, info);
-  return hipGetLastError();
-}
-
 hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
                          const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
                          uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
@@ -917,15 +904,12 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
                              const uint2 *RO, float4 *leaf_lo, float4 *leaf_hi,
                              uint32_t *leaf_cell, uint32_t *leaf_al, uint2 *leaf_sc,
                              uint2 *leaf_cbox, uint64_t *leaf_key, float4 *leaf_pos,
-                             hipStream_t st) {
-  if (mixed) {
-    if (nleaves)
-      k_leaf_desc_mixed<<<cdiv(nleaves, 256), 256, 0, st>>>(n, nleaves, leaf_lo, leaf_hi, leaf_cell,
-                                                            leaf_al, leaf_sc);
-  } else {
-    k_leaf_desc<<<cdiv(T, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, r, P4,
-                                              leaf_lo, leaf_hi, leaf_cell, leaf_al, leaf_sc);
-  }
+                             uint2 *cell_info, hipStream_t st) {
+  // the cell table has T + 1 entries; mixed leaves are described one a thread
+  const uint64_t cells = (uint64_t)T + 1, threads = mixed && nleaves > cells ? nleaves : cells;
+  k_cells<<<cdiv(threads, 256), 256, 0, st>>>(cell_start, cell_leaf, T, padded, cap, lpc, mixed, n,
+                                              nleaves, r, P4, cell_info, leaf_lo, leaf_hi,
+                                              leaf_cell, leaf_al, leaf_sc);
   if (nleaves)
     k_leaf_bbox<<<cdiv(nleaves, 4), 256, 0, st>>>(nleaves, r, P4, RO, leaf_lo, leaf_hi, leaf_cbox,
                                                   leaf_key, leaf_pos);
@@ -934,12 +918,9 @@ hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_le
 
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st) {
   if (c.nl1)
-    k_l1_init<<<cdiv(c.nl1, 4), 256, 0, st>>>(c.nleaves, c.nl1, c.leaf_key, c.leaf_pos, c.leaf_lo,
-                                              c.leaf_hi, c.l1_key, c.l1_pos, c.leaf_al, c.r.na,
-                                              const_cast<float4 *>(c.l1_lo),
-                                              const_cast<float4 *>(c.l1_hi),
-                                              const_cast<uint2 *>(c.l1_cbox));
-  k_init_state<<<1, 64, 0, st>>>(c, d_phys0);
+    k_l1_init_state<<<cdiv(c.nl1, 4), 256, 0, st>>>(c, d_phys0);
+  else
+    k_init_state<<<1, 64, 0, st>>>(c, d_phys0);
   return hipGetLastError();
 }
 
@@ -1072,8 +1053,8 @@ hipError_t launch_build_rest_many(const BuildDev *d_bd, uint32_t nclouds, uint32
 hipError_t preload_build_kernels() {
   return func_attributes(k_cell_keys_dr, k_cloud_bounds, k_range_of_bounds, k_seg_counts,
                          k_cell_keys, k_radix_hist, k_scan_excl, k_scan_sums, k_scan_apply,
-                         k_radix_scatter, k_seg_sort, k_cloud_keys, k_key2, k_leaf_counts, k_cell_info,
-                         k_gather, k_leaf_desc_mixed, k_leaf_desc, k_leaf_bbox, k_l1_init,
+                         k_radix_scatter, k_seg_sort, k_cloud_keys, k_key2, k_leaf_counts, k_cells,
+                         k_gather, k_leaf_bbox, k_l1_init_state,
                          k_init_state, k_fill_u32, kb_cell_keys_lds<true>,
                          kb_cell_keys_lds<false>, kb_leaf_counts, kb_scans,
                          kb_zero_slots, kb_gather, kb_cells, kb_leaf_bbox, kb_l1_init,

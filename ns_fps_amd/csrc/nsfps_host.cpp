@@ -1147,12 +1147,12 @@ nsfps_status finish_cloud(CloudPlan &p, const uint32_t *lorig, const uint32_t *p
   HIP_TRY(launch_gather(prank, lorig, base, p.d_bucket, p.d_counts, xyz, n, c.padded,
                         (uint32_t)p.cap, c.P4, const_cast<uint2 *>(c.RO), const_cast<uint32_t *>(c.R),
                         p.d_small + 2, st));
-  HIP_TRY(launch_cell_info(p.d_counts, p.d_lc, T, p.d_cell_info, st));
   HIP_TRY(launch_leaf_build(p.d_counts, p.d_lc, T, c.padded, (uint32_t)p.cap, c.lpc, c.mixed, n,
                             c.nleaves, p.rng.dev, c.P4, c.RO, const_cast<float4 *>(c.leaf_lo),
                             const_cast<float4 *>(c.leaf_hi), const_cast<uint32_t *>(c.leaf_cell),
                             const_cast<uint32_t *>(c.leaf_al), const_cast<uint2 *>(c.leaf_sc),
-                            const_cast<uint2 *>(c.leaf_cbox), c.leaf_key, c.leaf_pos, st));
+                            const_cast<uint2 *>(c.leaf_cbox), c.leaf_key, c.leaf_pos,
+                            p.d_cell_info, st));
   HIP_TRY(launch_init_state(c, p.d_small + 2, st));
   c.lds = plan_lds(c);
   return NSFPS_OK;

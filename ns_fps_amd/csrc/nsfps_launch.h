@@ -71,23 +71,22 @@ hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint
                        uint32_t *key2, hipStream_t st);
 hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
                               uint32_t *total, hipStream_t st);
-hipError_t launch_cell_info(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
-                            uint2 *info, hipStream_t st);
 // prank / lorig may come from sorts holding other clouds too: ranks and rows
 // of this cloud are base + 0 .. base + n - 1 (prank points at this cloud's part)
 hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
                          const uint32_t *bucket, const uint32_t *cell_start, const float *xyz,
                          uint32_t n, uint32_t padded, uint32_t cap, float4 *P4, uint2 *RO,
                          uint32_t *R, uint32_t *phys0, hipStream_t st);
-// Leaves: per bucket (padded or dense), or with mixed = 1 runs of 64 slots
-// of the logical order; then their boxes, cell corners and initial keys.
+// The cell table (cell_info, T + 1 entries) and the leaves: per bucket
+// (padded or dense), or with mixed = 1 runs of 64 slots of the logical order;
+// then their boxes, cell corners and initial keys.
 hipError_t launch_leaf_build(const uint32_t *cell_start, const uint32_t *cell_leaf, uint32_t T,
                              uint32_t padded, uint32_t cap, uint32_t lpc, uint32_t mixed,
                              uint32_t n, uint32_t nleaves, const RangeDev &r, const float4 *P4,
                              const uint2 *RO, float4 *leaf_lo, float4 *leaf_hi,
                              uint32_t *leaf_cell, uint32_t *leaf_al, uint2 *leaf_sc,
                              uint2 *leaf_cbox, uint64_t *leaf_key, float4 *leaf_pos,
-                             hipStream_t st);
+                             uint2 *cell_info, hipStream_t st);
 hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStream_t st);
 
 // The build of many clouds, each step one launch for all of them (grid y =
