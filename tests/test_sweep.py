@@ -93,3 +93,88 @@ def test_gpu_round_schedule_of_one_cloud_on_others(yf, oracle):
     for order in ([0, 1, 2, 3], [2, 0, 3, 1, 1, 2]):
         for i in order:
             assert np.array_equal(yf.fps(clouds[i], m, yf.make_range(*rng)), want[i]), (order, i)
+
+
+# A second sweep over other regimes: clouds a few cells wide inside a range
+# many cells wide (every cube then holds every point, as in the README's
+# example), shells (many near-equal distances), two far-apart clusters,
+# heavy duplication (the run ends at distance 0), skewed densities, points on
+# the cell boundaries of a power-of-two grid, and a dense core with far
+# outliers; ranges symmetric, asymmetric, or found from the points
+# (range=None, the reference's compute_bbox with the case's block counts).
+SHAPES2 = ["speck", "shell", "far", "dups", "skewed", "aligned", "outliers"]
+
+
+def make_case2(seed):
+    rs = np.random.RandomState(5000 + seed)
+    shape = SHAPES2[seed % len(SHAPES2)]
+    n = int(rs.randint(100, 30000))
+    if shape == "speck":
+        p = rs.randn(n, 3) * float(rs.choice([0.001, 0.01, 0.05]))
+    elif shape == "shell":
+        v = rs.randn(n, 3)
+        p = 0.8 * v / np.linalg.norm(v, axis=1, keepdims=True)
+    elif shape == "far":
+        p = rs.randn(n, 3) * 0.01 + np.where(rs.rand(n, 1) < 0.5, -0.9, 0.9)
+    elif shape == "dups":
+        base = rs.uniform(-1, 1, (int(rs.randint(1, 40)), 3))
+        p = base[rs.randint(0, len(base), n)]
+    elif shape == "skewed":
+        p = np.sign(rs.randn(n, 3)) * rs.exponential(0.1, (n, 3))
+    elif shape == "aligned":
+        k = int(rs.choice([2, 4, 8, 16]))
+        p = rs.randint(-k, k + 1, (n, 3)) / k
+    else:  # outliers
+        p = rs.randn(n, 3) * 0.05
+        far = rs.randint(0, n, max(1, n // 1000))
+        p[far] = rs.uniform(-1, 1, (len(far), 3))
+    p = np.ascontiguousarray(p, dtype=np.float32)
+    blocks = tuple(int(rs.choice([1, 2, 3, 4, 6, 8, 10, 16, 24, 32, 64])) for _ in range(3))
+    if seed % 2 == 0:
+        blocks = tuple(int(rs.choice([1, 2, 4, 8, 16, 32, 64])) for _ in range(3))
+    r1, r2 = int(rs.randint(1, n + 1)), int(rs.randint(1, min(n, 2000) + 1))
+    m = int(rs.choice([2, r1, r2, r2, n + 5]))
+    if seed % 4 == 3:
+        rng = None
+    elif seed % 4 == 1:
+        lo = rs.uniform(-1.3, -0.6, 3)
+        hi = rs.uniform(0.6, 1.3, 3)
+        rng = (float(lo[0]), float(hi[0]), float(lo[1]), float(hi[1]), float(lo[2]), float(hi[2]),
+               *blocks)
+    else:
+        rng = (-1.0, 1.0, -1.0, 1.0, -1.0, 1.0, *blocks)
+    return shape, p, m, rng, blocks
+
+
+SEEDS2 = list(range(42))
+
+
+def _ids2(seed):
+    shape, p, m, rng, blocks = make_case2(seed)
+    return f"{seed}-{shape}-{len(p)}-{m}-{'x'.join(map(str, blocks))}{'-bbox' if rng is None else ''}"
+
+
+@pytest.mark.parametrize("seed", SEEDS2, ids=_ids2)
+def test_oracle_matches_reference_on_second_sweep(oracle, seed):
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libyuezu_ref.so")
+    if not os.path.exists(ref_so):
+        pytest.skip("oracle/_ref not built (needs the reference sources)")
+    from oracle import Reference
+    shape, p, m, rng, blocks = make_case2(seed)
+    want = Reference(ref_so).fps(p, m, rng, blocks=blocks)
+    assert np.array_equal(oracle.fps(p, m, rng, blocks=blocks), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", SEEDS2, ids=_ids2)
+def test_gpu_matches_oracle_on_second_sweep(yf, oracle, seed):
+    from ns_fps_amd.capi import Lib
+    shape, p, m, rng, blocks = make_case2(seed)
+    if rng is None:
+        got = Lib().fps_bbox(p, m, blocks)
+    else:
+        got = yf.fps(p, m, yf.make_range(*rng))
+    want = oracle.fps(p, m, rng, blocks=blocks)
+    assert got.dtype == np.int32
+    assert np.array_equal(got, want), (len(got), len(want), f"first difference at "
+                                       f"{np.argmax(got[:len(want)] != want[:len(got)])}")
