@@ -102,7 +102,8 @@ typedef struct {
   uint32_t update_split; /* workgroups per level-1 node of the runs engine's update pass
                            (1, or 4 when the call has few level-1 nodes) */
   uint32_t mixed;       /* 1 when leaves were runs of 64 slots that may hold several buckets */
-  uint32_t reserved;
+  uint32_t hot_set;     /* copies per hot set of the runs engine's run kernel (64 or 128;
+                           0 for the tree loop) */
 } nsfps_stats;
 
 /* Library constants mirrored from src/yuezu_fps.h:19-50. */

@@ -41,7 +41,7 @@ class Stats(ctypes.Structure):
                 ("padded", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32),
                 ("rounds", ctypes.c_uint64), ("engine", ctypes.c_uint32),
                 ("update_split", ctypes.c_uint32),
-                ("mixed", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("mixed", ctypes.c_uint32), ("hot_set", ctypes.c_uint32)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

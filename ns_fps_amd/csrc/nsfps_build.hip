@@ -456,10 +456,11 @@ __global__ void k_key2(const uint32_t *__restrict__ lorig, const uint32_t *__res
 __device__ __forceinline__ void leaf_counts_block(uint32_t blk, const uint32_t *__restrict__ counts,
                                                   uint32_t T, uint32_t *__restrict__ lc,
                                                   uint32_t *__restrict__ maxocc,
-                                                  uint32_t *__restrict__ total, uint32_t *s_red) {
-  // s_red[0]: leaves of the block, s_red[1]: its largest bucket (one global
-  // atomic each per block)
-  if (threadIdx.x < 2) s_red[threadIdx.x] = 0;
+                                                  uint32_t *__restrict__ total,
+                                                  uint32_t *__restrict__ occupied, uint32_t *s_red) {
+  // s_red[0]: leaves of the block, s_red[1]: its largest bucket, s_red[2]:
+  // its buckets holding points (one global atomic each per block)
+  if (threadIdx.x < 3) s_red[threadIdx.x] = 0;
   __syncthreads();
   uint32_t b = blk * blockDim.x + threadIdx.x;
   if (b < T) {
@@ -468,19 +469,22 @@ __device__ __forceinline__ void leaf_counts_block(uint32_t blk, const uint32_t *
     if (c) {
       atomicMax(&s_red[1], c);
       atomicAdd(&s_red[0], (c + kLeaf - 1) / kLeaf);
+      atomicAdd(&s_red[2], 1u);
     }
   }
   __syncthreads();
   if (threadIdx.x == 0 && s_red[0]) atomicAdd(total, s_red[0]);
   if (threadIdx.x == 1 && s_red[1]) atomicMax(maxocc, s_red[1]);
+  if (threadIdx.x == 2 && s_red[2]) atomicAdd(occupied, s_red[2]);
 }
 
 __global__ __launch_bounds__(256) void k_leaf_counts(const uint32_t *__restrict__ counts,
                                                      uint32_t T, uint32_t *__restrict__ lc,
                                                      uint32_t *__restrict__ maxocc,
-                                                     uint32_t *__restrict__ total) {
-  __shared__ uint32_t s_red[2];
-  leaf_counts_block(blockIdx.x, counts, T, lc, maxocc, total, s_red);
+                                                     uint32_t *__restrict__ total,
+                                                     uint32_t *__restrict__ occupied) {
+  __shared__ uint32_t s_red[3];
+  leaf_counts_block(blockIdx.x, counts, T, lc, maxocc, total, occupied, s_red);
 }
 
 __device__ __forceinline__ void cell_info_at(uint32_t b, const uint32_t *__restrict__ cell_start,
@@ -884,8 +888,8 @@ hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint
 }
 
 hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
-                              uint32_t *total, hipStream_t st) {
-  k_leaf_counts<<<cdiv(T, 256), 256, 0, st>>>(counts, T, lc, maxocc, total);
+                              uint32_t *total, uint32_t *occupied, hipStream_t st) {
+  k_leaf_counts<<<cdiv(T, 256), 256, 0, st>>>(counts, T, lc, maxocc, total, occupied);
   return hipGetLastError();
 }
 
@@ -954,10 +958,10 @@ __global__ __launch_bounds__(1024) void kb_cell_keys_lds(const BuildDev *__restr
 }
 
 __global__ __launch_bounds__(256) void kb_leaf_counts(const BuildDev *__restrict__ bd) {
-  __shared__ uint32_t s_red[2];
+  __shared__ uint32_t s_red[3];
   const BuildDev &b = bd[blockIdx.y];
   if (blockIdx.x * blockDim.x >= b.T) return;  // the whole block: no barrier is split
-  leaf_counts_block(blockIdx.x, b.counts, b.T, b.lc, b.small + 1, b.small + 3, s_red);
+  leaf_counts_block(blockIdx.x, b.counts, b.T, b.lc, b.small + 1, b.small + 3, b.small + 4, s_red);
 }
 
 // block 2i scans cloud i's bucket populations, block 2i + 1 its leaf counts

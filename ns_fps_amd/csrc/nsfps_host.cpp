@@ -757,7 +757,9 @@ struct CloudPlan {
   // build-time buffers
   float *d_xyz_stage = nullptr;
   uint32_t *d_lut = nullptr, *d_counts = nullptr, *d_lc = nullptr;
-  uint32_t *d_small = nullptr;  // [0] non-finite flag, [1] max occupancy, [2] phys0
+  uint32_t *d_small = nullptr;  // kStatWords: [0] non-finite flag, [1] max occupancy, [2] phys0,
+                                //   [3] dense leaves, [4] occupied buckets
+  uint32_t occupied = 0;        // buckets holding points
   uint2 *d_cell_info = nullptr;
   uint32_t *d_bucket = nullptr, *d_fine = nullptr;  // per point: bucket, sub-cell code
   uint64_t cap = 0;                // slots per bucket in the padded layout
@@ -914,7 +916,7 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
   cb.counts = bp.take<uint32_t>(cb.counts_total);
   // small, drng and dbounds one after another: the build reads them back
   // in one copy
-  cb.small = bp.take<uint32_t>(4 * plans.size());
+  cb.small = bp.take<uint32_t>(kStatWords * plans.size());
   cb.drng = bp.take<RangeDev>(plans.size());
   cb.dbounds = bp.take<float>(6 * plans.size());
   cb.bucket = bp.take<uint32_t>(cb.n_total);
@@ -935,7 +937,7 @@ void layout_call(Bump &bp, std::vector<CloudPlan> &plans, CallBuffers &cb) {
     }
     p.d_counts = cb.counts + o_c;
     o_c += (size_t)p.rng.dev.T + 1;
-    p.d_small = cb.small + 4 * i;
+    p.d_small = cb.small + kStatWords * i;
     p.d_bucket = cb.bucket + o_n;
     p.d_fine = cb.fine + o_n;
     o_n += p.n;
@@ -998,7 +1000,8 @@ nsfps_status build_phase1(CloudPlan &p, const CloudPlan *lut_of, const Scratch &
     if (rc) return rc;
     HIP_TRY(launch_seg_counts(*keys, p.n, p.d_counts, st));
   }
-  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, p.d_small + 3, st));
+  HIP_TRY(launch_leaf_counts(p.d_counts, T, p.d_lc, p.d_small + 1, p.d_small + 3, p.d_small + 4,
+                             st));
   HIP_TRY(launch_scan(p.d_counts, T, s.scan, st));  // -> first dense position per bucket
   HIP_TRY(launch_scan(p.d_lc, T, s.scan, st));      // -> first leaf per bucket (dense)
   return NSFPS_OK;
@@ -1038,7 +1041,7 @@ bool mixed_wanted(const std::vector<CloudPlan> &plans, const uint32_t *hs) {
     if (p.tree || !p.rng.dev.bijective) return false;
     bool padded;
     uint64_t cap;
-    leaves += bucket_leaves(p, hs + 4 * i, &padded, &cap);
+    leaves += bucket_leaves(p, hs + kStatWords * i, &padded, &cap);
     points += p.n;
   }
   if (e && atoi(e) == 1) return true;
@@ -1049,6 +1052,7 @@ nsfps_status decide_layout(CloudPlan &p, const uint32_t *hs, bool mixed) {
   CloudDev &c = p.dev;
   const uint32_t n = p.n, T = p.rng.dev.T;
   if (hs[0]) return fail(NSFPS_EINVAL, "points must be finite");
+  p.occupied = hs[4];
   bool padded;
   uint64_t cap;
   const uint64_t leaves = bucket_leaves(p, hs, &padded, &cap);
@@ -1180,7 +1184,7 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     if (rc) return rc;
   }
   HIP_TRY(launch_fill_u32(cb.counts, 0u, cb.counts_total, st));
-  HIP_TRY(launch_fill_u32(cb.small, 0u, nc * 4, st));
+  HIP_TRY(launch_fill_u32(cb.small, 0u, nc * kStatWords, st));
   // many clouds sorted together, of few buckets each: one launch per build
   // step for all of them
   uint32_t nmax = 0, tmax = 0;
@@ -1265,24 +1269,24 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
     }
     HIP_TRY(launch_build_first_many(cb.bd, (uint32_t)nc, nmax, tmax, st));
   }
-  std::vector<uint32_t> hs(4 * nc);
+  std::vector<uint32_t> hs(kStatWords * nc);
   std::vector<float> hb(any_dev ? 6 * nc : 0);
   std::vector<RangeDev> hr(any_dev ? nc : 0);
   {  // one read-back: the build stats, and the ranges found on the device
     const char *const at = reinterpret_cast<const char *>(cb.small);
     const size_t o_r = reinterpret_cast<const char *>(cb.drng) - at;
     const size_t o_b = reinterpret_cast<const char *>(cb.dbounds) - at;
-    std::vector<char> rb(any_dev ? o_b + hb.size() * 4 : nc * 16);
+    std::vector<char> rb(any_dev ? o_b + hb.size() * 4 : nc * kStatWords * 4);
     const nsfps_status rc = readback(rb.data(), at, rb.size(), st);
     if (rc) return rc;
-    std::memcpy(hs.data(), rb.data(), nc * 16);
+    std::memcpy(hs.data(), rb.data(), nc * kStatWords * 4);
     if (any_dev) {
       std::memcpy(hr.data(), rb.data() + o_r, nc * sizeof(RangeDev));
       std::memcpy(hb.data(), rb.data() + o_b, hb.size() * 4);
     }
   }
   for (size_t i = 0; i < nc; ++i)
-    if (hs[4 * i]) return fail(NSFPS_EINVAL, "points must be finite");
+    if (hs[kStatWords * i]) return fail(NSFPS_EINVAL, "points must be finite");
   // the ranges found on the device: checked as a range given by the caller
   // would be, and kept for the rest of the build and the sampling
   for (size_t i = 0; i < nc && any_dev; ++i) {
@@ -1304,14 +1308,14 @@ nsfps_status build_clouds(std::vector<CloudPlan> &plans, const CallBuffers &cb, 
   }
   const bool mixed = mixed_wanted(plans, hs.data());
   for (size_t i = 0; i < nc; ++i) {
-    nsfps_status rc = decide_layout(plans[i], &hs[4 * i], mixed);
+    nsfps_status rc = decide_layout(plans[i], &hs[kStatWords * i], mixed);
     if (rc) return rc;
   }
   // the sub-cell sort for the tree engine, and where a bucket can fill a
   // level-1 node (the update pass's node boxes then lie inside one cell)
   bool physical = false;
   for (size_t i = 0; i < nc; ++i)
-    physical = physical || plans[i].tree || hs[4 * i + 1] >= kFan * kLeaf;
+    physical = physical || plans[i].tree || hs[kStatWords * i + 1] >= kFan * kLeaf;
   if (together) {
     uint32_t *lorig = nullptr, *prank = nullptr;
     nsfps_status rc = sort_points(cb.bucket, cb.fine, plans[0].n, (uint32_t)nc, cbits, bbits,
@@ -1418,12 +1422,31 @@ constexpr uint32_t kLeafBoundMaxPoints = 262144;
 // points (256 nodes) unchanged; the 1M-point uniform cube (512 nodes) 7.7 ->
 // 12.3 with it.
 constexpr uint32_t kSplitMaxNodes = 256;
+// Clouds whose points fill at least this many buckets are sampled with hot
+// sets of 128 copies.  The run's 1,024 list entries then average at most 4
+// in a cube of 3 x 3 x 3 cells, so the copies of a hot set seldom lower one
+// another and a set of 128 yields about twice the samples of a set of 64
+// (a CPU model of the acceptance rule on the 1M-point uniform cube's lists:
+// 84-118 samples against 53-63).  Where cubes hold many entries (clouds in
+// few cells, coarse grids, or many samples per point), the 128-copy sets
+// cost more than they yield.  Measured on the MI355X, 128 against 64
+// copies per call: 1M-point uniform cube (32,768 buckets filled) 7.35
+// against 7.69 ms, 8M-point clustered cloud (14,321) 62.4 against 70.6;
+// quickstart (8) 0.91 against 0.70, 120,000-point scan (1,266) 4.09 against
+// 3.90, 64 clouds of 16,384 points (about 2,530 each) 2.31 against 2.06.
+constexpr uint32_t kHot128MinCells = 6912;
+
+// The shape of a call's sampling passes: the update pass's workgroups per
+// level-1 node and the run kernel's hot-set size (0 when the tree engine ran).
+struct PassShape {
+  uint32_t split = 0, hot = 0;
+};
 
 // ev_end (or null) is recorded after each batch's launches, before its status
 // read-back; fin gets the clouds' statuses after the last batch.
 nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         const CloudStatus *d_status, hipStream_t st, bool profile,
-                        uint64_t *rounds_out, uint32_t *split_out, hipEvent_t ev_end,
+                        uint64_t *rounds_out, PassShape *shape_out, hipEvent_t ev_end,
                         std::vector<CloudStatus> &fin) {
   uint32_t max_nl1 = 1;
   bool alias = false;  // some cloud's cells share buckets
@@ -1436,7 +1459,17 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   const uint32_t nc = (uint32_t)plans.size();
   const bool mixed = plans[0].dev.mixed != 0;  // the same for every cloud of a call
   const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
-  *split_out = split ? kUpdateSplit : 1u;
+  // the run kernel's hot sets: 128 copies when every cloud's points fill at
+  // least kHot128MinCells buckets (and no cells share buckets); NSFPS_HOT=64
+  // or 128 forces either size
+  bool wide = !alias;
+  for (auto &p : plans) wide = wide && p.occupied >= kHot128MinCells;
+  const char *hot_env = getenv("NSFPS_HOT");
+  if (hot_env && atoi(hot_env) == 64) wide = false;
+  if (hot_env && atoi(hot_env) == 128) wide = !alias;
+  const uint32_t hot = wide ? 128u : 64u;
+  shape_out->split = split ? kUpdateSplit : 1u;
+  shape_out->hot = hot;
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
   const bool replay = std::equal(shape, shape + 5, g_schedule.shape) && !profile;
   std::vector<std::pair<uint32_t, uint32_t>> used;
@@ -1450,7 +1483,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            split, mixed, st));
+                            split, mixed, hot, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1460,7 +1493,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            split, mixed, st));
+                            split, mixed, hot, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }
@@ -1575,7 +1608,7 @@ bool choose_runs(std::vector<CloudPlan> &plans) {
 // fin: the runs engine's final statuses (left empty by the tree engine)
 nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
                            bool runs, uint64_t *rounds, uint64_t *wide_total,
-                           uint32_t *update_split, std::vector<CloudStatus> &fin) {
+                           PassShape *pass, std::vector<CloudStatus> &fin) {
   hipStream_t st = ws.st;
   std::vector<CloudDev> devs;
   uint32_t lds_bytes = 0;
@@ -1586,14 +1619,14 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
   const bool profile = getenv("NSFPS_PROFILE") != nullptr;
   *rounds = 0;
   *wide_total = 0;
-  *update_split = 0;
+  *pass = PassShape{};
   if (runs) {
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[3], st));
     HIP_TRY(hipMemcpyAsync(L.d_clouds, devs.data(), devs.size() * sizeof(CloudDev),
                            hipMemcpyHostToDevice, st));
     if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[4], st));
     if (profile) HIP_TRY(launch_fill_u32(plans[0].dev.prof, 0u, kProfWords * 2, st));
-    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, update_split,
+    return run_rounds(plans, L.d_clouds, L.d_status, st, profile, rounds, pass,
                       ws.ev ? ws.ev[2] : nullptr, fin);
   }
   if (plans.size() == 1) {
@@ -1618,7 +1651,7 @@ nsfps_status sample_clouds(std::vector<CloudPlan> &plans, const CallLayout &L, c
 // fin: the clouds' final statuses when the sampling read them back already
 // (the runs engine's last batch), else empty.
 nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, const Ws &ws,
-                         bool runs, uint64_t rounds, uint64_t wide_total, uint32_t update_split,
+                         bool runs, uint64_t rounds, uint64_t wide_total, const PassShape &pass,
                          std::vector<CloudStatus> &fin, bool out_on_host,
                          int32_t *h_out, uint64_t out_stride, uint64_t *out_lens,
                          std::chrono::steady_clock::time_point t0) {
@@ -1679,7 +1712,8 @@ nsfps_status finish_call(std::vector<CloudPlan> &plans, const CallLayout &L, con
   S.lds_bytes = runs ? 0 : lds_bytes;
   S.rounds = rounds;
   S.engine = runs ? 1u : 0u;
-  S.update_split = update_split;
+  S.update_split = pass.split;
+  S.hot_set = pass.hot;
   return NSFPS_OK;
 }
 
@@ -1731,11 +1765,11 @@ nsfps_status run_clouds_once(std::vector<CloudPlan> &plans, Ws &ws, bool out_on_
   if (rc) return rc;
   if (ws.ev) HIP_TRY(hipEventRecord(ws.ev[1], st));
   uint64_t rounds = 0, wide_total = 0;
-  uint32_t update_split = 0;
+  PassShape pass;
   std::vector<CloudStatus> fin;
-  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &update_split, fin);
+  rc = sample_clouds(plans, L, ws, runs, &rounds, &wide_total, &pass, fin);
   if (rc) return rc;
-  return finish_call(plans, L, ws, runs, rounds, wide_total, update_split, fin, out_on_host, h_out,
+  return finish_call(plans, L, ws, runs, rounds, wide_total, pass, fin, out_on_host, h_out,
                      out_stride, out_lens, t0);
 }
 
@@ -2361,12 +2395,12 @@ nsfps_status nsfps_plan_sample(nsfps_plan *plan, uint64_t m, int32_t *d_out, uin
       HIP_TRY(launch_init_state(c, p.d_small + 2, st));
       HIP_TRY(hipEventRecord(P.ev[1], st));
       uint64_t rounds = 0, wide_total = 0;
-      uint32_t update_split = 0;
+      PassShape pass;
       std::vector<CloudStatus> fin;
       const nsfps_status rc =
-          sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &update_split, fin);
+          sample_clouds(P.plans, P.L, ws, P.runs, &rounds, &wide_total, &pass, fin);
       if (rc) return rc;
-      return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, update_split, fin, false,
+      return finish_call(P.plans, P.L, ws, P.runs, rounds, wide_total, pass, fin, false,
                          nullptr, 0, out_len, t0);
     };
     const nsfps_status rc = body();

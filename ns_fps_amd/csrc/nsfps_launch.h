@@ -70,7 +70,7 @@ hipError_t launch_key2(const uint32_t *lorig, const uint32_t *bucket, const uint
                        uint32_t n, uint32_t n_per, int cloud_shift, int fine_shift, int fine_bits,
                        uint32_t *key2, hipStream_t st);
 hipError_t launch_leaf_counts(const uint32_t *counts, uint32_t T, uint32_t *lc, uint32_t *maxocc,
-                              uint32_t *total, hipStream_t st);
+                              uint32_t *total, uint32_t *occupied, hipStream_t st);
 // prank / lorig may come from sorts holding other clouds too: ranks and rows
 // of this cloud are base + 0 .. base + n - 1 (prank points at this cloud's part)
 hipError_t launch_gather(const uint32_t *prank, const uint32_t *lorig, uint32_t base,
@@ -92,13 +92,16 @@ hipError_t launch_init_state(const CloudDev &c, const uint32_t *d_phys0, hipStre
 // The build of many clouds, each step one launch for all of them (grid y =
 // cloud), when every cloud has at most kManyMaxBuckets buckets.  Parameters
 // per cloud live in device memory.
+// Words of build statistics per cloud (BuildDev::small), read back in one copy.
+constexpr uint32_t kStatWords = 8;
+
 struct BuildDev {
   CloudDev c;                // the cloud's buffers and sizes
   const float *xyz;          // input (device)
   uint32_t *bucket, *fine;   // per input row
   uint32_t *counts, *lc;     // per bucket, scanned to first slot / first leaf
-  uint32_t *small;           // [0] non-finite flag, [1] largest bucket, [2] slot of row 0,
-                             // [3] dense leaves
+  uint32_t *small;           // kStatWords: [0] non-finite flag, [1] largest bucket, [2] slot
+                             // of row 0, [3] dense leaves, [4] buckets holding points
   const uint32_t *prank;     // the sorts: this cloud's part of the physical order (null: the
                              // logical order)
   const uint32_t *lorig;     //   and the logical order of all clouds sorted together
@@ -137,10 +140,11 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 // alias: some cloud's cells share buckets.  leaf_bound: the update pass also
 // bounds each pick by each leaf's box; split: it takes kUpdateSplit
 // workgroups per level-1 node; mixed: the clouds' leaves are runs of 64 slots
-// that may hold several buckets (never with alias).
+// that may hold several buckets (never with alias).  hot: the run kernel's
+// hot-set size, 64 or 128 (with alias always 64).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, bool mixed, hipStream_t st);
+                         bool leaf_bound, bool split, bool mixed, uint32_t hot, hipStream_t st);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

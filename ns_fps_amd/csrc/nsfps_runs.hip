@@ -900,14 +900,26 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 constexpr uint32_t kRunThreads = 512;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
-constexpr uint32_t kHot = 64;
-constexpr uint32_t kCopyLanes = kRunThreads / kHot;  // threads per hot copy (and per sample)
-constexpr uint32_t kCmp = kHot / kCopyLanes;         // copies each of them compares against
+// A hot set holds at most HOT copies (64, or 128 when no cells share
+// buckets).  Each copy has kLanes threads, each comparing it with kCmp other
+// copies; masks over the copies (or their ranks) take kWords 64-bit words.
+template <uint32_t HOT>
+struct HotSet {
+  static constexpr uint32_t kLanes = kRunThreads / HOT;  // threads per hot copy (and per sample)
+  static constexpr uint32_t kCmp = HOT / kLanes;         // copies each of them compares against
+  static constexpr uint32_t kWords = HOT / 64;
+  static constexpr uint32_t kCmpMask = kCmp >= 32 ? 0xffffffffu : (1u << kCmp) - 1u;
+  static_assert((kLanes == 4 || kLanes == 8 || kLanes == 16) && (HOT == 64 || HOT == 128) &&
+                    kCmp <= 32 && kCmp % 8 == 0,
+                "the run kernel layout");
+};
+constexpr uint32_t kHotMax = 128;
 constexpr uint32_t kSelBins = 256;
 constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
 // Copies >= the hot threshold left after a phase that justify another phase.
-// A phase accepts at least the first-ranked copy, so kHot means one phase per
-// hot set, the copies left over going back to the next selection: ranking
+// A phase accepts at least the first-ranked copy, so a value of at least the
+// hot set's size means one phase per hot set, the copies left over going back
+// to the next selection: ranking
 // them again in further phases measured slower (uniform cube 8.36 ms per call
 // at 12, 8.26 at 32, 8.20 at 48, 8.09 at kHot; LiDAR scan 5.38 / 5.26 / 5.19 /
 // 5.14 ms).  Measured again on the later kernels, further phases at 32 gain
@@ -915,7 +927,7 @@ constexpr uint32_t kCells = 4096;    // coarse cells of the list's cell index
 // against 0.732 ms) and lose elsewhere (uniform cube 8.02 against 7.70 ms,
 // clustered cloud 73.5 against 69.8); allowing them only after a phase of at
 // most 24 samples still cost the uniform cube 3 % and the clustered cloud 4 %.
-constexpr uint32_t kPhaseMin = kHot;
+constexpr uint32_t kPhaseMin = kHotMax;
 // Cubes over more coarse rows, or with more list entries in one lane's rows,
 // are applied by every thread to its own entries instead of walked.  Rows
 // below 64 keep the walk's row arithmetic exact.  With a lane's rows walked
@@ -926,8 +938,6 @@ constexpr uint32_t kWalkRows = 16;
 constexpr uint32_t kWalkLaneEntries = 16;
 static_assert(kWalkRows <= 64, "the walk's row arithmetic");
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
-static_assert((kCopyLanes == 4 || kCopyLanes == 8 || kCopyLanes == 16) && kHot == 64,
-              "the run kernel layout");
 static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 
 // Phase clocks of the run kernel (s_memtime cycles of wave 0, summed over
@@ -997,25 +1007,28 @@ struct SmallHalves {
 };
 
 // LDS slot of hot copy i.  Lane q of a copy's group compares against copies
-// q * kCmp + u; the kCopyLanes copies read together for one u sit side by
-// side, so one read by a wave touches distinct banks.
+// q * kCmp + u; the kLanes copies read together for one u sit side by side,
+// so one read by a wave touches distinct banks.
+template <uint32_t HOT>
 __device__ __forceinline__ uint32_t hot_slot(uint32_t i) {
-  return (i % kCmp) * kCopyLanes + i / kCmp;
+  return (i % HotSet<HOT>::kCmp) * HotSet<HOT>::kLanes + i / HotSet<HOT>::kCmp;
 }
 
-// Sum / minimum over the kCopyLanes lanes of a group (aligned lanes).
+// Sum / minimum over the L lanes of a group (aligned lanes).
+template <uint32_t L>
 __device__ __forceinline__ uint32_t group_sum(uint32_t v) {
   v += dpp_mov<kDppQuad1032>(v);
   v += dpp_mov<kDppQuad2301>(v);
-  if (kCopyLanes >= 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
-  if (kCopyLanes >= 16) v += dpp_mov<kDppMirror>(v);     // lane i and 15 - i: the other half
+  if (L >= 8) v += dpp_mov<kDppHalfMirror>(v);  // lane i and 7 - i: the other quad
+  if (L >= 16) v += dpp_mov<kDppMirror>(v);     // lane i and 15 - i: the other half
   return v;
 }
+template <uint32_t L>
 __device__ __forceinline__ uint32_t group_min(uint32_t v) {
   v = min(v, dpp_mov<kDppQuad1032>(v));
   v = min(v, dpp_mov<kDppQuad2301>(v));
-  if (kCopyLanes >= 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
-  if (kCopyLanes >= 16) v = min(v, dpp_mov<kDppMirror>(v));
+  if (L >= 8) v = min(v, dpp_mov<kDppHalfMirror>(v));
+  if (L >= 16) v = min(v, dpp_mov<kDppMirror>(v));
   return v;
 }
 
@@ -1048,17 +1061,21 @@ __device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, ui
 // bucket has further cells are few and listed apart, and after each walk
 // every one of them is tested against every sample of the hot set; the
 // phases test every cell of a hot copy's bucket.
-template <bool PROF, bool ALIAS>
+template <bool PROF, bool ALIAS, uint32_t HOT>
 __device__ __forceinline__ void run_list(const CloudDev &c) {
+  // the alias pass holds one sample per lane
+  static_assert(!ALIAS || HOT == 64, "shared buckets take hot sets of 64");
+  constexpr uint32_t kHot = HOT, kCopyLanes = HotSet<HOT>::kLanes, kCmp = HotSet<HOT>::kCmp,
+                     kWords = HotSet<HOT>::kWords;
   __shared__ uint4 s_pc[kListCap];      // sorted list: {x, y, z, pack11(cell)}
   __shared__ uint32_t s_dd[kListCap];   // its distances (bits)
   __shared__ uint2 s_rk[kListCap];      // its {~logical rank, input row}
-  __shared__ uint4 s_hq[2][kHot];       // hot copies at hot_slot(i), one buffer per phase parity:
+  __shared__ uint4 s_hq[2][kHot];       // hot copies at hot_slot<HOT>(i), one buffer per phase parity:
                                         //   {pack11(cube lo), pack11(cube hi) | guards, ~rank,
                                         //   distance bits}; key 0 once taken
   __shared__ __align__(16) uint32_t s_rank[kHot];  // rank of each hot copy in the phase
-  __shared__ unsigned long long s_lowm[2];  // bit r: the copy ranked r is lowered
-  __shared__ unsigned long long s_lowc[2];  // bit j: hot copy j is lowered
+  __shared__ unsigned long long s_lowm[2][kWords];  // bit r: the copy ranked r is lowered
+  __shared__ unsigned long long s_lowc[2][kWords];  // bit j: hot copy j is lowered
   __shared__ uint32_t s_stop[2];            // the first rank a lowered copy holds back
   __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
                                         //   half-widths}
@@ -1066,7 +1083,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
   __shared__ uint4 s_rp[kHot];          // accepted hot copies at their slot: {x, y, z, row}
   __shared__ uint2 s_rc[kHot];          //   cube corners, pack11 (hi with guards)
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
-  __shared__ uint32_t s_big[2];                         // samples with large cubes
+  __shared__ uint32_t s_big[2 * kWords];                // samples with large cubes
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
   __shared__ uint32_t s_nhot;
   __shared__ unsigned long long s_kmr;   // largest key of a hot copy left unaccepted
@@ -1396,16 +1413,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           }
         }
       }
-      if (tid < 2) s_big[tid] = 0;
+      if (tid < 2 * kWords) s_big[tid] = 0;
       if (tid == 0) {
-        s_lowm[0] = 0;
-        s_lowc[0] = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) {
+          s_lowm[0][w] = 0;
+          s_lowc[0][w] = 0;
+        }
         s_stop[0] = kHot;
         s_kmr = 0;
       }
       __syncthreads();
-      if (wave == 0 && lane < min(s_nhot, kHot)) {
-        const uint4 hx = s_hx[lane];
+      if (tid < min(s_nhot, kHot)) {  // the first kHot / 64 waves, a copy a lane
+        const uint4 hx = s_hx[tid];
         const float D = __uint_as_float(hx.z);
         const SmallHalves sh(c.r);
         uint32_t h;
@@ -1413,8 +1433,8 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         else h = packed_halves(c.r, D);
         uint32_t lo_c, hi_c;
         cube_corners(hx.x, h, b0, b1, b2, lo_c, hi_c);
-        s_hq[0][hot_slot(lane)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hx.y, hx.z);
-        s_hx[lane] = make_uint4(hx.x, pack11(hx.x) | kGuards, pack11(hx.x), h);
+        s_hq[0][hot_slot<HOT>(tid)] = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, hx.y, hx.z);
+        s_hx[tid] = make_uint4(hx.x, pack11(hx.x) | kGuards, pack11(hx.x), h);
       }
       __syncthreads();
     }
@@ -1454,23 +1474,27 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
       return r;
     };
     while (true) {
-      const uint4 me = s_hq[ph][hot_slot(hj)];
+      const uint4 me = s_hq[ph][hot_slot<HOT>(hj)];
       const uint4 mx = s_hx[hj];
-      // the kCmp copies of this lane, all loads issued before any use
-      uint4 og[kCmp];
-#pragma unroll
-      for (uint32_t u = 0; u < kCmp; ++u) og[u] = s_hq[ph][kCopyLanes * u + hq];  // copy kCmp hq + u
-      __builtin_amdgcn_sched_barrier(0);
       const uint64_t mkey = ((uint64_t)me.w << 32) | me.z;
       my_key = mkey;
       const bool remj = mkey != 0;  // copies taken earlier, and unused slots, have key 0
-      // bit u of cand: copy kCmp q + u is remaining, ranked above j, and its cube holds j
+      // bit u of cand: copy kCmp q + u is remaining, ranked above j, and its
+      // cube holds j.  The kCmp copies of this lane are read 8 at a time, all
+      // loads of a chunk issued before any use.
       uint32_t cnt = 0, cand = 0;
 #pragma unroll
-      for (uint32_t u = 0; u < kCmp; ++u) {
-        const uint32_t gt = (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > mkey);
-        cnt += gt;
-        cand |= (gt & j_in(mx.y, mx.z, og[u].x, og[u].y)) << u;
+      for (uint32_t c0 = 0; c0 < kCmp; c0 += 8) {
+        uint4 og[8];
+#pragma unroll
+        for (uint32_t v = 0; v < 8; ++v) og[v] = s_hq[ph][kCopyLanes * (c0 + v) + hq];  // copy kCmp hq + c0 + v
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t v = 0; v < 8; ++v) {
+          const uint32_t gt = (uint32_t)((((uint64_t)og[v].w << 32) | og[v].z) > mkey);
+          cnt += gt;
+          cand |= (gt & j_in(mx.y, mx.z, og[v].x, og[v].y)) << (c0 + v);
+        }
       }
       uint32_t low = 0;
       if (cand) {  // rare: the exact distance decides
@@ -1484,15 +1508,15 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           low |= dd < __uint_as_float(me.w) ? 1u : 0u;
         }
       }
-      const uint32_t rank = group_sum(cnt);
-      const bool lowered = group_sum(low) != 0;
+      const uint32_t rank = group_sum<kCopyLanes>(cnt);
+      const bool lowered = group_sum<kCopyLanes>(low) != 0;
       const bool rep = remj && hq == 0;
       const bool ge = mkey >= hth;
       if (rep) s_rank[hj] = rank;
       if (hq == 0 && !remj) s_rank[hj] = kHot;  // never accepted
       if (rep && lowered) {
-        atomicOr(&s_lowm[ph], 1ull << rank);
-        atomicOr(&s_lowc[ph], 1ull << hj);
+        atomicOr(&s_lowm[ph][rank >> 6], 1ull << (rank & 63u));
+        atomicOr(&s_lowc[ph][hj >> 6], 1ull << (hj & 63u));
       }
       const uint32_t wge = (uint32_t)__popcll(__ballot(rep && ge));
       const uint32_t wnz = (uint32_t)__popcll(__ballot(rep && ge && me.w != 0u));
@@ -1501,14 +1525,22 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         s_wr[ph][wave][1] = wnz;
       }
       if (tid == 0) {
-        s_lowm[ph ^ 1] = 0;
-        s_lowc[ph ^ 1] = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) {
+          s_lowm[ph ^ 1][w] = 0;
+          s_lowc[ph ^ 1][w] = 0;
+        }
         s_stop[ph ^ 1] = kHot;
       }
       __syncthreads();
       NSFPS_RMARK(kRpRank);
       // copies >= the hot threshold with distance > 0 are ranks 0 .. nnz - 1
-      const unsigned long long lowm = s_lowm[ph];
+      unsigned long long lowm[kWords], lowany = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kWords; ++w) {
+        lowm[w] = s_lowm[ph][w];
+        lowany |= lowm[w];
+      }
       uint32_t nge = 0, nnz = 0;
 #pragma unroll
       for (uint32_t w = 0; w < kRunWaves; ++w) {
@@ -1519,11 +1551,12 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
       // every copy above it that is not lowered is a sample (more samples
       // only lower it further): ranks at or below K_j wait for the next phase.
       uint32_t sstop = kHot;
-      if (lowm) {
+      if (lowany) {
         if (remj && lowered) {  // the whole group of a lowered copy
-          const uint32_t lowc = (uint32_t)(s_lowc[ph] >> (hq * kCmp));
+          const uint32_t lb = hq * kCmp;  // this lane's copies' bits
+          const uint32_t lowc = (uint32_t)(s_lowc[ph][lb >> 6] >> (lb & 63u));
           uint32_t nk = me.w;
-          uint32_t nm = cand & ~lowc & ((1u << kCmp) - 1u);
+          uint32_t nm = cand & ~lowc & HotSet<HOT>::kCmpMask;
           if (nm) {
             const uint4 pj = s_hp[hj];
             for (; nm; nm &= nm - 1) {
@@ -1535,12 +1568,14 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
               nk = min(nk, __float_as_uint(dd));  // non-negative floats order like their bits
             }
           }
-          const uint64_t K = ((uint64_t)group_min(nk) << 32) | me.z;
+          const uint64_t K = ((uint64_t)group_min<kCopyLanes>(nk) << 32) | me.z;
           uint32_t above = 0;
 #pragma unroll
-          for (uint32_t u = 0; u < kCmp; ++u)
-            above += (uint32_t)((((uint64_t)og[u].w << 32) | og[u].z) > K);
-          const uint32_t tj = group_sum(above);  // the first rank at or below K_j
+          for (uint32_t u = 0; u < kCmp; ++u) {
+            const uint4 o = s_hq[ph][kCopyLanes * u + hq];
+            above += (uint32_t)((((uint64_t)o.w << 32) | o.z) > K);
+          }
+          const uint32_t tj = group_sum<kCopyLanes>(above);  // the first rank at or below K_j
           if (hq == 0) atomicMin(&s_stop[ph], tj);
         }
         __syncthreads();
@@ -1549,21 +1584,49 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
       // the samples: copies not lowered, ranked below min(stop, nnz), the
       // first room - npk of them, in rank order
       const uint32_t seff = min(sstop, nnz);
-      uint64_t accr = (seff >= 64 ? ~0ull : ((1ull << seff) - 1ull)) & ~lowm;  // by rank
-      uint32_t P = (uint32_t)__popcll(accr);
-      while (P > room - npk) {  // the last samples of the call
-        accr &= ~(1ull << (63 - __clzll(accr)));
+      uint64_t accr[kWords];  // by rank
+      uint32_t P = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kWords; ++w) {
+        const uint32_t r0 = 64 * w;
+        const uint64_t f = seff >= r0 + 64 ? ~0ull : seff > r0 ? (1ull << (seff - r0)) - 1ull : 0ull;
+        accr[w] = f & ~lowm[w];
+        P += (uint32_t)__popcll(accr[w]);
+      }
+      while (P > room - npk) {  // the last samples of the call: the highest ranks go
+#pragma unroll
+        for (int w = (int)kWords - 1; w >= 0; --w) {
+          if (accr[w]) {
+            accr[w] &= ~(1ull << (63 - __clzll(accr[w])));
+            break;
+          }
+        }
         --P;
       }
+      // ranks below r among the accepted, and whether r is accepted
+      const auto acc_below = [&](uint32_t r) -> uint32_t {
+        uint32_t b = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) {
+          const uint32_t r0 = 64 * w;
+          b += r >= r0 + 64 ? (uint32_t)__popcll(accr[w])
+               : r > r0     ? (uint32_t)__popcll(accr[w] & ((1ull << (r - r0)) - 1ull))
+                            : 0u;
+        }
+        return b;
+      };
+      const auto acc_has = [&](uint32_t r) -> bool {
+        return (accr[(r >> 6) & (kWords - 1u)] >> (r & 63u)) & 1u;
+      };
       if (P == 0) {  // rank 0: below the hot threshold, or distance 0
         stop = (nge == 0) ? 1u : 2u;
         break;
       }
-      const bool acc = remj && rank < kHot && ((accr >> rank) & 1u);
+      const bool acc = remj && rank < kHot && acc_has(rank);
       if (acc) {
         my_acc = true;
         my_key = 0;
-        my_out = npk + (uint32_t)__popcll(accr & ((1ull << rank) - 1ull));
+        my_out = npk + acc_below(rank);
         my_qc = mx.x;
         my_hh = mx.w;
       }
@@ -1597,10 +1660,10 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         }
         uint32_t cand2 = 0;
 #pragma unroll
-        for (uint32_t u = 0; u < kCmp; ++u)
-          cand2 |= ((rk[u] < kHot ? (uint32_t)(accr >> rk[u]) & 1u : 0u) &
-                    j_in(mx.y, mx.z, og[u].x, og[u].y))
-                   << u;
+        for (uint32_t u = 0; u < kCmp; ++u) {
+          const uint4 o = s_hq[ph][kCopyLanes * u + hq];
+          cand2 |= ((rk[u] < kHot ? (uint32_t)acc_has(rk[u]) : 0u) & j_in(mx.y, mx.z, o.x, o.y)) << u;
+        }
         if (cand2) {  // rare: the exact distances
           const uint4 pj = s_hp[hj];
           while (cand2) {
@@ -1614,7 +1677,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           }
         }
       }
-      mnb = group_min(mnb);
+      mnb = group_min<kCopyLanes>(mnb);
       // the next buffer: accepted copies get key 0, lowered ones new cubes
       if (hq == 0) {
         uint4 nv = me;
@@ -1628,7 +1691,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           nv = make_uint4(pack11(lo_c), pack11(hi_c) | kGuards, me.z, mnb);
           s_hx[hj].w = h;
         }
-        s_hq[ph ^ 1][hot_slot(hj)] = nv;
+        s_hq[ph ^ 1][hot_slot<HOT>(hj)] = nv;
       }
       __syncthreads();
       ph ^= 1;
@@ -1816,8 +1879,13 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
       for (uint32_t s = 0; s < kOwnSlots; ++s)
         if (s * kRunThreads + tid < nlist) d[s] = __uint_as_float(s_dd[s * kRunThreads + tid]);
       NSFPS_RMARK(kRpApply);
-      uint64_t bigm = ((uint64_t)uniform(s_big[1]) << 32) | uniform(s_big[0]);
-      if (bigm) {
+      uint64_t bigm[kWords], bany = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kWords; ++w) {
+        bigm[w] = ((uint64_t)uniform(s_big[2 * w + 1]) << 32) | uniform(s_big[2 * w]);
+        bany |= bigm[w];
+      }
+      if (bany) {
         // branch-free (the distance is always computed, the box test masks
         // it), two samples a trip so that their LDS reads overlap; a lone
         // last sample is applied twice (min is idempotent)
@@ -1839,15 +1907,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             d[s] = __uint_as_float(min(__float_as_uint(d[s]), __float_as_uint(dd) | (in - 1u)));
           }
         };
-        while (bigm) {
-          const uint32_t ka = (uint32_t)__builtin_ctzll(bigm);
-          bigm &= bigm - 1;
-          const uint32_t kc = bigm ? (uint32_t)__builtin_ctzll(bigm) : ka;
-          bigm &= bigm - 1;
-          const uint4 a0 = s_rp[ka], a1 = s_rp[kc];
-          const uint2 b0 = s_rc[ka], b1 = s_rc[kc];
-          take(a0, b0);
-          take(a1, b1);
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) {
+          uint64_t bm = bigm[w];
+          while (bm) {
+            const uint32_t ka = 64 * w + (uint32_t)__builtin_ctzll(bm);
+            bm &= bm - 1;
+            const uint32_t kc = bm ? 64 * w + (uint32_t)__builtin_ctzll(bm) : ka;
+            bm &= bm - 1;
+            const uint4 a0 = s_rp[ka], a1 = s_rp[kc];
+            const uint2 b0 = s_rc[ka], b1 = s_rc[kc];
+            take(a0, b0);
+            take(a1, b1);
+          }
         }
 #pragma unroll
         for (uint32_t s = 0; s < kOwnSlots; ++s)
@@ -1902,9 +1974,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
 #undef NSFPS_RMARK
 }
 
-template <bool PROF, bool ALIAS>
+template <bool PROF, bool ALIAS, uint32_t HOT>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  run_list<PROF, ALIAS>(clouds[blockIdx.x]);
+  run_list<PROF, ALIAS, HOT>(clouds[blockIdx.x]);
 }
 
 
@@ -1952,8 +2024,8 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
 hipError_t preload_runs_kernels() {
   constexpr uint32_t S = kUpdateSplit;
   return func_attributes(
-      k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>, k_run<false, false>,
-      k_run<false, true>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
+      k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>, k_run<false, false, 64>,
+      k_run<false, false, 128>, k_run<false, true, 64>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
       k_update<false, false, true, 1, false>, k_update<false, false, true, S, false>,
       k_update<false, true, false, 1, false>, k_update<false, true, false, S, false>,
       k_update<false, true, true, 1, false>, k_update<false, true, true, S, false>,
@@ -1967,25 +2039,30 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
   return hipGetLastError();
 }
 
-// The classic round's update, gather and run kernels of one variant.
+// The classic round's update, gather and run kernels of one variant; hot:
+// the run kernel's hot-set size where cells do not share buckets (64 or 128).
 template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT, bool MIXED>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
-                    uint32_t passes, hipStream_t st) {
+                    uint32_t passes, uint32_t hot, hipStream_t st) {
   k_update<PROF, ALIAS, LB, SPLIT, MIXED>
       <<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
-  k_run<PROF, ALIAS><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+  if (!ALIAS && hot == 128)
+    k_run<PROF, false, 128><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+  else
+    k_run<PROF, ALIAS, 64><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
 }
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, bool mixed, hipStream_t st) {
+                         bool leaf_bound, bool split, bool mixed, uint32_t hot, hipStream_t st) {
   if (alias && mixed) return hipErrorInvalidValue;  // leaves of several buckets: one cell each
+  if (hot != 64 && hot != 128) return hipErrorInvalidValue;
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
-  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, hipStream_t);
+  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, uint32_t, hipStream_t);
   constexpr uint32_t S = kUpdateSplit;
   // [profile][cells: one per leaf, shared buckets, several per leaf][leaf_bound][split]
   static constexpr Launch kClassic[2][3][2][2] = {
@@ -2002,7 +2079,7 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
        {{launch_classic<true, false, false, 1, true>, launch_classic<true, false, false, S, true>},
         {launch_classic<true, false, true, 1, true>, launch_classic<true, false, true, S, true>}}}};
   const Launch classic = kClassic[profile][alias ? 1 : mixed ? 2 : 0][leaf_bound][split];
-  for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, st);
+  for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, hot, st);
   return hipGetLastError();
 }
 

@@ -286,6 +286,7 @@ py::dict last_stats_py() {
   d["engine"] = s.engine ? "runs" : "tree";
   d["update_split"] = s.update_split;
   d["mixed"] = s.mixed;
+  d["hot_set"] = s.hot_set;
   return d;
 }
 

@@ -84,6 +84,33 @@ def test_workload_hash_in_both_leaf_layouts(yf, lib, wname, mixed, monkeypatch):
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("hot", ["64", "128"])
+@pytest.mark.parametrize("wname", ["quickstart", "uniform_cube", "uniform_cube_30", "lidar_scan",
+                                   "batched_shapes", "clustered"])
+def test_workload_hash_with_either_hot_set(yf, lib, wname, hot, monkeypatch):
+    """The run kernel takes hot sets of 64 or 128 copies (128 where the points
+    fill many buckets; NSFPS_HOT forces either, and grids whose cells share
+    buckets always take 64).  Both give the reference's samples."""
+    monkeypatch.setenv("NSFPS_HOT", hot)
+    w, g, outs = run_workload(yf, lib, wname)
+    want = 64 if wname == "uniform_cube_30" else int(hot)
+    assert yf.last_stats()["hot_set"] == want
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
+@pytest.mark.parametrize("wname,hot", [("quickstart", 64), ("lidar_scan", 64), ("batched_shapes", 64),
+                                       ("uniform_cube", 128), ("clustered", 128),
+                                       ("uniform_cube_30", 64)])
+def test_hot_set_size_follows_the_filled_buckets(yf, lib, wname, hot):
+    """128-copy hot sets where the points fill at least 6,912 buckets (the
+    uniform cube 32,768, the clustered cloud 14,321), 64 otherwise (the
+    quickstart 8, the LiDAR scan 1,266, each batched cloud about 2,530) and
+    wherever cells share buckets."""
+    run_workload(yf, lib, wname)
+    assert yf.last_stats()["hot_set"] == hot
+
+
 @pytest.mark.parametrize("wname", ["quickstart", "batched_shapes"])
 def test_workload_hash_with_either_logical_sort(yf, lib, wname, monkeypatch):
     """Clouds of at most 16,384 points are sorted by bucket in one workgroup
@@ -199,7 +226,8 @@ TREE = {"NSFPS_ENGINE": "tree"}
 
 @pytest.mark.parametrize("env", [
     {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
-    {"NSFPS_GLOBAL_SORT": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
+    {"NSFPS_GLOBAL_SORT": "1"}, {"NSFPS_HOT": "64"}, {"NSFPS_HOT": "128"},
+    {"NSFPS_HOT": "128", "NSFPS_PROFILE": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
     {**TREE, "NSFPS_LATE_THREADS": "1024"},

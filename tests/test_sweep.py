@@ -178,3 +178,26 @@ def test_gpu_matches_oracle_on_second_sweep(yf, oracle, seed):
     assert got.dtype == np.int32
     assert np.array_equal(got, want), (len(got), len(want), f"first difference at "
                                        f"{np.argmax(got[:len(want)] != want[:len(got)])}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sweep,seed", [(1, s) for s in SEEDS] + [(2, s) for s in SEEDS2],
+                         ids=lambda v: str(v))
+def test_gpu_matches_oracle_with_hot_sets_of_128(yf, oracle, sweep, seed, monkeypatch):
+    """Both sweeps with the run kernel's 128-copy hot sets forced (the size
+    otherwise taken only where the points fill many buckets; grids whose
+    cells share buckets keep 64)."""
+    from ns_fps_amd.capi import Lib
+    monkeypatch.setenv("NSFPS_HOT", "128")
+    if sweep == 1:
+        shape, p, m, rng = make_case(seed)
+        blocks = rng[6:9]
+    else:
+        shape, p, m, rng, blocks = make_case2(seed)
+    if rng is None:
+        got = Lib().fps_bbox(p, m, blocks)
+    else:
+        got = yf.fps(p, m, yf.make_range(*rng))
+    want = oracle.fps(p, m, rng, blocks=blocks)
+    assert np.array_equal(got, want), (len(got), len(want), f"first difference at "
+                                       f"{np.argmax(got[:len(want)] != want[:len(got)])}")
