@@ -1076,7 +1076,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
   __shared__ __align__(16) uint32_t s_rank[kHot];  // rank of each hot copy in the phase
   __shared__ unsigned long long s_lowm[2][kWords];  // bit r: the copy ranked r is lowered
   __shared__ unsigned long long s_lowc[2][kWords];  // bit j: hot copy j is lowered
-  __shared__ uint32_t s_stop[2];            // the first rank a lowered copy holds back
+  __shared__ unsigned long long s_kmax[2];  // the largest bound K_j of a lowered copy
   __shared__ uint4 s_hx[kHot];          // hot copies: {cell, pack11(cell) | guards, pack11(cell),
                                         //   half-widths}
   __shared__ uint4 s_hp[kHot];          // hot copies: {x, y, z, row}
@@ -1420,7 +1420,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           s_lowm[0][w] = 0;
           s_lowc[0][w] = 0;
         }
-        s_stop[0] = kHot;
+        s_kmax[0] = 0;
         s_kmr = 0;
       }
       __syncthreads();
@@ -1530,7 +1530,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
           s_lowm[ph ^ 1][w] = 0;
           s_lowc[ph ^ 1][w] = 0;
         }
-        s_stop[ph ^ 1] = kHot;
+        s_kmax[ph ^ 1] = 0;
       }
       __syncthreads();
       NSFPS_RMARK(kRpRank);
@@ -1569,17 +1569,19 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             }
           }
           const uint64_t K = ((uint64_t)group_min<kCopyLanes>(nk) << 32) | me.z;
-          uint32_t above = 0;
-#pragma unroll
-          for (uint32_t u = 0; u < kCmp; ++u) {
-            const uint4 o = s_hq[ph][kCopyLanes * u + hq];
-            above += (uint32_t)((((uint64_t)o.w << 32) | o.z) > K);
-          }
-          const uint32_t tj = group_sum<kCopyLanes>(above);  // the first rank at or below K_j
-          if (hq == 0) atomicMin(&s_stop[ph], tj);
+          if (hq == 0) atomicMax(&s_kmax[ph], (unsigned long long)K);
         }
         __syncthreads();
-        sstop = s_stop[ph];
+        // the first rank at or below some K_j: the least number of copies
+        // above a K_j is the number above the largest, which every wave
+        // counts over the copies itself
+        const unsigned long long kmax = s_kmax[ph];
+        sstop = 0;
+#pragma unroll
+        for (uint32_t t = 0; t < kHot / 64; ++t) {
+          const uint4 o = s_hq[ph][64 * t + lane];
+          sstop += (uint32_t)__popcll(__ballot((((uint64_t)o.w << 32) | o.z) > kmax));
+        }
       }
       // the samples: copies not lowered, ranked below min(stop, nnz), the
       // first room - npk of them, in rank order
