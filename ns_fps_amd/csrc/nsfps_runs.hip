@@ -937,6 +937,16 @@ constexpr uint32_t kPhaseMin = kHotMax;
 constexpr uint32_t kWalkRows = 16;
 constexpr uint32_t kWalkLaneEntries = 16;
 static_assert(kWalkRows <= 64, "the walk's row arithmetic");
+// With hot sets of 128 copies a sample has 4 lanes: 16 rows (4 a lane) and
+// 24 entries a lane.  Measured per call (rows / entries): uniform cube 7.21 ms
+// at 16 / 16, 16 / 24 and 16 / 32, 7.26 at 12 / 24, 7.38 at 24 / 16, 8.47 at
+// 8 / 16; clustered cloud 62.1, 61.6, 61.6, 60.5, 63.8 and 60.5 ms.
+template <uint32_t HOT>
+struct WalkLimits {
+  static constexpr uint32_t kRows = kWalkRows;
+  static constexpr uint32_t kLaneEntries = HOT == 128 ? 24 : kWalkLaneEntries;
+  static_assert(kRows <= 64, "the walk's row arithmetic");
+};
 constexpr uint32_t kCellsPerThread = kCells / kRunThreads;
 static_assert(kCellsPerThread % 4 == 0, "the cell scan reads whole uint4s");
 
@@ -1737,7 +1747,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
         const uint32_t z0 = (lo_c >> 20) >> gsz, z1 = (hi_c >> 20) >> gsz;
         const uint32_t ny = y1 - y0 + 1, nrows = ny * (z1 - z0 + 1);
-        bool big = nrows > kWalkRows;
+        bool big = nrows > WalkLimits<HOT>::kRows;
         if (!big) {
           // row rr = rz * ny + ry; rz = floor((rr + 0.5) / ny) holds with an
           // approximate reciprocal: rr < 64 leaves a margin of 0.5 / ny
@@ -1769,7 +1779,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             // as one list.  Per call, against row by row (whose last step in
             // each row mostly repeats): uniform cube 2.6 % and LiDAR scan
             // 5.5 % faster, clustered cloud (full rows) 2.5 % slower.
-            constexpr uint32_t kLaneRows = (kWalkRows + kCopyLanes - 1) / kCopyLanes;
+            constexpr uint32_t kLaneRows = (WalkLimits<HOT>::kRows + kCopyLanes - 1) / kCopyLanes;
             uint32_t rs[kLaneRows], rn[kLaneRows], ne = 0;
 #pragma unroll
             for (uint32_t t = 0; t < kLaneRows; ++t) {
@@ -1784,7 +1794,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             }
             // more entries than the lane's budget: the sample is flagged (the
             // same samples as a row-by-row test: running totals only grow)
-            if (ne > kWalkLaneEntries) {
+            if (ne > WalkLimits<HOT>::kLaneEntries) {
               big = true;
             } else {
               for (uint32_t f = 0; f < ne; f += 4) {
