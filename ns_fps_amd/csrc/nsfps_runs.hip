@@ -882,8 +882,8 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // row the cube spans, the entries of its x range.
 //
 // The threshold argument is applied once more inside the list: a hot
-// threshold H leaves at most kHot entries at or above it, and those are
-// resolved in parallel phases.  Rank the remaining hot copies by key; copy j
+// threshold H leaves at most HOT entries at or above it (64, or 128 where the
+// points fill many buckets), and those are resolved in parallel phases.  Rank the remaining hot copies by key; copy j
 // is "lowered" when the cube of a higher-ranked copy contains it and brings
 // its distance down.  Every copy ranked above the first lowered one is a
 // sample, in rank order: all copies ranked above it are samples too, a copy
@@ -894,9 +894,9 @@ __global__ __launch_bounds__(kPassThreads) void k_gather(const CloudDev *__restr
 // comes).  So a phase takes those samples at once, applies their cubes to
 // the remaining copies, and ranks again, until no copy is >= max(H, B).  Then the
 // hot run's samples are applied to every list entry (a
-// sample with a small cube is applied by one quad walking its rows of the
-// cell index, one with a large cube by every thread to its own entries) and
-// the next hot set is chosen.  The run ends when no entry is >= B.
+// sample with a small cube is applied by its copy's lanes walking its rows of
+// the cell index, one with a large cube by every thread to its own entries)
+// and the next hot set is chosen.  The run ends when no entry is >= B.
 constexpr uint32_t kRunThreads = 512;
 constexpr uint32_t kRunWaves = kRunThreads / 64;
 constexpr uint32_t kOwnSlots = kListCap / kRunThreads;
