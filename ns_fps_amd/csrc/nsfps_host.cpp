@@ -1411,8 +1411,14 @@ RoundSchedule g_schedule;
 // work pays where cubes are large against the leaves: sparse clouds).
 // Measured on the MI355X: 10,000-point quickstart 1.04 -> 0.99 ms per call,
 // 120,000-point scan 4.55 -> 4.40; with it, the 1M-point uniform cube was
-// 1.8 % slower and the 8M-point clustered cloud 0.8 %.
+// 1.8 % slower (0.6 % on the later kernels).
 constexpr uint32_t kLeafBoundMaxPoints = 262144;
+// Larger clouds whose filled buckets hold more than this many points on
+// average take it too: dense buckets fill several leaves each, and the bound
+// spares the leaves of a cube's cells that no pick can lower.  8M-point
+// clustered cloud (586 points a filled bucket) 61.25 against 61.79 ms per
+// call; the 1M-point uniform cube (32) was 7.28 against 7.24 with it.
+constexpr uint32_t kLeafBoundDensity = 64;
 // Rounds with at most this many level-1 nodes over all clouds split each
 // node's leaves over kUpdateSplit workgroups of the update pass (its work
 // then spreads over that many more CUs; a node's key is the largest of the
@@ -1454,8 +1460,10 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   for (auto &p : plans) {
     max_nl1 = std::max(max_nl1, p.dev.nl1);
     alias = alias || !p.rng.dev.bijective;
-    leaf_bound = leaf_bound && p.n <= kLeafBoundMaxPoints;
+    leaf_bound = leaf_bound && (p.n <= kLeafBoundMaxPoints ||
+                                (uint64_t)p.n > kLeafBoundDensity * std::max(1u, p.occupied));
   }
+  if (const char *e = getenv("NSFPS_LEAF_BOUND")) leaf_bound = atoi(e) != 0;  // forced either way
   const uint32_t nc = (uint32_t)plans.size();
   const bool mixed = plans[0].dev.mixed != 0;  // the same for every cloud of a call
   const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;

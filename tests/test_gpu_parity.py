@@ -99,6 +99,18 @@ def test_workload_hash_with_either_hot_set(yf, lib, wname, hot, monkeypatch):
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("lb", ["0", "1"])
+@pytest.mark.parametrize("wname", ["uniform_cube", "clustered", "lidar_scan"])
+def test_workload_hash_with_either_update_bound(yf, lib, wname, lb, monkeypatch):
+    """The update pass bounds each pick by each leaf's box for small clouds
+    and for dense ones (the clustered cloud), not for the uniform cube;
+    NSFPS_LEAF_BOUND forces either way.  Both give the reference's samples."""
+    monkeypatch.setenv("NSFPS_LEAF_BOUND", lb)
+    w, g, outs = run_workload(yf, lib, wname)
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
 @pytest.mark.parametrize("wname,hot", [("quickstart", 64), ("lidar_scan", 64), ("batched_shapes", 64),
                                        ("uniform_cube", 128), ("clustered", 128),
                                        ("uniform_cube_30", 64)])
@@ -227,6 +239,7 @@ TREE = {"NSFPS_ENGINE": "tree"}
 @pytest.mark.parametrize("env", [
     {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
     {"NSFPS_GLOBAL_SORT": "1"}, {"NSFPS_HOT": "64"}, {"NSFPS_HOT": "128"},
+    {"NSFPS_LEAF_BOUND": "0"}, {"NSFPS_LEAF_BOUND": "1"},
     {"NSFPS_HOT": "128", "NSFPS_PROFILE": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
