@@ -1456,14 +1456,17 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
                         std::vector<CloudStatus> &fin) {
   uint32_t max_nl1 = 1;
   bool alias = false;  // some cloud's cells share buckets
-  bool leaf_bound = true;  // every cloud small enough for the leaf-box bound
+  bool leaf_bound = true;  // every cloud small enough (or dense enough) for the leaf-box bound
+  bool dense = true;       // every cloud's filled buckets hold more than kLeafBoundDensity points
   for (auto &p : plans) {
     max_nl1 = std::max(max_nl1, p.dev.nl1);
     alias = alias || !p.rng.dev.bijective;
-    leaf_bound = leaf_bound && (p.n <= kLeafBoundMaxPoints ||
-                                (uint64_t)p.n > kLeafBoundDensity * std::max(1u, p.occupied));
+    const bool d = (uint64_t)p.n > kLeafBoundDensity * std::max(1u, p.occupied);
+    leaf_bound = leaf_bound && (p.n <= kLeafBoundMaxPoints || d);
+    dense = dense && d;
   }
   if (const char *e = getenv("NSFPS_LEAF_BOUND")) leaf_bound = atoi(e) != 0;  // forced either way
+  if (const char *e = getenv("NSFPS_DENSE_WALK")) dense = atoi(e) != 0;
   const uint32_t nc = (uint32_t)plans.size();
   const bool mixed = plans[0].dev.mixed != 0;  // the same for every cloud of a call
   const bool split = (uint64_t)nc * max_nl1 <= kSplitMaxNodes;
@@ -1491,7 +1494,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            split, mixed, hot, st));
+                            split, mixed, hot, dense, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1501,7 +1504,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            split, mixed, hot, st));
+                            split, mixed, hot, dense, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }

@@ -141,10 +141,12 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 // bounds each pick by each leaf's box; split: it takes kUpdateSplit
 // workgroups per level-1 node; mixed: the clouds' leaves are runs of 64 slots
 // that may hold several buckets (never with alias).  hot: the run kernel's
-// hot-set size, 64 or 128 (with alias always 64).
+// hot-set size, 64 or 128 (with alias always 64); dense: with 128, the walk
+// for clouds whose filled buckets hold many points.
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, bool mixed, uint32_t hot, hipStream_t st);
+                         bool leaf_bound, bool split, bool mixed, uint32_t hot, bool dense,
+                         hipStream_t st);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

@@ -936,14 +936,18 @@ constexpr uint32_t kPhaseMin = kHotMax;
 // 71.0 and 73.4 (row by row at 24 rows: 7.94, 4.75, 69.3).
 constexpr uint32_t kWalkRows = 16;
 constexpr uint32_t kWalkLaneEntries = 16;
+constexpr uint32_t kDenseWalkRows = 12;  // 128-copy sets on dense clouds
 static_assert(kWalkRows <= 64, "the walk's row arithmetic");
-// With hot sets of 128 copies a sample has 4 lanes: 16 rows (4 a lane) and
-// 24 entries a lane.  Measured per call (rows / entries): uniform cube 7.21 ms
-// at 16 / 16, 16 / 24 and 16 / 32, 7.26 at 12 / 24, 7.38 at 24 / 16, 8.47 at
-// 8 / 16; clustered cloud 62.1, 61.6, 61.6, 60.5, 63.8 and 60.5 ms.
-template <uint32_t HOT>
+// With hot sets of 128 copies a sample has 4 lanes: ROWS rows (16, or 12 for
+// dense clouds) and 24 entries a lane.  Measured per call (rows / entries):
+// uniform cube 7.21 ms at 16 / 16, 16 / 24 and 16 / 32, 7.26 at 12 / 24,
+// 7.38 at 24 / 16, 8.47 at 8 / 16; clustered cloud 62.1, 61.6, 61.6, 60.5,
+// 63.8 and 60.5 ms.  The rows' gain is the lane's row slots (3 against 4 in
+// the walk's entry-to-row mapping): a limit of 12 rows read at run time, the
+// slots still sized for 16, left the clustered cloud at 61.9 ms.
+template <uint32_t HOT, uint32_t ROWS>
 struct WalkLimits {
-  static constexpr uint32_t kRows = kWalkRows;
+  static constexpr uint32_t kRows = ROWS;
   static constexpr uint32_t kLaneEntries = HOT == 128 ? 24 : kWalkLaneEntries;
   static_assert(kRows <= 64, "the walk's row arithmetic");
 };
@@ -1071,7 +1075,7 @@ __device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, ui
 // bucket has further cells are few and listed apart, and after each walk
 // every one of them is tested against every sample of the hot set; the
 // phases test every cell of a hot copy's bucket.
-template <bool PROF, bool ALIAS, uint32_t HOT>
+template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS>
 __device__ __forceinline__ void run_list(const CloudDev &c) {
   // the alias pass holds one sample per lane
   static_assert(!ALIAS || HOT == 64, "shared buckets take hot sets of 64");
@@ -1747,7 +1751,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         const uint32_t y0 = ((lo_c >> 10) & 1023u) >> gsy, y1 = ((hi_c >> 10) & 1023u) >> gsy;
         const uint32_t z0 = (lo_c >> 20) >> gsz, z1 = (hi_c >> 20) >> gsz;
         const uint32_t ny = y1 - y0 + 1, nrows = ny * (z1 - z0 + 1);
-        bool big = nrows > WalkLimits<HOT>::kRows;
+        bool big = nrows > WalkLimits<HOT, ROWS>::kRows;
         if (!big) {
           // row rr = rz * ny + ry; rz = floor((rr + 0.5) / ny) holds with an
           // approximate reciprocal: rr < 64 leaves a margin of 0.5 / ny
@@ -1779,7 +1783,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             // as one list.  Per call, against row by row (whose last step in
             // each row mostly repeats): uniform cube 2.6 % and LiDAR scan
             // 5.5 % faster, clustered cloud (full rows) 2.5 % slower.
-            constexpr uint32_t kLaneRows = (WalkLimits<HOT>::kRows + kCopyLanes - 1) / kCopyLanes;
+            constexpr uint32_t kLaneRows = (WalkLimits<HOT, ROWS>::kRows + kCopyLanes - 1) / kCopyLanes;
             uint32_t rs[kLaneRows], rn[kLaneRows], ne = 0;
 #pragma unroll
             for (uint32_t t = 0; t < kLaneRows; ++t) {
@@ -1794,7 +1798,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             }
             // more entries than the lane's budget: the sample is flagged (the
             // same samples as a row-by-row test: running totals only grow)
-            if (ne > WalkLimits<HOT>::kLaneEntries) {
+            if (ne > WalkLimits<HOT, ROWS>::kLaneEntries) {
               big = true;
             } else {
               for (uint32_t f = 0; f < ne; f += 4) {
@@ -1986,9 +1990,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
 #undef NSFPS_RMARK
 }
 
-template <bool PROF, bool ALIAS, uint32_t HOT>
+template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  run_list<PROF, ALIAS, HOT>(clouds[blockIdx.x]);
+  run_list<PROF, ALIAS, HOT, ROWS>(clouds[blockIdx.x]);
 }
 
 
@@ -2036,8 +2040,9 @@ __global__ __launch_bounds__(kPassThreads) void k_runs_init(const CloudDev *__re
 hipError_t preload_runs_kernels() {
   constexpr uint32_t S = kUpdateSplit;
   return func_attributes(
-      k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>, k_run<false, false, 64>,
-      k_run<false, false, 128>, k_run<false, true, 64>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
+      k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>,
+      k_run<false, false, 64, kWalkRows>, k_run<false, false, 128, kWalkRows>,
+      k_run<false, false, 128, kDenseWalkRows>, k_run<false, true, 64, kWalkRows>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
       k_update<false, false, true, 1, false>, k_update<false, false, true, S, false>,
       k_update<false, true, false, 1, false>, k_update<false, true, false, S, false>,
       k_update<false, true, true, 1, false>, k_update<false, true, true, S, false>,
@@ -2052,29 +2057,34 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 }
 
 // The classic round's update, gather and run kernels of one variant; hot:
-// the run kernel's hot-set size where cells do not share buckets (64 or 128).
+// the run kernel's hot-set size where cells do not share buckets (64 or 128);
+// dense: 128-copy sets walk at most kDenseWalkRows rows.
 template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT, bool MIXED>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
-                    uint32_t passes, uint32_t hot, hipStream_t st) {
+                    uint32_t passes, uint32_t hot, bool dense, hipStream_t st) {
   k_update<PROF, ALIAS, LB, SPLIT, MIXED>
       <<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
-  if (!ALIAS && hot == 128)
-    k_run<PROF, false, 128><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+  if (!ALIAS && hot == 128 && dense)
+    k_run<PROF, false, 128, kDenseWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+  else if (!ALIAS && hot == 128)
+    k_run<PROF, false, 128, kWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
   else
-    k_run<PROF, ALIAS, 64><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    k_run<PROF, ALIAS, 64, kWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
 }
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
-                         bool leaf_bound, bool split, bool mixed, uint32_t hot, hipStream_t st) {
+                         bool leaf_bound, bool split, bool mixed, uint32_t hot, bool dense,
+                         hipStream_t st) {
   if (alias && mixed) return hipErrorInvalidValue;  // leaves of several buckets: one cell each
   if (hot != 64 && hot != 128) return hipErrorInvalidValue;
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
-  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, uint32_t, hipStream_t);
+  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, uint32_t, bool,
+                          hipStream_t);
   constexpr uint32_t S = kUpdateSplit;
   // [profile][cells: one per leaf, shared buckets, several per leaf][leaf_bound][split]
   static constexpr Launch kClassic[2][3][2][2] = {
@@ -2091,7 +2101,8 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
        {{launch_classic<true, false, false, 1, true>, launch_classic<true, false, false, S, true>},
         {launch_classic<true, false, true, 1, true>, launch_classic<true, false, true, S, true>}}}};
   const Launch classic = kClassic[profile][alias ? 1 : mixed ? 2 : 0][leaf_bound][split];
-  for (uint32_t r = 0; r < rounds; ++r) classic(d_clouds, nclouds, grid, sparse, passes, hot, st);
+  for (uint32_t r = 0; r < rounds; ++r)
+    classic(d_clouds, nclouds, grid, sparse, passes, hot, dense, st);
   return hipGetLastError();
 }
 

@@ -99,6 +99,19 @@ def test_workload_hash_with_either_hot_set(yf, lib, wname, hot, monkeypatch):
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("dense", ["0", "1"])
+@pytest.mark.parametrize("wname", ["uniform_cube", "clustered"])
+def test_workload_hash_with_either_walk(yf, lib, wname, dense, monkeypatch):
+    """128-copy hot sets walk at most 12 coarse rows a sample on dense clouds
+    (more than 64 points a filled bucket) and 16 elsewhere; NSFPS_DENSE_WALK
+    forces either.  Both give the reference's samples."""
+    monkeypatch.setenv("NSFPS_DENSE_WALK", dense)
+    w, g, outs = run_workload(yf, lib, wname)
+    assert yf.last_stats()["hot_set"] == 128
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
 @pytest.mark.parametrize("lb", ["0", "1"])
 @pytest.mark.parametrize("wname", ["uniform_cube", "clustered", "lidar_scan"])
 def test_workload_hash_with_either_update_bound(yf, lib, wname, lb, monkeypatch):
@@ -239,7 +252,7 @@ TREE = {"NSFPS_ENGINE": "tree"}
 @pytest.mark.parametrize("env", [
     {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
     {"NSFPS_GLOBAL_SORT": "1"}, {"NSFPS_HOT": "64"}, {"NSFPS_HOT": "128"},
-    {"NSFPS_LEAF_BOUND": "0"}, {"NSFPS_LEAF_BOUND": "1"},
+    {"NSFPS_LEAF_BOUND": "0"}, {"NSFPS_LEAF_BOUND": "1"}, {"NSFPS_HOT": "128", "NSFPS_DENSE_WALK": "1"},
     {"NSFPS_HOT": "128", "NSFPS_PROFILE": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},
