@@ -42,12 +42,23 @@ SOURCES = ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_group
 # forward an option with an argument to the device pass alone
 # (-Xarch_device refuses it), so that host-pass warning is filtered from the
 # build output and the device assembly is checked instead (check_no_packed_fp32).
+# The backend's atomic optimizer is off: by default it turns an atomic whose
+# address is the same in every lane into a loop over the active lanes (a
+# read-lane and a scalar step each) ahead of one atomic, and in these kernels
+# such atomics have few active lanes on the run kernel's critical path (the
+# largest key left unaccepted, the lowered copies' masks and bounds).  With
+# one LDS atomic per lane instead, per call on one MI355X, bit-exact: 1M-point
+# uniform cube 7.20-7.22 -> 6.99-7.01 ms, quickstart 0.71 -> 0.65-0.66,
+# LiDAR scan 3.91 -> 3.77-3.80, batched clouds 2.05 -> 1.93-1.98, clustered
+# cloud 60.2-60.3 -> 59.5.  Its DPP form (a reduction across lanes in place of
+# the loop) measured in between: uniform cube 7.16-7.23, quickstart 0.67-0.69.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fno-fast-math",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-result",
 ]
 HOST_PASS_WARNING = "'-packed-fp32-ops' is not a recognized feature for this target"
