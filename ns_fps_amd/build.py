@@ -52,6 +52,15 @@ SOURCES = ("nsfps_build.hip", "nsfps_sample.hip", "nsfps_runs.hip", "nsfps_group
 # LiDAR scan 3.91 -> 3.77-3.80, batched clouds 2.05 -> 1.93-1.98, clustered
 # cloud 60.2-60.3 -> 59.5.  Its DPP form (a reduction across lanes in place of
 # the loop) measured in between: uniform cube 7.16-7.23, quickstart 0.67-0.69.
+# The machine scheduler favours instruction-level parallelism (max-ilp): the
+# run kernel is latency-bound with two waves per SIMD.  Per call, two runs on
+# each of two boxes, bit-exact, against the default strategy: uniform cube
+# 7.01-7.02 -> 6.96-7.00 ms, LiDAR scan 3.77-3.79 -> 3.67-3.69, batched
+# clouds 1.99-2.00 -> 1.89-1.94, clustered cloud 59.5-59.8 -> 58.3-58.6,
+# quickstart 0.66-0.68 -> 0.65-0.66.  The others measured: max-memory-clause
+# slower everywhere (uniform cube 7.04-7.05), iterative-ilp and
+# iterative-maxocc in between (uniform cube 6.95-6.97 and 7.00-7.01,
+# clustered 58.7 and 58.9-59.0).
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-fno-fast-math",
@@ -59,6 +68,7 @@ DEVICE_FLAGS = [
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+    "-mllvm", "-amdgpu-sched-strategy=max-ilp",
     "-Wall", "-Wno-unused-result",
 ]
 HOST_PASS_WARNING = "'-packed-fp32-ops' is not a recognized feature for this target"
