@@ -170,15 +170,20 @@ def run_single(lib, hip, w, steps, warmup):
             lib.fps_device(d_xyz, len(P), m, w["range"], d_out)
         hip.synchronize()
         stats, per_call, lens = [], [], []
+        # the range struct built once, and each call's statistics kept as the
+        # C struct: Python conversions stay out of the timed calls
+        from ns_fps_amd.capi import Range
+        rng = Range.of(w["range"])
         t0 = time.perf_counter()
         for k in range(steps):
             tc = time.perf_counter()
-            n = lib.fps_device(d_xyz, len(P), m, w["range"], d_outs[k])  # returns after the stream
+            n = lib.fps_device(d_xyz, len(P), m, rng, d_outs[k])  # returns after the stream
             per_call.append((time.perf_counter() - tc) * 1e3)
-            stats.append(lib.stats())
+            stats.append(lib.stats_raw())
             lens.append(n)
         hip.synchronize()
         t1 = time.perf_counter()
+        stats = [st.as_dict() for st in stats]
         outs = [hip.download(d_outs[k], lens[k], np.int32) for k in range(steps)]
     finally:
         hip.free(d_xyz)
@@ -256,9 +261,10 @@ def run_batched(lib, hip, w, steps, warmup):
             tc = time.perf_counter()
             lens = lib.fps_batched_device(d_xyz, B, n, m, d_outs[k], w["range"], w["blocks"])
             per_call.append((time.perf_counter() - tc) * 1e3)
-            stats.append(lib.stats())
+            stats.append(lib.stats_raw())  # converted after the timed calls
             all_lens.append(lens)
         t1 = time.perf_counter()
+        stats = [st.as_dict() for st in stats]
         outs = [hip.download(d_outs[k], B * m, np.int32).reshape(B, m) for k in range(steps)]
     finally:
         hip.free(d_xyz)

@@ -28,6 +28,8 @@ class Range(ctypes.Structure):
 
     @classmethod
     def of(cls, rng):
+        if isinstance(rng, cls):  # already converted (a caller's loop converts once)
+            return rng
         return cls(*[float(v) for v in rng[:6]], *[int(v) for v in rng[6:9]])
 
 
@@ -216,9 +218,13 @@ class Lib:
                                                      _vp(stream)))
 
     def stats(self):
+        return self.stats_raw().as_dict()
+
+    def stats_raw(self):
+        """The last call's statistics as the C struct (as_dict() converts)."""
         s = Stats()
         self._check(self.lib.nsfps_get_stats(ctypes.byref(s)))
-        return s.as_dict()
+        return s
 
     def loop_profile(self):
         w = (ctypes.c_uint64 * 64)()
