@@ -1441,6 +1441,12 @@ constexpr uint32_t kSplitMaxNodes = 256;
 // quickstart (8) 0.91 against 0.70, 120,000-point scan (1,266) 4.09 against
 // 3.90, 64 clouds of 16,384 points (about 2,530 each) 2.31 against 2.06.
 constexpr uint32_t kHot128MinCells = 6912;
+// Clouds whose points fill at most this many buckets take the run kernel that
+// applies a large-cube sample whose cube holds the list's cell box without a
+// cell test per entry.  The 10,000-point quickstart (8 buckets, every cube of
+// a positive distance holding every point), per call on the MI355X: 0.65-0.66
+// -> 0.62-0.63 ms (large-cube samples 4.5 k -> 3.2 k cycles a hot set).
+constexpr uint32_t kWholeMaxCells = 8;
 
 // The shape of a call's sampling passes: the update pass's workgroups per
 // level-1 node and the run kernel's hot-set size (0 when the tree engine ran).
@@ -1479,6 +1485,12 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   if (hot_env && atoi(hot_env) == 64) wide = false;
   if (hot_env && atoi(hot_env) == 128) wide = !alias;
   const uint32_t hot = wide ? 128u : 64u;
+  // clouds in few buckets: their large cubes hold the whole list (a sample's
+  // cube is checked against the list's cell box in the kernel, so this only
+  // chooses the kernel); NSFPS_WHOLE=0 or 1 forces either
+  bool whole = !alias && hot == 64;
+  for (auto &p : plans) whole = whole && p.occupied <= kWholeMaxCells;
+  if (const char *e = getenv("NSFPS_WHOLE")) whole = atoi(e) != 0 && !alias && hot == 64;
   shape_out->split = split ? kUpdateSplit : 1u;
   shape_out->hot = hot;
   const uint64_t shape[5] = {nc, plans[0].n, plans[0].m, plans[0].rng.dev.T, max_nl1};
@@ -1494,7 +1506,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       const uint32_t take = (uint32_t)std::min<uint64_t>(bp.first, g_schedule.rounds - enqueued);
       if (take == 0) break;
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, take, bp.second, profile, alias, leaf_bound,
-                            split, mixed, hot, dense, st));
+                            split, mixed, hot, dense, whole, st));
       enqueued += take;
       used.emplace_back(take, bp.second);
       passes = bp.second;
@@ -1504,7 +1516,7 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   while (true) {
     if (!launched) {
       HIP_TRY(launch_rounds(d_clouds, nc, max_nl1, batch, passes, profile, alias, leaf_bound,
-                            split, mixed, hot, dense, st));
+                            split, mixed, hot, dense, whole, st));
       enqueued += batch;
       used.emplace_back(batch, passes);
     }

@@ -142,11 +142,13 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 // workgroups per level-1 node; mixed: the clouds' leaves are runs of 64 slots
 // that may hold several buckets (never with alias).  hot: the run kernel's
 // hot-set size, 64 or 128 (with alias always 64); dense: with 128, the walk
-// for clouds whose filled buckets hold many points.
+// for clouds whose filled buckets hold many points; whole: with 64 and no
+// alias, the run kernel that applies a large-cube sample holding the list's
+// cell box with no cell test (for clouds in few buckets).
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
                          bool leaf_bound, bool split, bool mixed, uint32_t hot, bool dense,
-                         hipStream_t st);
+                         bool whole, hipStream_t st);
 
 // grouping after sampling (nsfps_group.hip): out[i] = xyz[idx[i]] (bad gets 1
 // for an index outside [0, n), whose row is zeroed); ball query rows of

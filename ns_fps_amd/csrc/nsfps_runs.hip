@@ -1075,8 +1075,9 @@ __device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, ui
 // bucket has further cells are few and listed apart, and after each walk
 // every one of them is tested against every sample of the hot set; the
 // phases test every cell of a hot copy's bucket.
-template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS>
+template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS, bool WHOLE>
 __device__ __forceinline__ void run_list(const CloudDev &c) {
+  static_assert(!(WHOLE && ALIAS), "the list box is of the entries' own cells");
   // the alias pass holds one sample per lane
   static_assert(!ALIAS || HOT == 64, "shared buckets take hot sets of 64");
   constexpr uint32_t kHot = HOT, kCopyLanes = HotSet<HOT>::kLanes, kCmp = HotSet<HOT>::kCmp,
@@ -1098,6 +1099,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
   __shared__ uint2 s_rc[kHot];          //   cube corners, pack11 (hi with guards)
   __shared__ __align__(16) uint32_t s_cell[kCells + 4];  // first entry of each coarse cell
   __shared__ uint32_t s_big[2 * kWords];                // samples with large cubes
+  __shared__ uint32_t s_bigw[WHOLE ? 2 * kWords : 1];  // WHOLE: those whose cube holds the list box
   __shared__ __align__(16) uint32_t s_sel[3][kSelBins];  // hot-threshold histograms, rotating
   __shared__ uint32_t s_nhot;
   __shared__ unsigned long long s_kmr;   // largest key of a hot copy left unaccepted
@@ -1121,6 +1123,8 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
   __shared__ uint32_t s_alist[ALIAS ? kListCap : 1];
   __shared__ uint32_t s_nal;
   __shared__ uint32_t s_hpos[kHot];
+  // WHOLE: the list's cell box, per axis the largest cell and 1023 - the smallest
+  __shared__ uint32_t s_lb[WHOLE ? 6 : 1];
   __shared__ uint2 s_sbox[ALIAS ? kHot : 1];
   __shared__ float4 s_spos[ALIAS ? kHot : 1];
   const uint64_t rt0 = PROF ? __builtin_amdgcn_s_memrealtime() : 0;
@@ -1180,6 +1184,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
     s_sel[1][tid] = 0;
   }
   if (tid < kHot) s_hq[0][tid] = make_uint4(0u, 0u, 0u, 0u);  // key 0: an unused slot
+  if (WHOLE && tid < 6) s_lb[tid] = 0;
   if (tid == 0) {
     s_nhot = 0;
     if (ALIAS) {
@@ -1319,6 +1324,32 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
     c11[s] = e0.w;
     cc[s] = (e0.w & 1023u) | (((e0.w >> 11) & 1023u) << 10) | ((e0.w >> 22) << 20);
   }
+  if (WHOLE) {  // the list's cell box (every entry's cell lies in it)
+    uint32_t bmax[3] = {0u, 0u, 0u}, bmin[3] = {0u, 0u, 0u};  // bmin: 1023 - the smallest
+#pragma unroll
+    for (uint32_t s = 0; s < kOwnSlots; ++s) {
+      if (s * kRunThreads + tid < nlist) {
+#pragma unroll
+        for (uint32_t a = 0; a < 3; ++a) {
+          const uint32_t v = (cc[s] >> (10 * a)) & 1023u;
+          bmax[a] = max(bmax[a], v);
+          bmin[a] = max(bmin[a], 1023u - v);
+        }
+      }
+    }
+#pragma unroll
+    for (uint32_t a = 0; a < 3; ++a) {
+      bmax[a] = wave_max_u32(bmax[a]);
+      bmin[a] = wave_max_u32(bmin[a]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (uint32_t a = 0; a < 3; ++a) {
+        atomicMax(&s_lb[a], bmax[a]);
+        atomicMax(&s_lb[3 + a], bmin[a]);
+      }
+    }
+  }
   uint32_t it = *gptr(c.iter);
   const uint32_t m = c.m;
   NSFPS_GLOBAL int32_t *const out = gptr(c.out);
@@ -1333,6 +1364,13 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
   uint32_t S = sel_shift(kref, bkey);
   hist_live(d, lo, bkey, kref, S, s_sel[0], err);
   __syncthreads();
+  // WHOLE: the list box's corners in pack11 form (an empty list leaves them
+  // crossed, and no cube then holds them both)
+  uint32_t lb_lo = 0, lb_hi = 0;
+  if (WHOLE) {
+    lb_lo = pack11(pack_cell(1023u - s_lb[3], 1023u - s_lb[4], 1023u - s_lb[5]));
+    lb_hi = pack11(pack_cell(s_lb[0], s_lb[1], s_lb[2]));
+  }
   // coarse grid, kept in vector registers (the scalar file is full in the walk)
   const uint32_t gsh = s_geo[0], gx = s_geo[1], gy = s_geo[2];
   const uint32_t gsx = gsh & 255u, gsy = (gsh >> 8) & 255u, gsz = gsh >> 16;
@@ -1428,6 +1466,7 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
         }
       }
       if (tid < 2 * kWords) s_big[tid] = 0;
+      if (WHOLE && tid < 2 * kWords) s_bigw[WHOLE ? tid : 0] = 0;
       if (tid == 0) {
 #pragma unroll
         for (uint32_t w = 0; w < kWords; ++w) {
@@ -1848,7 +1887,13 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             }
           }
         }
-        if (big) atomicOr(&s_big[hj >> 5], 1u << (hj & 31u));
+        if (big) {
+          // WHOLE: a cube holding the list box holds every entry's cell
+          const bool all = WHOLE && (in_box11(lb_lo | kGuards, lb_lo, lo11, hi11g) &
+                                     in_box11(lb_hi | kGuards, lb_hi, lo11, hi11g)) != 0;
+          if (all) atomicOr(&s_bigw[WHOLE ? hj >> 5 : 0], 1u << (hj & 31u));
+          else atomicOr(&s_big[hj >> 5], 1u << (hj & 31u));
+        }
       }
       NSFPS_RMARK(kRpWalk);
       __syncthreads();  // the walks' updates are in LDS
@@ -1895,11 +1940,14 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
       for (uint32_t s = 0; s < kOwnSlots; ++s)
         if (s * kRunThreads + tid < nlist) d[s] = __uint_as_float(s_dd[s * kRunThreads + tid]);
       NSFPS_RMARK(kRpApply);
-      uint64_t bigm[kWords], bany = 0;
+      uint64_t bigm[kWords], bigw[kWords], bany = 0;
 #pragma unroll
       for (uint32_t w = 0; w < kWords; ++w) {
         bigm[w] = ((uint64_t)uniform(s_big[2 * w + 1]) << 32) | uniform(s_big[2 * w]);
-        bany |= bigm[w];
+        bigw[w] = WHOLE ? ((uint64_t)uniform(s_bigw[WHOLE ? 2 * w + 1 : 0]) << 32) |
+                              uniform(s_bigw[WHOLE ? 2 * w : 0])
+                        : 0ull;
+        bany |= bigm[w] | bigw[w];
       }
       if (bany) {
         // branch-free (the distance is always computed, the box test masks
@@ -1923,9 +1971,29 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
             d[s] = __uint_as_float(min(__float_as_uint(d[s]), __float_as_uint(dd) | (in - 1u)));
           }
         };
+        // WHOLE: a sample whose cube holds the list box holds every entry's
+        // cell, and takes the distances with no cell test
+        const auto take_all = [&](const uint4 a0) {
+#pragma unroll
+          for (uint32_t s = 0; s < kOwnSlots; ++s) {
+            const float dd = sqdist(x[s], y[s], z[s], __uint_as_float(a0.x),
+                                    __uint_as_float(a0.y), __uint_as_float(a0.z));
+            d[s] = __uint_as_float(min(__float_as_uint(d[s]), __float_as_uint(dd)));
+          }
+        };
 #pragma unroll
         for (uint32_t w = 0; w < kWords; ++w) {
-          uint64_t bm = bigm[w];
+          uint64_t bm = bigw[w];
+          while (WHOLE && bm) {
+            const uint32_t ka = 64 * w + (uint32_t)__builtin_ctzll(bm);
+            bm &= bm - 1;
+            const uint32_t kc = bm ? 64 * w + (uint32_t)__builtin_ctzll(bm) : ka;
+            bm &= bm - 1;
+            const uint4 a0 = s_rp[ka], a1 = s_rp[kc];
+            take_all(a0);
+            take_all(a1);
+          }
+          bm = bigm[w];
           while (bm) {
             const uint32_t ka = 64 * w + (uint32_t)__builtin_ctzll(bm);
             bm &= bm - 1;
@@ -1990,9 +2058,9 @@ __device__ __forceinline__ void run_list(const CloudDev &c) {
 #undef NSFPS_RMARK
 }
 
-template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS>
+template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS, bool WHOLE>
 __global__ __launch_bounds__(kRunThreads) void k_run(const CloudDev *__restrict__ clouds) {
-  run_list<PROF, ALIAS, HOT, ROWS>(clouds[blockIdx.x]);
+  run_list<PROF, ALIAS, HOT, ROWS, WHOLE>(clouds[blockIdx.x]);
 }
 
 
@@ -2041,8 +2109,9 @@ hipError_t preload_runs_kernels() {
   constexpr uint32_t S = kUpdateSplit;
   return func_attributes(
       k_runs_init, k_refine, k_gather<false, false>, k_gather<false, true>,
-      k_run<false, false, 64, kWalkRows>, k_run<false, false, 128, kWalkRows>,
-      k_run<false, false, 128, kDenseWalkRows>, k_run<false, true, 64, kWalkRows>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
+      k_run<false, false, 64, kWalkRows, false>, k_run<false, false, 64, kWalkRows, true>,
+      k_run<false, false, 128, kWalkRows, false>, k_run<false, false, 128, kDenseWalkRows, false>,
+      k_run<false, true, 64, kWalkRows, false>, k_update<false, false, false, 1, false>, k_update<false, false, false, S, false>,
       k_update<false, false, true, 1, false>, k_update<false, false, true, S, false>,
       k_update<false, true, false, 1, false>, k_update<false, true, false, S, false>,
       k_update<false, true, true, 1, false>, k_update<false, true, true, S, false>,
@@ -2061,29 +2130,31 @@ hipError_t launch_runs_init(const CloudDev *d_clouds, uint32_t nclouds, bool spl
 // dense: 128-copy sets walk at most kDenseWalkRows rows.
 template <bool PROF, bool ALIAS, bool LB, uint32_t SPLIT, bool MIXED>
 void launch_classic(const CloudDev *d_clouds, uint32_t nclouds, dim3 grid, dim3 sparse,
-                    uint32_t passes, uint32_t hot, bool dense, hipStream_t st) {
+                    uint32_t passes, uint32_t hot, bool dense, bool whole, hipStream_t st) {
   k_update<PROF, ALIAS, LB, SPLIT, MIXED>
       <<<dim3(grid.x * SPLIT, grid.y), kPassThreads, 0, st>>>(d_clouds);
   for (uint32_t p = 1; p <= passes; ++p)
     k_refine<<<sparse, kPassThreads, 0, st>>>(d_clouds, p, passes);
   k_gather<PROF, ALIAS><<<sparse, kPassThreads, 0, st>>>(d_clouds, passes);
   if (!ALIAS && hot == 128 && dense)
-    k_run<PROF, false, 128, kDenseWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    k_run<PROF, false, 128, kDenseWalkRows, false><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
   else if (!ALIAS && hot == 128)
-    k_run<PROF, false, 128, kWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    k_run<PROF, false, 128, kWalkRows, false><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+  else if (!ALIAS && whole)
+    k_run<PROF, false, 64, kWalkRows, true><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
   else
-    k_run<PROF, ALIAS, 64, kWalkRows><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
+    k_run<PROF, ALIAS, 64, kWalkRows, false><<<nclouds, kRunThreads, 0, st>>>(d_clouds);
 }
 
 hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t max_nl1,
                          uint32_t rounds, uint32_t passes, bool profile, bool alias,
                          bool leaf_bound, bool split, bool mixed, uint32_t hot, bool dense,
-                         hipStream_t st) {
+                         bool whole, hipStream_t st) {
   if (alias && mixed) return hipErrorInvalidValue;  // leaves of several buckets: one cell each
   if (hot != 64 && hot != 128) return hipErrorInvalidValue;
   const dim3 grid(max_nl1, nclouds);
   const dim3 sparse(max_nl1 < kSparseGroups ? max_nl1 : kSparseGroups, nclouds);
-  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, uint32_t, bool,
+  using Launch = void (*)(const CloudDev *, uint32_t, dim3, dim3, uint32_t, uint32_t, bool, bool,
                           hipStream_t);
   constexpr uint32_t S = kUpdateSplit;
   // [profile][cells: one per leaf, shared buckets, several per leaf][leaf_bound][split]
@@ -2102,7 +2173,7 @@ hipError_t launch_rounds(const CloudDev *d_clouds, uint32_t nclouds, uint32_t ma
         {launch_classic<true, false, true, 1, true>, launch_classic<true, false, true, S, true>}}}};
   const Launch classic = kClassic[profile][alias ? 1 : mixed ? 2 : 0][leaf_bound][split];
   for (uint32_t r = 0; r < rounds; ++r)
-    classic(d_clouds, nclouds, grid, sparse, passes, hot, dense, st);
+    classic(d_clouds, nclouds, grid, sparse, passes, hot, dense, whole, st);
   return hipGetLastError();
 }
 

@@ -124,6 +124,20 @@ def test_workload_hash_with_either_update_bound(yf, lib, wname, lb, monkeypatch)
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("whole", ["0", "1"])
+@pytest.mark.parametrize("wname", ["quickstart", "lidar_scan", "batched_shapes"])
+def test_workload_hash_with_either_large_cube_form(yf, lib, wname, whole, monkeypatch):
+    """Clouds in few buckets (the quickstart's 8) take the run kernel that
+    applies a large-cube sample whose cube holds the list's cell box with no
+    cell test per entry; NSFPS_WHOLE forces that kernel or the general one.
+    Both give the reference's samples."""
+    monkeypatch.setenv("NSFPS_WHOLE", whole)
+    w, g, outs = run_workload(yf, lib, wname)
+    assert yf.last_stats()["hot_set"] == 64
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
 @pytest.mark.parametrize("wname,hot", [("quickstart", 64), ("lidar_scan", 64), ("batched_shapes", 64),
                                        ("uniform_cube", 128), ("clustered", 128),
                                        ("uniform_cube_30", 64)])
@@ -253,6 +267,7 @@ TREE = {"NSFPS_ENGINE": "tree"}
     {}, {"NSFPS_NO_PADDED": "1"}, {"NSFPS_MIXED": "0"}, {"NSFPS_MIXED": "1"},
     {"NSFPS_GLOBAL_SORT": "1"}, {"NSFPS_HOT": "64"}, {"NSFPS_HOT": "128"},
     {"NSFPS_LEAF_BOUND": "0"}, {"NSFPS_LEAF_BOUND": "1"}, {"NSFPS_HOT": "128", "NSFPS_DENSE_WALK": "1"},
+    {"NSFPS_WHOLE": "0"}, {"NSFPS_WHOLE": "1"}, {"NSFPS_WHOLE": "1", "NSFPS_PROFILE": "1"},
     {"NSFPS_HOT": "128", "NSFPS_PROFILE": "1"}, {**TREE, "NSFPS_WIDE_ITERS": "0"}, {**TREE, "NSFPS_WIDE_ITERS": "1"},
     {**TREE, "NSFPS_WIDE_ITERS": "37"}, {**TREE, "NSFPS_WIDE_ITERS": "100000"},
     {**TREE, "NSFPS_NO_PADDED": "1"}, {**TREE, "NSFPS_PROFILE": "1"},

@@ -201,3 +201,27 @@ def test_gpu_matches_oracle_with_hot_sets_of_128(yf, oracle, sweep, seed, monkey
     want = oracle.fps(p, m, rng, blocks=blocks)
     assert np.array_equal(got, want), (len(got), len(want), f"first difference at "
                                        f"{np.argmax(got[:len(want)] != want[:len(got)])}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sweep,seed", [(1, s) for s in SEEDS] + [(2, s) for s in SEEDS2],
+                         ids=lambda v: str(v))
+def test_gpu_matches_oracle_with_the_list_box_form(yf, oracle, sweep, seed, monkeypatch):
+    """Both sweeps with the run kernel forced to the form that applies a
+    large-cube sample holding the list's cell box with no cell test (taken
+    otherwise only for clouds in few buckets; grids whose cells share buckets
+    and 128-copy hot sets keep the general form)."""
+    from ns_fps_amd.capi import Lib
+    monkeypatch.setenv("NSFPS_WHOLE", "1")
+    if sweep == 1:
+        shape, p, m, rng = make_case(seed)
+        blocks = rng[6:9]
+    else:
+        shape, p, m, rng, blocks = make_case2(seed)
+    if rng is None:
+        got = Lib().fps_bbox(p, m, blocks)
+    else:
+        got = yf.fps(p, m, yf.make_range(*rng))
+    want = oracle.fps(p, m, rng, blocks=blocks)
+    assert np.array_equal(got, want), (len(got), len(want), f"first difference at "
+                                       f"{np.argmax(got[:len(want)] != want[:len(got)])}")
