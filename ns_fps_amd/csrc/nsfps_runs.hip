@@ -1074,7 +1074,10 @@ __device__ __forceinline__ void hist_live(const float *d, const uint32_t *lo, ui
 // 573-597).  The walk finds entries by their own cell; the entries whose
 // bucket has further cells are few and listed apart, and after each walk
 // every one of them is tested against every sample of the hot set; the
-// phases test every cell of a hot copy's bucket.
+// phases test every cell of a hot copy's bucket.  HOT: copies per hot set;
+// ROWS: the walk's row limit.  WHOLE (clouds in few buckets): the list's
+// cell box is taken at its load, and a large-cube sample whose cube holds it
+// is applied to every entry with no cell test.
 template <bool PROF, bool ALIAS, uint32_t HOT, uint32_t ROWS, bool WHOLE>
 __device__ __forceinline__ void run_list(const CloudDev &c) {
   static_assert(!(WHOLE && ALIAS), "the list box is of the entries' own cells");
