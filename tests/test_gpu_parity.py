@@ -124,6 +124,17 @@ def test_workload_hash_with_either_update_bound(yf, lib, wname, lb, monkeypatch)
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
+@pytest.mark.parametrize("streams", ["1", "2"])
+def test_batched_hash_with_one_or_two_streams(yf, lib, streams, monkeypatch):
+    """Calls of many clouds sample them in two halves on two streams (one
+    half's update and gather passes beside the other half's run kernel);
+    NSFPS_STREAMS=1 keeps one stream.  Both give the reference's samples."""
+    monkeypatch.setenv("NSFPS_STREAMS", streams)
+    w, g, outs = run_workload(yf, lib, "batched_shapes")
+    assert [len(o) for o in outs] == g["lengths"]
+    assert [sha256_i32(o) for o in outs] == g["output_sha256"]
+
+
 @pytest.mark.parametrize("whole", ["0", "1"])
 @pytest.mark.parametrize("wname", ["quickstart", "lidar_scan", "batched_shapes"])
 def test_workload_hash_with_either_large_cube_form(yf, lib, wname, whole, monkeypatch):
