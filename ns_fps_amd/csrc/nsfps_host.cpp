@@ -475,14 +475,19 @@ struct PinStage {
   bool pending = false;
 };
 
+// Streams of one call's sampling rounds, at most.  The runtime gives a
+// process 4 hardware queues by default: 4 streams of rounds (with the
+// caller's own) shared them, and 64 clouds of 16,384 points took 3.0 ms per
+// call against 1.8 with 2 or 3.
+constexpr uint32_t kMaxStreams = 3;
 struct Arena {
   char *base = nullptr;
   size_t cap = 0;
   hipStream_t stream = nullptr;
-  // the second half of a call's clouds during the sampling rounds, and the
-  // events that order it after the build and before each status read
-  hipStream_t stream2 = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  // the other groups of a call's clouds during the sampling rounds, and the
+  // events that order them after the build and before each status read
+  hipStream_t stream2[kMaxStreams - 1] = {};
+  hipEvent_t fork = nullptr, join[kMaxStreams - 1] = {};
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   int device = -1;
   PinStage pin;
@@ -1454,9 +1459,11 @@ constexpr uint32_t kWholeMaxCells = 8;
 // Calls of at least this many clouds sample them in two halves on two
 // streams: each round's run kernel takes one CU per cloud, and one half's
 // update and gather passes then run on the other CUs beside the other half's
-// run kernel (clouds are independent).  NSFPS_STREAMS=1 or 2 forces either.
-// 64 clouds of 16,384 points, per call on the MI355X: 1.88-1.94 -> 1.79-1.81 ms.
+// run kernel (clouds are independent).  NSFPS_STREAMS=n asks for n groups
+// (at most kMaxStreams).  64 clouds of 16,384 points, per call on the
+// MI355X: one stream 1.94 ms, two 1.79-1.81, three 1.71-1.80.
 constexpr uint32_t kTwoStreamMinClouds = 8;
+constexpr uint32_t kStreamGroups = 2;
 
 // The shape of a call's sampling passes: the update pass's workgroups per
 // level-1 node and the run kernel's hot-set size (0 when the tree engine ran).
@@ -1509,36 +1516,44 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
   HIP_TRY(launch_runs_init(d_clouds, nc, split, st));
   // two halves on two streams (kTwoStreamMinClouds); not for the
   // allocation-free entry point, which creates nothing
-  bool two = nc >= kTwoStreamMinClouds && !profile && !g_call_no_alloc;
-  if (const char *e = getenv("NSFPS_STREAMS")) two = atoi(e) == 2 && nc >= 2 && !g_call_no_alloc;
-  hipStream_t st2 = nullptr;
+  uint32_t groups = nc >= kTwoStreamMinClouds && !profile && !g_call_no_alloc ? kStreamGroups : 1u;
+  if (const char *e = getenv("NSFPS_STREAMS")) groups = g_call_no_alloc ? 1u : (uint32_t)std::max(1, atoi(e));
+  groups = std::min({groups, nc, kMaxStreams});
+  const bool two = groups > 1;
+  hipStream_t sts[kMaxStreams] = {st};
+  uint32_t g0[kMaxStreams + 1] = {}, gmax[kMaxStreams] = {};
   Arena *ap2 = nullptr;
-  const uint32_t h = nc / 2;
-  uint32_t max_a = 1, max_b = 1;
   if (two) {
     const nsfps_status rc = arena_for_device(&ap2);
     if (rc) return rc;
-    if (!ap2->stream2) {
-      HIP_TRY(hipStreamCreateWithFlags(&ap2->stream2, hipStreamNonBlocking));
-      HIP_TRY(hipEventCreateWithFlags(&ap2->fork, hipEventDisableTiming));
-      HIP_TRY(hipEventCreateWithFlags(&ap2->join, hipEventDisableTiming));
+    if (!ap2->fork) HIP_TRY(hipEventCreateWithFlags(&ap2->fork, hipEventDisableTiming));
+    for (uint32_t k = 1; k < groups; ++k) {
+      if (!ap2->stream2[k - 1]) {
+        HIP_TRY(hipStreamCreateWithFlags(&ap2->stream2[k - 1], hipStreamNonBlocking));
+        HIP_TRY(hipEventCreateWithFlags(&ap2->join[k - 1], hipEventDisableTiming));
+      }
+      sts[k] = ap2->stream2[k - 1];
     }
-    st2 = ap2->stream2;
-    for (uint32_t i = 0; i < nc; ++i)
-      (i < h ? max_a : max_b) = std::max(i < h ? max_a : max_b, plans[i].dev.nl1);
-    // the second stream starts after the build and the run state's set-up
+    // the other streams start after the build and the run state's set-up
     HIP_TRY(hipEventRecord(ap2->fork, st));
-    HIP_TRY(hipStreamWaitEvent(st2, ap2->fork, 0));
+    for (uint32_t k = 1; k < groups; ++k) HIP_TRY(hipStreamWaitEvent(sts[k], ap2->fork, 0));
+  }
+  for (uint32_t k = 0; k <= groups; ++k) g0[k] = (uint32_t)((uint64_t)nc * k / groups);
+  for (uint32_t k = 0; k < groups; ++k) {
+    gmax[k] = 1;
+    for (uint32_t i = g0[k]; i < g0[k + 1]; ++i) gmax[k] = std::max(gmax[k], plans[i].dev.nl1);
   }
   const auto enqueue = [&](uint32_t take, uint32_t np) -> hipError_t {
     if (!two)
       return launch_rounds(d_clouds, nc, max_nl1, take, np, profile, alias, leaf_bound, split,
                            mixed, hot, dense, whole, st);
-    const hipError_t e = launch_rounds(d_clouds, h, max_a, take, np, profile, alias, leaf_bound,
-                                       split, mixed, hot, dense, whole, st);
-    if (e != hipSuccess) return e;
-    return launch_rounds(d_clouds + h, nc - h, max_b, take, np, profile, alias, leaf_bound, split,
-                         mixed, hot, dense, whole, st2);
+    for (uint32_t k = 0; k < groups; ++k) {
+      const hipError_t e = launch_rounds(d_clouds + g0[k], g0[k + 1] - g0[k], gmax[k], take, np,
+                                         profile, alias, leaf_bound, split, mixed, hot, dense,
+                                         whole, sts[k]);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
   };
   std::vector<CloudStatus> pr(nc);
   uint64_t last_samples = 0, enqueued = 0;
@@ -1562,9 +1577,9 @@ nsfps_status run_rounds(std::vector<CloudPlan> &plans, const CloudDev *d_clouds,
       used.emplace_back(batch, passes);
     }
     launched = false;
-    if (two) {  // the statuses are read on st once the second half's rounds are done
-      HIP_TRY(hipEventRecord(ap2->join, st2));
-      HIP_TRY(hipStreamWaitEvent(st, ap2->join, 0));
+    for (uint32_t k = 1; k < groups; ++k) {  // the statuses are read on st once every group's rounds are done
+      HIP_TRY(hipEventRecord(ap2->join[k - 1], sts[k]));
+      HIP_TRY(hipStreamWaitEvent(st, ap2->join[k - 1], 0));
     }
     if (ev_end) HIP_TRY(hipEventRecord(ev_end, st));
     {
@@ -1802,8 +1817,9 @@ nsfps_status run_clouds(std::vector<CloudPlan> &plans, Ws ws, bool out_on_host, 
     (void)hipStreamSynchronize(ws.st);
     // a failed call may leave rounds of its second half queued
     int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 16 && g_arena[dev].stream2)
-      (void)hipStreamSynchronize(g_arena[dev].stream2);
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 16)
+      for (hipStream_t s2 : g_arena[dev].stream2)
+        if (s2) (void)hipStreamSynchronize(s2);
   }
   return rc;
 }

@@ -124,11 +124,12 @@ def test_workload_hash_with_either_update_bound(yf, lib, wname, lb, monkeypatch)
     assert [sha256_i32(o) for o in outs] == g["output_sha256"]
 
 
-@pytest.mark.parametrize("streams", ["1", "2"])
-def test_batched_hash_with_one_or_two_streams(yf, lib, streams, monkeypatch):
-    """Calls of many clouds sample them in two halves on two streams (one
-    half's update and gather passes beside the other half's run kernel);
-    NSFPS_STREAMS=1 keeps one stream.  Both give the reference's samples."""
+@pytest.mark.parametrize("streams", ["1", "2", "3"])
+def test_batched_hash_with_one_to_three_streams(yf, lib, streams, monkeypatch):
+    """Calls of many clouds sample them in groups on their own streams (one
+    group's update and gather passes beside another's run kernel; two groups
+    by default); NSFPS_STREAMS sets the number.  All give the reference's
+    samples."""
     monkeypatch.setenv("NSFPS_STREAMS", streams)
     w, g, outs = run_workload(yf, lib, "batched_shapes")
     assert [len(o) for o in outs] == g["lengths"]
